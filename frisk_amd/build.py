@@ -1,0 +1,64 @@
+"""Ahead-of-time build of libfrisk_hip.so (the C-ABI of include/frisk_hip.h).
+
+Every .hip file under csrc/ is compiled for gfx950 with hipcc and linked into
+one shared library placed next to this file, so it travels with the source
+tree.  Invoked by __graft_entry__.build() and by `python -m frisk_amd.build`.
+"""
+from __future__ import annotations
+
+import os
+import shlex
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+CSRC = HERE / "csrc"
+LIB = HERE / "libfrisk_hip.so"
+ARCH = "gfx950"
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+COMMON = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    # Packed-fp32 VALU forms are kept out of generated code on this platform.
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wno-unused-command-line-argument",
+]
+
+
+def sources() -> list[Path]:
+    return sorted(CSRC.glob("*.hip"))
+
+
+def build(verbose: bool = False, extra: list[str] | None = None) -> Path:
+    objdir = HERE / "_build"
+    objdir.mkdir(exist_ok=True)
+    flags = COMMON + (extra or [])
+
+    def compile_one(src: Path) -> Path:
+        obj = objdir / (src.stem + ".o")
+        cmd = [HIPCC, *flags, "-c", str(src), "-o", str(obj)]
+        if verbose:
+            print(" ".join(shlex.quote(c) for c in cmd), flush=True)
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"hipcc failed on {src.name}:\n{r.stdout}\n{r.stderr}")
+        return obj
+
+    with ThreadPoolExecutor(max_workers=min(8, os.cpu_count() or 1)) as ex:
+        objs = list(ex.map(compile_one, sources()))
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

@@ -1,0 +1,514 @@
+// MFMA GEMM kernels for gfx950 (MI355X).
+//
+// Semantics follow frisk.gemm (include/Dialect/Frisk/IR/FriskOps.td:252-292):
+// C = op(A).op(B) when clear_accum, else C += op(A).op(B).  The reference
+// lowers one 64xN tile of that op to SM90 wgmma text
+// (benchmark/layout/execution/backend.py:383-431); here the whole problem is
+// tiled for CDNA4:
+//
+//  * 256x256 output tile per 256-thread workgroup (4 waves, 2x2), each wave
+//    owning a 128x128 sub-tile as 4x4 v_mfma 32x32 accumulators in AGPRs.
+//  * K is consumed in stages of 128 bytes per row (64 bf16/f16, 128 fp8/i8):
+//    the A and B stage tiles are 256 rows x 128 B = 32 KiB each, loaded with
+//    one dwordx4 per lane per row chunk (8 lanes cover one 128 B row
+//    segment, fully coalesced) into registers, then written to LDS.
+//  * Two LDS stages (128 KiB of the 160 KiB per CU): the global loads of
+//    stage s+1 are in flight while the MFMAs of stage s run; one barrier per
+//    stage.
+//  * LDS rows are 128 B = 8 chunks of 16 B; chunk c of row r is stored at
+//    chunk c ^ swz(r).  The fragment read of a 32x32 MFMA has 32 lanes read
+//    the same logical chunk of 32 consecutive rows; the XOR spreads those
+//    rows over distinct bank groups.  swz is an F2-linear map of the row
+//    bits (a GF(2) layout in the sense of the reference's bit-linear
+//    shared layouts, SM90GemmConstraints.cpp:106-150).
+//  * The epilogue stages each 32x128 f32 slice of a wave through LDS so the
+//    global stores are row-contiguous 16 B per lane.
+//
+// Operand contract of the fast kernel: A is [M, K] and B is [N, K] (both
+// K-contiguous, i.e. trans_a == 0, trans_b == 1), K*esize % 16 == 0, 16 B
+// aligned rows; the generic kernel covers every other layout and type.
+
+#include "common.h"
+#include "kernels.h"
+
+namespace frisk {
+
+// ---------------------------------------------------------------------------
+// MFMA wrappers.  kBytes = bytes of one operand row consumed by one 32x32
+// MFMA; every lane supplies kBytes/2 of them (lanes 0-31 and 32-63 split the
+// row), as i32x4 chunks.  A and B fragments use the same (lane, byte) -> k
+// assignment, so the k order inside an instruction never matters.
+// ---------------------------------------------------------------------------
+template <Elt E> struct Mfma32;
+
+template <> struct Mfma32<Elt::BF16> {
+  static constexpr int kBytes = 32;
+  using Acc = f32x16;
+  __device__ static inline Acc run(const i32x4* a, const i32x4* b, Acc c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a[0]),
+                                                   __builtin_bit_cast(bf16x8, b[0]), c, 0, 0, 0);
+  }
+};
+
+template <> struct Mfma32<Elt::F16> {
+  static constexpr int kBytes = 32;
+  using Acc = f32x16;
+  __device__ static inline Acc run(const i32x4* a, const i32x4* b, Acc c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a[0]),
+                                                  __builtin_bit_cast(f16x8, b[0]), c, 0, 0, 0);
+  }
+};
+
+template <> struct Mfma32<Elt::E4M3> {
+  static constexpr int kBytes = 64;
+  using Acc = f32x16;
+  __device__ static inline Acc run(const i32x4* a, const i32x4* b, Acc c) {
+    const i32x8 av = {a[0][0], a[0][1], a[0][2], a[0][3], a[1][0], a[1][1], a[1][2], a[1][3]};
+    const i32x8 bv = {b[0][0], b[0][1], b[0][2], b[0][3], b[1][0], b[1][1], b[1][2], b[1][3]};
+    // Format 0 = fp8 e4m3 for both operands; E8M0 block scales 127 = 2^0.
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, bv, c, 0, 0, 0, 127, 0, 127);
+  }
+};
+
+template <> struct Mfma32<Elt::I8> {
+  static constexpr int kBytes = 32;
+  using Acc = i32x16;
+  __device__ static inline Acc run(const i32x4* a, const i32x4* b, Acc c) {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a[0], b[0], c, 0, 0, 0);
+  }
+};
+
+// ---------------------------------------------------------------------------
+// Tiling.  Each stage holds 64 bytes of K per row (32 bf16/f16, 64 fp8/i8)
+// for the 256 A rows and 256 B rows: 2 x 16 KiB.  kStages stages rotate
+// through LDS; a stage is filled by LDS-DMA (buffer_load_dwordx4 ... lds),
+// so no VGPRs stage the data and the loads of kStages-2 stages are in
+// flight while one stage is multiplied.
+//
+// LDS row = 4 chunks of 16 B.  Chunk c of row r is stored at physical chunk
+// c ^ swz(r), swz(r) = ((r >> 1) ^ (r >> 3)) & 3.  A 32x32 MFMA fragment
+// read has lanes 0-31 read one logical chunk of 32 consecutive rows; with
+// 128 B bank lines (32 banks) the 8 rows of a lane octet land on (r & 1,
+// swz) = 8 distinct 16 B bank groups, and with 256 B lines (64 banks) the
+// 16 rows of a lane group land on (r & 3, swz) = 16 distinct groups.  swz is
+// linear over GF(2) in the row bits, i.e. a bit-linear shared layout.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int swz(int row) { return ((row >> 1) ^ (row >> 3)) & 3; }
+
+constexpr int kBM = 256, kBN = 256, kRow = 64;
+constexpr int kTileBytes = kBM * kRow;    // 16 KiB per operand per stage
+constexpr int kStageBytes = 2 * kTileBytes;
+#ifndef FRISK_GEMM_STAGES
+#define FRISK_GEMM_STAGES 4
+#endif
+constexpr int kStages = FRISK_GEMM_STAGES;
+constexpr int kLdsBytes = kStages * kStageBytes;
+static_assert(kLdsBytes <= 160 * 1024, "LDS budget of one CU");
+
+// s_waitcnt with only the vector-memory counter limited to n (gfx9 encoding:
+// vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]).
+#define FRISK_WAIT_VMCNT(n) \
+  __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+template <Elt OUT, typename AccS>
+__device__ inline void store8(void* c, int64_t idx, const AccS* v, bool accumulate, float scale) {
+  if constexpr (OUT == Elt::I32) {
+    int32_t* p = (int32_t*)c + idx;
+    i32x4 lo = {(int)v[0], (int)v[1], (int)v[2], (int)v[3]};
+    i32x4 hi = {(int)v[4], (int)v[5], (int)v[6], (int)v[7]};
+    if (accumulate) {
+      lo += *(const i32x4*)p;
+      hi += *(const i32x4*)(p + 4);
+    }
+    *(i32x4*)p = lo;
+    *(i32x4*)(p + 4) = hi;
+  } else if constexpr (OUT == Elt::F32) {
+    float* p = (float*)c + idx;
+    f32x4 lo = {v[0] * scale, v[1] * scale, v[2] * scale, v[3] * scale};
+    f32x4 hi = {v[4] * scale, v[5] * scale, v[6] * scale, v[7] * scale};
+    if (accumulate) {
+      lo += *(const f32x4*)p;
+      hi += *(const f32x4*)(p + 4);
+    }
+    *(f32x4*)p = lo;
+    *(f32x4*)(p + 4) = hi;
+  } else {
+    uint16_t* p = (uint16_t*)c + idx;
+    float f[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[i] = v[i] * scale;
+    if (accumulate) {
+      const i32x4 old = *(const i32x4*)p;
+      const uint16_t* o = (const uint16_t*)&old;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if constexpr (OUT == Elt::BF16) f[i] += bf16_bits_to_f32(o[i]);
+        else f[i] += (float)__builtin_bit_cast(_Float16, o[i]);
+      }
+    }
+    uint16_t r[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if constexpr (OUT == Elt::BF16) r[i] = f32_to_bf16_bits(f[i]);
+      else r[i] = __builtin_bit_cast(uint16_t, (_Float16)f[i]);
+    }
+    *(i32x4*)p = *(const i32x4*)r;
+  }
+}
+
+// MFMA operand fragments of one k-step: TM A tiles and TN B tiles.
+template <int TM, int TN, int LC>
+struct Frags {
+  i32x4 a[TM][LC];
+  i32x4 b[TN][LC];
+};
+
+// WM x WN waves tile the 256x256 output; each wave owns a
+// (256/WM) x (256/WN) sub-tile as TM x TN 32x32 accumulators.
+template <Elt IN, Elt OUT, int WM, int WN>
+__global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_tn(const char* __restrict__ A,
+                                                             const char* __restrict__ B,
+                                                             void* __restrict__ C, int M, int N,
+                                                             int Kb, int64_t lda_b, int64_t ldb_b,
+                                                             int64_t ldc, float scale,
+                                                             int accumulate) {
+  // The body is device code only; the host pass just needs the kernel stub.
+#if defined(__HIP_DEVICE_COMPILE__)
+  using Op = Mfma32<IN>;
+  using Acc = typename Op::Acc;
+  using AccS = typename std::conditional<IN == Elt::I8, int32_t, float>::type;
+  constexpr int kWaves = WM * WN;
+  constexpr int TM = kBM / WM / 32, TN = kBN / WN / 32;
+  constexpr int kStepChunks = Op::kBytes / 16;  // 16 B chunks per row per MFMA
+  constexpr int kLaneChunks = kStepChunks / 2;  // chunks per lane per MFMA
+  constexpr int kSteps = kRow / Op::kBytes;     // MFMA k-steps per stage (2 or 1)
+  constexpr int kBlocks = kTileBytes / 1024 / kWaves;  // 1 KiB DMA blocks per wave per operand
+  constexpr int kLoads = 2 * kBlocks;                  // DMA loads per lane per stage
+  constexpr int kFragReads = (TM + TN) * kLaneChunks;  // ds_read_b128 per lane per k-step
+
+  extern __shared__ __attribute__((aligned(1024))) char smem[];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+  const int l32 = lane & 31, half = lane >> 5;
+
+  const int tiles_m = (M + kBM - 1) / kBM, tiles_n = (N + kBN - 1) / kBN;
+  int tm, tn;
+  tile_of_block<4>(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
+  const int row0 = tm * kBM, col0 = tn * kBN;
+
+  // ---- LDS-DMA mapping ----------------------------------------------------
+  // DMA instruction i of wave w writes the 1 KiB block of rows
+  // (kBlocks w + i) * 16 .. +16 of a tile; lane L lands at row +L/4,
+  // physical chunk L%4, so it fetches logical chunk (L%4) ^ swz(row) of that
+  // row.  Loads are raw buffer loads based at the tile's first row: an
+  // offset past num_records returns zeros, which zero-fills the K tail
+  // without branches.
+  const char* a_base = A + (int64_t)row0 * lda_b;
+  const char* b_base = B + (int64_t)col0 * ldb_b;
+  const int64_t a_left = (int64_t)(M - 1 - row0) * lda_b + Kb;
+  const int64_t b_left = (int64_t)(N - 1 - col0) * ldb_b + Kb;
+  const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)a_base, (short)0, (int)min(a_left, (int64_t)0x7fffffff), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rsb = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)b_base, (short)0, (int)min(b_left, (int64_t)0x7fffffff), 0x00020000);
+  uint32_t a_off[kBlocks], b_off[kBlocks];
+  int kmax[kBlocks];
+#pragma unroll
+  for (int i = 0; i < kBlocks; ++i) {
+    const int r = (kBlocks * wave + i) * 16 + (lane >> 2);
+    const int c = (lane & 3) ^ swz(r);
+    // Rows past the matrix edge are clamped: they only feed output rows or
+    // columns that are never stored.
+    a_off[i] = (uint32_t)(min(r, M - 1 - row0) * lda_b) + c * 16;
+    b_off[i] = (uint32_t)(min(r, N - 1 - col0) * ldb_b) + c * 16;
+    kmax[i] = Kb - c * 16;  // the chunk is live while kb < kmax
+  }
+  auto issue_stage = [&](int stage, int slot) {
+    const int kb = stage * kRow;
+    char* dst = smem + slot * kStageBytes + wave * kBlocks * 1024;
+#pragma unroll
+    for (int i = 0; i < kBlocks; ++i) {
+      const bool live = kb < kmax[i];
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (lds_ptr_t)(dst + i * 1024), 16,
+                                               live ? a_off[i] + kb : 0x80000000u, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsb, (lds_ptr_t)(dst + kTileBytes + i * 1024), 16,
+                                               live ? b_off[i] + kb : 0x80000000u, 0, 0, 0);
+    }
+  };
+
+  // ---- fragment reads -----------------------------------------------------
+  int fa_off[TM], fb_off[TN], fa_sw[TM], fb_sw[TN];
+#pragma unroll
+  for (int t = 0; t < TM; ++t) {
+    const int r = wm * (32 * TM) + t * 32 + l32;
+    fa_off[t] = r * kRow;
+    fa_sw[t] = swz(r);
+  }
+#pragma unroll
+  for (int t = 0; t < TN; ++t) {
+    const int r = wn * (32 * TN) + t * 32 + l32;
+    fb_off[t] = kTileBytes + r * kRow;
+    fb_sw[t] = swz(r);
+  }
+  using Frag = Frags<TM, TN, kLaneChunks>;
+  auto load_frags = [&](int slot, int s, Frag& f) {
+    const char* base = smem + slot * kStageBytes;
+#pragma unroll
+    for (int j = 0; j < kLaneChunks; ++j) {
+      const int chunk = s * kStepChunks + half * kLaneChunks + j;
+#pragma unroll
+      for (int t = 0; t < TM; ++t)
+        f.a[t][j] = *(const i32x4*)(base + fa_off[t] + ((chunk ^ fa_sw[t]) << 4));
+#pragma unroll
+      for (int t = 0; t < TN; ++t)
+        f.b[t][j] = *(const i32x4*)(base + fb_off[t] + ((chunk ^ fb_sw[t]) << 4));
+    }
+  };
+
+  Acc acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = Acc{};
+  auto mfma_rows = [&](const Frag& f, int i0, int i1) {
+#pragma unroll
+    for (int i = i0; i < i1; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) acc[i][j] = Op::run(f.a[i], f.b[j], acc[i][j]);
+  };
+
+  // ---- pipeline -----------------------------------------------------------
+  // Stage kt lives in slot kt % kStages.  Before the second half of the last
+  // k-step of stage kt a barrier (after waiting for this lane's loads of
+  // stage kt+1) makes stage kt+1 readable and proves every wave is done
+  // with slot (kt-1) % kStages, which then receives stage kt+kStages-1.
+  // Every iteration issues exactly kLoads loads (stages past the end reload
+  // the last stage into a slot nobody reads), so vmcnt bookkeeping is static.
+  const int nk = (Kb + kRow - 1) / kRow;
+#pragma unroll
+  for (int st = 0; st < kStages - 1; ++st) issue_stage(min(st, nk - 1), st);
+  FRISK_WAIT_VMCNT(kLoads * (kStages - 2));
+  __builtin_amdgcn_s_barrier();
+
+  Frag fr[2];
+  load_frags(0, 0, fr[0]);
+  int slot = 0;
+  for (int kt = 0; kt < nk; ++kt) {
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) {
+      const int cur = s & 1, nxt = cur ^ 1;
+      if (s + 1 < kSteps) {
+        load_frags(slot, s + 1, fr[nxt]);
+        mfma_rows(fr[cur], 0, TM);
+        // Fragment reads first, each under one MFMA.
+#pragma unroll
+        for (int i = 0; i < kFragReads; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      } else {
+        mfma_rows(fr[cur], 0, TM / 2);
+        __builtin_amdgcn_sched_barrier(0);
+        FRISK_WAIT_VMCNT(kLoads * (kStages - 3));
+        __builtin_amdgcn_s_barrier();
+        const int nslot = slot + 1 == kStages ? 0 : slot + 1;
+        const int fslot = slot == 0 ? kStages - 1 : slot - 1;
+        issue_stage(min(kt + kStages - 1, nk - 1), fslot);
+        load_frags(nslot, 0, fr[kSteps & 1 ? nxt : 0]);
+        mfma_rows(fr[cur], TM / 2, TM);
+        // DMA issue and next-stage fragment reads interleaved with the
+        // remaining MFMAs.
+#pragma unroll
+        for (int i = 0; i < kLoads; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM (LDS-DMA)
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        slot = nslot;
+      }
+    }
+    if constexpr (kSteps == 1) fr[0] = fr[1];
+  }
+  // Drain the trailing DMA loads before the stage buffers are reused.
+  FRISK_WAIT_VMCNT(0);
+  __syncthreads();
+
+  // Epilogue: per wave, stage a 32 x (32 TN) slice (one accumulator row
+  // block) as 32-bit values, then each lane stores 8 consecutive columns.
+  // The MFMA 32x32 accumulator holds D[8*(r/4) + 4*(lane/32) + r%4][lane%32]
+  // in element r.
+  constexpr int kPitch = 32 * TN + 4;
+  static_assert(kWaves * 32 * kPitch * 4 <= kLdsBytes, "epilogue staging fits in the stage buffers");
+  AccS* stage = (AccS*)(smem + wave * (32 * kPitch * 4));
+  constexpr int kGroups = 32 * TN / 8;  // 8-column groups per staged row
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int rr = 8 * (r >> 2) + 4 * half + (r & 3);
+        stage[rr * kPitch + j * 32 + l32] = acc[i][j][r];
+      }
+    __syncthreads();
+#pragma unroll
+    for (int it = 0; it < 32 * kGroups / 64; ++it) {
+      const int q = it * 64 + lane;
+      const int rr = q / kGroups, g = q % kGroups;
+      const int gr = row0 + wm * (32 * TM) + i * 32 + rr;
+      const int gc = col0 + wn * (32 * TN) + g * 8;
+      if (gr < M && gc < N) {
+        AccS v[8];
+        *(i32x4*)&v[0] = *(const i32x4*)&stage[rr * kPitch + g * 8];
+        *(i32x4*)&v[4] = *(const i32x4*)&stage[rr * kPitch + g * 8 + 4];
+        store8<OUT>(C, (int64_t)gr * ldc + gc, v, accumulate != 0, scale);
+      }
+    }
+    __syncthreads();
+  }
+#endif  // __HIP_DEVICE_COMPILE__
+}
+
+// ---------------------------------------------------------------------------
+// Generic kernel: any layout, any supported type, any shape.  64x64 output
+// tile per 256 threads (4x4 per thread), K in steps of 16 through LDS with
+// operands converted to the accumulator type on load.
+// ---------------------------------------------------------------------------
+template <Elt IN, Elt OUT>
+__global__ __launch_bounds__(256) void gemm_generic(const void* __restrict__ A,
+                                                    const void* __restrict__ B,
+                                                    void* __restrict__ C, int M, int N, int K,
+                                                    int64_t lda, int64_t ldb, int64_t ldc,
+                                                    int trans_a, int trans_b, float scale,
+                                                    int accumulate) {
+  using Acc = typename std::conditional<IN == Elt::I8, int32_t, float>::type;
+  __shared__ Acc as[16][65];
+  __shared__ Acc bs[16][65];
+  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+  const int row0 = blockIdx.y * 64, col0 = blockIdx.x * 64;
+  Acc acc[4][4] = {};
+  for (int k0 = 0; k0 < K; k0 += 16) {
+    for (int e = threadIdx.x; e < 64 * 16; e += 256) {
+      const int kk = e & 15, rr = e >> 4;
+      const int gm = row0 + rr, gn = col0 + rr, gk = k0 + kk;
+      Acc va = 0, vb = 0;
+      if (gm < M && gk < K) {
+        const int64_t ia = trans_a ? (int64_t)gk * lda + gm : (int64_t)gm * lda + gk;
+        if constexpr (IN == Elt::I8) va = ((const int8_t*)A)[ia];
+        else va = load_as_f32<IN>(A, ia);
+      }
+      if (gn < N && gk < K) {
+        const int64_t ib = trans_b ? (int64_t)gn * ldb + gk : (int64_t)gk * ldb + gn;
+        if constexpr (IN == Elt::I8) vb = ((const int8_t*)B)[ib];
+        else vb = load_as_f32<IN>(B, ib);
+      }
+      as[kk][rr] = va;
+      bs[kk][rr] = vb;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < 16; ++kk) {
+      Acc a[4], b[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[i] = as[kk][ty + 16 * i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) b[j] = bs[kk][tx + 16 * j];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] += a[i] * b[j];
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int gm = row0 + ty + 16 * i, gn = col0 + tx + 16 * j;
+      if (gm >= M || gn >= N) continue;
+      const int64_t ic = (int64_t)gm * ldc + gn;
+      if constexpr (OUT == Elt::I32) {
+        int32_t* p = (int32_t*)C + ic;
+        *p = accumulate ? *p + acc[i][j] : acc[i][j];
+      } else {
+        float v = (float)acc[i][j] * scale;
+        if (accumulate) v += load_as_f32<OUT>(C, ic);
+        store_from_f32<OUT>(C, ic, v);
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Launchers.
+// ---------------------------------------------------------------------------
+#ifndef FRISK_GEMM_WM
+#define FRISK_GEMM_WM 2
+#endif
+#ifndef FRISK_GEMM_WN
+#define FRISK_GEMM_WN 4
+#endif
+
+template <Elt IN, Elt OUT>
+static hipError_t launch_tn(const GemmArgs& g, hipStream_t stream) {
+  constexpr int kEsz = EltInfo<IN>::bytes;
+  constexpr int WM = FRISK_GEMM_WM, WN = FRISK_GEMM_WN;
+  auto kern = gemm_mfma_tn<IN, OUT, WM, WN>;
+  // Thread-safe one-time opt-in to more than 64 KiB of dynamic LDS.
+  static const hipError_t attr = hipFuncSetAttribute(
+      (const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+  if (attr != hipSuccess) return attr;
+  const int tiles = (int)(((g.m + kBM - 1) / kBM) * ((g.n + kBN - 1) / kBN));
+  hipLaunchKernelGGL(kern, dim3(tiles), dim3(64 * WM * WN), kLdsBytes, stream, (const char*)g.a,
+                     (const char*)g.b, g.c, (int)g.m, (int)g.n, (int)(g.k * kEsz),
+                     g.lda * kEsz, g.ldb * kEsz, g.ldc, g.scale, g.accumulate);
+  return hipGetLastError();
+}
+
+template <Elt IN, Elt OUT>
+static hipError_t launch_generic(const GemmArgs& g, hipStream_t stream) {
+  dim3 grid((unsigned)((g.n + 63) / 64), (unsigned)((g.m + 63) / 64));
+  hipLaunchKernelGGL((gemm_generic<IN, OUT>), grid, dim3(256), 0, stream, g.a, g.b, g.c,
+                     (int)g.m, (int)g.n, (int)g.k, g.lda, g.ldb, g.ldc, g.trans_a, g.trans_b,
+                     g.scale, g.accumulate);
+  return hipGetLastError();
+}
+
+#define FRISK_PAIR(i, o) (((int)(i) << 8) | (int)(o))
+
+hipError_t gemm_tn_mfma(const GemmArgs& g, hipStream_t s) {
+  switch (FRISK_PAIR(g.in, g.out)) {
+    case FRISK_PAIR(Elt::BF16, Elt::BF16): return launch_tn<Elt::BF16, Elt::BF16>(g, s);
+    case FRISK_PAIR(Elt::BF16, Elt::F32): return launch_tn<Elt::BF16, Elt::F32>(g, s);
+    case FRISK_PAIR(Elt::F16, Elt::F16): return launch_tn<Elt::F16, Elt::F16>(g, s);
+    case FRISK_PAIR(Elt::F16, Elt::F32): return launch_tn<Elt::F16, Elt::F32>(g, s);
+    case FRISK_PAIR(Elt::E4M3, Elt::BF16): return launch_tn<Elt::E4M3, Elt::BF16>(g, s);
+    case FRISK_PAIR(Elt::E4M3, Elt::F16): return launch_tn<Elt::E4M3, Elt::F16>(g, s);
+    case FRISK_PAIR(Elt::E4M3, Elt::F32): return launch_tn<Elt::E4M3, Elt::F32>(g, s);
+    case FRISK_PAIR(Elt::I8, Elt::I32): return launch_tn<Elt::I8, Elt::I32>(g, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t gemm_generic_any(const GemmArgs& g, hipStream_t s) {
+  switch (FRISK_PAIR(g.in, g.out)) {
+    case FRISK_PAIR(Elt::F32, Elt::F32): return launch_generic<Elt::F32, Elt::F32>(g, s);
+    case FRISK_PAIR(Elt::BF16, Elt::BF16): return launch_generic<Elt::BF16, Elt::BF16>(g, s);
+    case FRISK_PAIR(Elt::BF16, Elt::F32): return launch_generic<Elt::BF16, Elt::F32>(g, s);
+    case FRISK_PAIR(Elt::F16, Elt::F16): return launch_generic<Elt::F16, Elt::F16>(g, s);
+    case FRISK_PAIR(Elt::F16, Elt::F32): return launch_generic<Elt::F16, Elt::F32>(g, s);
+    case FRISK_PAIR(Elt::E4M3, Elt::BF16): return launch_generic<Elt::E4M3, Elt::BF16>(g, s);
+    case FRISK_PAIR(Elt::E4M3, Elt::F16): return launch_generic<Elt::E4M3, Elt::F16>(g, s);
+    case FRISK_PAIR(Elt::E4M3, Elt::F32): return launch_generic<Elt::E4M3, Elt::F32>(g, s);
+    case FRISK_PAIR(Elt::I8, Elt::I32): return launch_generic<Elt::I8, Elt::I32>(g, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace frisk

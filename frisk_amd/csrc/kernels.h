@@ -1,0 +1,52 @@
+// Host-side launcher interface between the C-ABI layer and the kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "common.h"
+
+
+namespace frisk {
+
+// A validated GEMM request (sizes in elements).
+struct GemmArgs {
+  Elt in, out;
+  int64_t m, n, k;
+  int trans_a, trans_b;
+  const void* a;
+  int64_t lda;
+  const void* b;
+  int64_t ldb;
+  void* c;
+  int64_t ldc;
+  float scale;  // scale_a * scale_b
+  int accumulate;
+};
+
+// 256x256-tile MFMA kernel; requires trans_a == 0, trans_b == 1 and 16 B
+// aligned, K-contiguous rows (checked by the caller).
+hipError_t gemm_tn_mfma(const GemmArgs& g, hipStream_t s);
+// Any layout / shape; LDS-tiled FMA kernel.
+hipError_t gemm_generic_any(const GemmArgs& g, hipStream_t s);
+
+// A validated attention request.
+struct AttnArgs {
+  Elt dtype;
+  int64_t batch, heads, seq_q, seq_k, head_dim;
+  int causal;
+  float sm_scale;
+  const void* q;
+  int64_t q_sb, q_sh, q_ss;
+  const void* k;
+  int64_t k_sb, k_sh, k_ss;
+  const void* v;
+  int64_t v_sb, v_sh, v_ss;
+  void* o;
+  int64_t o_sb, o_sh, o_ss;
+  float* lse;
+};
+
+hipError_t attn_fwd_d128(const AttnArgs& a, hipStream_t s);
+
+}  // namespace frisk

@@ -1,0 +1,177 @@
+"""ctypes binding of libfrisk_hip.so (include/frisk_hip.h).
+
+This is the Python side of the C-ABI: it fills the descriptors from torch
+device tensors and calls frisk_gemm / frisk_attn_fwd on the current HIP
+stream.  There is no fallback: if the library is missing or a call fails,
+a RuntimeError (or ValueError for rejected requests, matching the
+reference's ValueError on contract violations, ffi/ir.cpp:333-341) is raised.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libfrisk_hip.so"
+
+F32, F16, BF16, E4M3, I8, I32, F64 = 0, 1, 2, 3, 4, 5, 6
+OK, EINVAL, EUNSUP, EHIP = 0, -1, -2, -3
+
+DTYPE_NAMES = {F32: "f32", F16: "f16", BF16: "bf16", E4M3: "e4m3", I8: "i8", I32: "i32", F64: "f64"}
+
+# Exported symbols declared by include/frisk_hip.h.
+EXPORTS = ("frisk_gemm", "frisk_attn_fwd", "frisk_last_error", "frisk_abi_version")
+ABI_VERSION = 1
+
+
+class GemmDesc(ctypes.Structure):
+    _fields_ = [
+        ("m", ctypes.c_int64), ("n", ctypes.c_int64), ("k", ctypes.c_int64),
+        ("trans_a", ctypes.c_int32), ("trans_b", ctypes.c_int32),
+        ("a_type", ctypes.c_int32), ("b_type", ctypes.c_int32), ("c_type", ctypes.c_int32),
+        ("clear_accum", ctypes.c_int32),
+        ("a", ctypes.c_void_p), ("lda", ctypes.c_int64),
+        ("b", ctypes.c_void_p), ("ldb", ctypes.c_int64),
+        ("c", ctypes.c_void_p), ("ldc", ctypes.c_int64),
+        ("scale_a", ctypes.c_float), ("scale_b", ctypes.c_float),
+    ]
+
+
+class AttnDesc(ctypes.Structure):
+    _fields_ = [
+        ("batch", ctypes.c_int64), ("heads", ctypes.c_int64), ("seq_q", ctypes.c_int64),
+        ("seq_k", ctypes.c_int64), ("head_dim", ctypes.c_int64),
+        ("dtype", ctypes.c_int32), ("causal", ctypes.c_int32), ("sm_scale", ctypes.c_float),
+        ("q", ctypes.c_void_p), ("q_stride_b", ctypes.c_int64), ("q_stride_h", ctypes.c_int64),
+        ("q_stride_s", ctypes.c_int64),
+        ("k", ctypes.c_void_p), ("k_stride_b", ctypes.c_int64), ("k_stride_h", ctypes.c_int64),
+        ("k_stride_s", ctypes.c_int64),
+        ("v", ctypes.c_void_p), ("v_stride_b", ctypes.c_int64), ("v_stride_h", ctypes.c_int64),
+        ("v_stride_s", ctypes.c_int64),
+        ("o", ctypes.c_void_p), ("o_stride_b", ctypes.c_int64), ("o_stride_h", ctypes.c_int64),
+        ("o_stride_s", ctypes.c_int64),
+        ("lse", ctypes.c_void_p),
+    ]
+
+
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """Load libfrisk_hip.so once; raise if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise RuntimeError(
+            f"{LIB_PATH} is missing: build it with `python -m frisk_amd.build` "
+            "(there is no CPU fallback for the GEMM/attention path)")
+    lib = ctypes.CDLL(str(LIB_PATH))
+    lib.frisk_gemm.argtypes = [ctypes.POINTER(GemmDesc), ctypes.c_void_p]
+    lib.frisk_gemm.restype = ctypes.c_int
+    lib.frisk_attn_fwd.argtypes = [ctypes.POINTER(AttnDesc), ctypes.c_void_p]
+    lib.frisk_attn_fwd.restype = ctypes.c_int
+    lib.frisk_last_error.argtypes = []
+    lib.frisk_last_error.restype = ctypes.c_char_p
+    lib.frisk_abi_version.argtypes = []
+    lib.frisk_abi_version.restype = ctypes.c_int
+    if lib.frisk_abi_version() != ABI_VERSION:
+        raise RuntimeError("libfrisk_hip.so ABI version mismatch; rebuild it")
+    _lib = lib
+    return lib
+
+
+def _check(rc: int, what: str) -> None:
+    if rc == OK:
+        return
+    msg = load().frisk_last_error().decode()
+    if rc in (EINVAL, EUNSUP):
+        raise ValueError(f"{what}: {msg}")
+    raise RuntimeError(f"{what}: {msg}")
+
+
+def torch_dtype_code(dt) -> int:
+    import torch
+    table = {
+        torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16,
+        torch.float8_e4m3fn: E4M3, torch.int8: I8, torch.int32: I32, torch.float64: F64,
+    }
+    if dt not in table:
+        raise ValueError(f"unsupported tensor dtype {dt}")
+    return table[dt]
+
+
+def _stream_handle(stream) -> int:
+    import torch
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return int(stream.cuda_stream) if hasattr(stream, "cuda_stream") else int(stream)
+
+
+def _row_major(t, name: str) -> int:
+    if t.dim() != 2 or t.stride(1) != 1:
+        raise ValueError(f"{name} must be a rank-2 tensor with unit column stride")
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a device tensor")
+    return t.stride(0)
+
+
+def gemm_desc(a, b, c, *, trans_a=False, trans_b=False, clear_accum=True,
+              scale_a=1.0, scale_b=1.0) -> GemmDesc:
+    """Describe C (+)= op(A).op(B) for row-major device tensors (see frisk_hip.h)."""
+    lda, ldb, ldc = _row_major(a, "A"), _row_major(b, "B"), _row_major(c, "C")
+    m = a.shape[1] if trans_a else a.shape[0]
+    k = a.shape[0] if trans_a else a.shape[1]
+    kb = b.shape[1] if trans_b else b.shape[0]
+    n = b.shape[0] if trans_b else b.shape[1]
+    if kb != k or tuple(c.shape) != (m, n):
+        raise ValueError(f"legacy-gemm-shape: effective shapes A{tuple(a.shape)} B{tuple(b.shape)} "
+                         f"C{tuple(c.shape)} do not form an MxK . KxN -> MxN product")
+    return GemmDesc(m, n, k, int(bool(trans_a)), int(bool(trans_b)),
+                    torch_dtype_code(a.dtype), torch_dtype_code(b.dtype), torch_dtype_code(c.dtype),
+                    int(bool(clear_accum)), a.data_ptr(), lda, b.data_ptr(), ldb,
+                    c.data_ptr(), ldc, float(scale_a), float(scale_b))
+
+
+def gemm(a, b, c, *, trans_a=False, trans_b=False, clear_accum=True,
+         scale_a=1.0, scale_b=1.0, stream=None):
+    """C = op(A).op(B) (or C += ... with clear_accum=False) on the GPU."""
+    d = gemm_desc(a, b, c, trans_a=trans_a, trans_b=trans_b, clear_accum=clear_accum,
+                  scale_a=scale_a, scale_b=scale_b)
+    _check(load().frisk_gemm(ctypes.byref(d), ctypes.c_void_p(_stream_handle(stream))),
+           "frisk_gemm")
+    return c
+
+
+def attn_desc(q, k, v, o, *, causal=False, sm_scale=None, lse=None) -> AttnDesc:
+    for name, t in (("Q", q), ("K", k), ("V", v), ("O", o)):
+        if t.dim() != 4 or t.stride(3) != 1 or not t.is_cuda:
+            raise ValueError(f"{name} must be a [batch, heads, seq, head_dim] device tensor "
+                             "with unit head_dim stride")
+    b, h, sq, d = q.shape
+    sk = k.shape[2]
+    if tuple(k.shape) != (b, h, sk, d) or tuple(v.shape) != (b, h, sk, d) \
+            or tuple(o.shape) != (b, h, sq, d):
+        raise ValueError("attention shapes disagree")
+    if not (q.dtype == k.dtype == v.dtype == o.dtype):
+        raise ValueError("Q/K/V/O must share one dtype")
+    if lse is not None and (tuple(lse.shape) != (b, h, sq) or not lse.is_contiguous()
+                            or lse.dtype.is_floating_point is False or lse.element_size() != 4):
+        raise ValueError("lse must be a contiguous f32 [batch, heads, seq_q] tensor")
+    if sm_scale is None:
+        sm_scale = d ** -0.5
+    return AttnDesc(b, h, sq, sk, d, torch_dtype_code(q.dtype), int(bool(causal)),
+                    float(sm_scale),
+                    q.data_ptr(), q.stride(0), q.stride(1), q.stride(2),
+                    k.data_ptr(), k.stride(0), k.stride(1), k.stride(2),
+                    v.data_ptr(), v.stride(0), v.stride(1), v.stride(2),
+                    o.data_ptr(), o.stride(0), o.stride(1), o.stride(2),
+                    lse.data_ptr() if lse is not None else None)
+
+
+def attn_fwd(q, k, v, o, *, causal=False, sm_scale=None, lse=None, stream=None):
+    """O = softmax(sm_scale . Q K^T [causal mask]) V on the GPU."""
+    d = attn_desc(q, k, v, o, causal=causal, sm_scale=sm_scale, lse=lse)
+    _check(load().frisk_attn_fwd(ctypes.byref(d), ctypes.c_void_p(_stream_handle(stream))),
+           "frisk_attn_fwd")
+    return o
