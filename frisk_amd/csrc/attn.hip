@@ -1,6 +1,399 @@
-// Flash-attention forward (placeholder until the MFMA kernel lands).
+// Flash-attention forward for gfx950 (MI355X), head_dim 128, bf16 / f16.
+//
+// Semantics: the attention tile program of the reference
+// (tmp/ir.mlir:89-157: S = Q.K^T per K tile, running row max, exp2 of the
+// scaled scores, running row sum, acc_o rescale, acc_o += P.V, final
+// division) and the softmax of benchmark/layout/execution/
+// tail_attention_reference.py:81-114; the reference executes it only as a
+// three-pass D64 kernel (tiled_attention.py:210-728).  Here it is one pass
+// with an online softmax.
+//
+// Layout choices (all per 64-lane wave, MFMA v_mfma_f32_32x32x16):
+//  * S^T = K.Q^T, not S = Q.K^T: the 32x32 accumulator keeps one column per
+//    lane, so lane l owns query l%32 and holds 16 of its key scores per
+//    32-key tile.  Row max / row sum of a query are in-lane reductions plus
+//    one exchange with lane l^32.
+//  * The S^T accumulator element r of lane (l32, h) is key 8(r/4)+4h+r%4.
+//    Converted to bf16 it is used unchanged as the B operand (P^T) of
+//    O^T = V^T.P^T: MFMA k-slot (h, e) then means key
+//    16ks + (e < 4 ? 4h+e : 8+4h+e-4).  V is stored transposed in LDS (V^T,
+//    one 128 B row per head-dim index) with keys permuted inside every group
+//    of 16 the same way, so a lane's 8 keys are one 16 B chunk.
+//  * O^T accumulators also keep query = lane%32, so the softmax rescale is a
+//    per-lane scalar.  Rescaling is lazy: the running max only moves when a
+//    block's max exceeds it by more than 2^8 in the exp2 domain, keeping
+//    every p <= 256 (exact in the final O / l, representable in bf16/f16).
+//  * K tiles (64 keys x 256 B) arrive by LDS-DMA with a 16-chunk XOR
+//    swizzle; V tiles go through registers, are transposed 4x8 in
+//    registers and written as 8 B pieces of V^T (8-chunk XOR swizzle).
+//  * Both tiles are double-buffered: the loads of key block j+1 are in
+//    flight during the MFMAs and softmax of block j.
+
+#include "common.h"
 #include "kernels.h"
 
 namespace frisk {
-hipError_t attn_fwd_d128(const AttnArgs&, hipStream_t) { return hipErrorNotSupported; }
+
+namespace {
+
+constexpr int kD = 128;       // head dim
+constexpr int kBN = 64;       // keys per block
+constexpr int kKTile = kBN * kD * 2;  // 16 KiB
+constexpr int kVTile = kBN * kD * 2;  // 16 KiB (as V^T)
+constexpr int kBuf = kKTile + kVTile;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kRescaleSlack = 8.0f;  // log2 headroom before the running max moves
+
+#define FRISK_WAIT_VMCNT0() __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8))
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+template <Elt T> struct AttnMfma;
+template <> struct AttnMfma<Elt::BF16> {
+  __device__ static inline f32x16 run(i32x4 a, i32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  __device__ static inline uint32_t pack(float lo, float hi) {
+    typedef __bf16 v2 __attribute__((ext_vector_type(2)));
+    v2 v = {(__bf16)lo, (__bf16)hi};
+    return __builtin_bit_cast(uint32_t, v);
+  }
+};
+template <> struct AttnMfma<Elt::F16> {
+  __device__ static inline f32x16 run(i32x4 a, i32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  __device__ static inline uint32_t pack(float lo, float hi) {
+    typedef _Float16 v2 __attribute__((ext_vector_type(2)));
+    v2 v = {(_Float16)lo, (_Float16)hi};
+    return __builtin_bit_cast(uint32_t, v);
+  }
+};
+
+__device__ __forceinline__ float pair_reduce(float x, bool max_op) {
+  // Combines lane l with lane l^32 (ds_bpermute).  The v_permlane32_swap
+  // builtin of this toolchain returns the vdst register for both of its
+  // results, so it is not used.
+  const float y = __shfl_xor(x, 32);
+  return max_op ? fmaxf(x, y) : x + y;
+}
+
+}  // namespace
+
+// QT query tiles of 32 per wave, NW waves per workgroup:
+// BM = 32 * QT * NW queries per workgroup.
+template <Elt T, int QT, int NW, bool CAUSAL>
+__global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(
+    const char* __restrict__ Q, const char* __restrict__ K, const char* __restrict__ V,
+    char* __restrict__ O, float* __restrict__ LSE, int heads, int seq_q, int seq_k,
+    int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t k_sb, int64_t k_sh, int64_t k_ss,
+    int64_t v_sb, int64_t v_sh, int64_t v_ss, int64_t o_sb, int64_t o_sh, int64_t o_ss,
+    float scale_log2, int q_blocks) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  using Mf = AttnMfma<T>;
+  constexpr int kThreads = 64 * NW;
+  constexpr int BM = 32 * QT * NW;
+  extern __shared__ __attribute__((aligned(1024))) char smem[];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31, half = lane >> 5;
+
+  // Block -> (batch*head, query block).  All query blocks of one head are
+  // kept on one XCD (block ids congruent mod 8) so its K/V stay in one L2;
+  // under a causal mask the heaviest (last) query blocks start first.
+  int bh, qb;
+  {
+    const int pid = blockIdx.x;
+    const int nbh = gridDim.x / q_blocks;
+    if (nbh % 8 == 0) {
+      const int xcd = pid & 7, idx = pid >> 3;
+      bh = (idx / q_blocks) * 8 + xcd;
+      qb = idx % q_blocks;
+    } else {
+      bh = pid / q_blocks;
+      qb = pid % q_blocks;
+    }
+    if (CAUSAL) qb = q_blocks - 1 - qb;
+  }
+  const int b = bh / heads, h = bh % heads;
+  const int q0 = qb * BM;
+  const int diag = seq_k - seq_q;  // key j is visible to query i iff j <= i + diag
+  int kv_len = seq_k;
+  if (CAUSAL) kv_len = min(seq_k, q0 + BM + diag);
+  const int nkb = kv_len > 0 ? (kv_len + kBN - 1) / kBN : 0;
+
+  const char* qh = Q + (b * q_sb + h * q_sh) * 2;
+  const char* kh = K + (b * k_sb + h * k_sh) * 2;
+  const char* vh = V + (b * v_sb + h * v_sh) * 2;
+
+  // ---- Q fragments (B operand of S^T = K.Q^T), loaded once -------------
+  const int wq0 = q0 + wave * 32 * QT;  // first query of this wave
+  i32x4 qf[QT][8];
+#pragma unroll
+  for (int t = 0; t < QT; ++t) {
+    const int qi = min(wq0 + t * 32 + l32, seq_q - 1);
+    const char* row = qh + (int64_t)qi * q_ss * 2 + half * 16;
+#pragma unroll
+    for (int ds = 0; ds < 8; ++ds) qf[t][ds] = *(const i32x4*)(row + ds * 32);
+  }
+
+  // ---- K tile by LDS-DMA ------------------------------------------------
+  // One DMA instruction writes 1 KiB = 4 key rows of 256 B; lane L lands in
+  // row L/16, physical chunk L%16 and fetches logical chunk (L%16)^(row&15).
+  // Rows past seq_k read zeros (buffer range check).
+  const __amdgpu_buffer_rsrc_t rsk = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)kh, (short)0, (int)min((int64_t)(seq_k - 1) * k_ss * 2 + kD * 2, (int64_t)0x7fffffff),
+      0x00020000);
+  const __amdgpu_buffer_rsrc_t rsv = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)vh, (short)0, (int)min((int64_t)(seq_k - 1) * v_ss * 2 + kD * 2, (int64_t)0x7fffffff),
+      0x00020000);
+  constexpr int kKInst = 16 / NW;  // DMA instructions per wave per K tile
+  uint32_t k_off[kKInst];
+#pragma unroll
+  for (int i = 0; i < kKInst; ++i) {
+    const int r = (wave * kKInst + i) * 4 + (lane >> 4);
+    const int c = (lane & 15) ^ (r & 15);
+    k_off[i] = (uint32_t)(r * k_ss * 2) + c * 16;
+  }
+  auto issue_k = [&](int kb, int buf) {
+    char* dst = smem + buf * kBuf + wave * kKInst * 1024;
+    const uint32_t base = (uint32_t)((int64_t)kb * kBN * k_ss * 2);
+#pragma unroll
+    for (int i = 0; i < kKInst; ++i) {
+      const int r = kb * kBN + (wave * kKInst + i) * 4 + (lane >> 4);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsk, (lds_ptr_t)(dst + i * 1024), 16,
+                                               r < seq_k ? base + k_off[i] : 0x80000000u, 0, 0,
+                                               0);
+    }
+  };
+
+  // ---- V tile through registers, transposed -----------------------------
+  // Unit u = (g, hh, sub, dc): keys 16g + 8sub + 4hh + 0..3, head dims
+  // 8dc..8dc+7.  Its 4 key rows x 8 dims become 8 V^T pieces of 4 keys
+  // (8 B), stored in V^T row d, logical chunk 2g+hh, byte 8*sub.
+  static_assert(kThreads <= 256 && 256 % kThreads == 0, "V transpose units per thread");
+  constexpr int kVUnits = 256 / kThreads;  // units per thread
+  i32x4 vr[kVUnits][4];
+  auto load_v = [&](int kb) {
+#pragma unroll
+    for (int u = 0; u < kVUnits; ++u) {
+      const int unit = tid + u * kThreads;
+      const int dc = unit & 15, sub = (unit >> 4) & 1, hh = (unit >> 5) & 1, g = unit >> 6;
+      const int key0 = kb * kBN + 16 * g + 8 * sub + 4 * hh;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int key = key0 + i;
+        vr[u][i] = __builtin_amdgcn_raw_buffer_load_b128(
+            rsv, key < seq_k ? (uint32_t)((int64_t)key * v_ss * 2) + dc * 16 : 0x80000000u, 0, 0);
+      }
+    }
+  };
+  auto store_vt = [&](int buf) {
+    char* vt = smem + buf * kBuf + kKTile;
+#pragma unroll
+    for (int u = 0; u < kVUnits; ++u) {
+      const int unit = tid + u * kThreads;
+      const int dc = unit & 15, sub = (unit >> 4) & 1, hh = (unit >> 5) & 1, g = unit >> 6;
+      const uint32_t* w0 = (const uint32_t*)&vr[u][0];
+      const uint32_t* w1 = (const uint32_t*)&vr[u][1];
+      const uint32_t* w2 = (const uint32_t*)&vr[u][2];
+      const uint32_t* w3 = (const uint32_t*)&vr[u][3];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        // dims 8dc+2j (low halves) and 8dc+2j+1 (high halves) of keys 0..3
+        const uint32_t lo01 = (w0[j] & 0xffffu) | (w1[j] << 16);
+        const uint32_t lo23 = (w2[j] & 0xffffu) | (w3[j] << 16);
+        const uint32_t hi01 = (w0[j] >> 16) | (w1[j] & 0xffff0000u);
+        const uint32_t hi23 = (w2[j] >> 16) | (w3[j] & 0xffff0000u);
+        const int d0 = 8 * dc + 2 * j, d1 = d0 + 1;
+        const int c = 2 * g + hh;
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        *(u32x2*)(vt + d0 * 128 + ((c ^ (d0 & 7)) << 4) + 8 * sub) = u32x2{lo01, lo23};
+        *(u32x2*)(vt + d1 * 128 + ((c ^ (d1 & 7)) << 4) + 8 * sub) = u32x2{hi01, hi23};
+      }
+    }
+  };
+
+  // ---- state ---------------------------------------------------------------
+  f32x16 o[QT][4];
+  float m[QT], l[QT];
+#pragma unroll
+  for (int t = 0; t < QT; ++t) {
+    m[t] = -__builtin_inff();
+    l[t] = 0.0f;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) o[t][dt] = f32x16{};
+  }
+
+  if (nkb > 0) {
+    issue_k(0, 0);
+    load_v(0);
+    FRISK_WAIT_VMCNT0();
+    store_vt(0);
+    __syncthreads();
+  }
+
+  for (int j = 0; j < nkb; ++j) {
+    const int buf = j & 1;
+    const bool more = j + 1 < nkb;
+    if (more) {
+      issue_k(j + 1, buf ^ 1);
+      load_v(j + 1);
+    }
+    const char* ks = smem + buf * kBuf;
+    const char* vt = ks + kKTile;
+
+    // S^T = K . Q^T: two 32-key tiles x QT query tiles, 8 head-dim steps.
+    f32x16 s[QT][2];
+#pragma unroll
+    for (int t = 0; t < QT; ++t) s[t][0] = s[t][1] = f32x16{};
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      const int r = kt * 32 + l32;
+#pragma unroll
+      for (int ds = 0; ds < 8; ++ds) {
+        const i32x4 kf = *(const i32x4*)(ks + r * 256 + (((2 * ds + half) ^ (r & 15)) << 4));
+#pragma unroll
+        for (int t = 0; t < QT; ++t) s[t][kt] = Mf::run(kf, qf[t][ds], s[t][kt]);
+      }
+    }
+
+    // Online softmax in the exp2 domain.
+    const int kbase = j * kBN;
+    const bool tail = kbase + kBN > seq_k;
+#pragma unroll
+    for (int t = 0; t < QT; ++t) {
+      const int qi = wq0 + t * 32 + l32;
+      const bool diag_blk = CAUSAL && (kbase + kBN - 1 > wq0 + t * 32 + diag);
+      float mb = -__builtin_inff();
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          float x = s[t][kt][r] * scale_log2;
+          if (tail || diag_blk) {
+            const int key = kbase + kt * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+            if (key >= seq_k || (CAUSAL && key > qi + diag)) x = -__builtin_inff();
+          }
+          s[t][kt][r] = x;
+          mb = fmaxf(mb, x);
+        }
+      mb = pair_reduce(mb, true);
+      const bool move = mb > m[t] + kRescaleSlack;
+      if (__builtin_amdgcn_ballot_w64(move)) {
+        const float mn = move ? mb : m[t];
+        // exp2(-inf) = 0 on a row's first visible block; rows that do not
+        // move keep alpha = 1 (m - mn would be NaN for m = mn = -inf).
+        const float alpha = move ? __builtin_amdgcn_exp2f(m[t] - mn) : 1.0f;
+        m[t] = mn;
+        l[t] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) o[t][dt] *= alpha;
+      }
+      // A row with every key masked so far keeps m = -inf; use 0 as the
+      // subtrahend so its (all -inf) scores give p = 0 instead of NaN.
+      const float msub = m[t] == -__builtin_inff() ? 0.0f : m[t];
+      float rs = 0.0f;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float p = __builtin_amdgcn_exp2f(s[t][kt][r] - msub);
+          s[t][kt][r] = p;
+          rs += p;
+        }
+      l[t] += rs;
+    }
+
+    // O^T += V^T . P^T over 4 key steps of 16.
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      i32x4 pf[QT];
+#pragma unroll
+      for (int t = 0; t < QT; ++t) {
+        const int kt = kk >> 1, r0 = 8 * (kk & 1);
+        pf[t] = i32x4{(int)Mf::pack(s[t][kt][r0 + 0], s[t][kt][r0 + 1]),
+                      (int)Mf::pack(s[t][kt][r0 + 2], s[t][kt][r0 + 3]),
+                      (int)Mf::pack(s[t][kt][r0 + 4], s[t][kt][r0 + 5]),
+                      (int)Mf::pack(s[t][kt][r0 + 6], s[t][kt][r0 + 7])};
+      }
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        const int d = dt * 32 + l32;
+        const i32x4 vf = *(const i32x4*)(vt + d * 128 + (((2 * kk + half) ^ (d & 7)) << 4));
+#pragma unroll
+        for (int t = 0; t < QT; ++t) o[t][dt] = Mf::run(vf, pf[t], o[t][dt]);
+      }
+    }
+
+    if (more) {
+      FRISK_WAIT_VMCNT0();
+      store_vt(buf ^ 1);
+    }
+    __syncthreads();
+  }
+
+  // ---- epilogue: O = O^T / l, LSE -----------------------------------------
+  char* oh = O + (b * o_sb + h * o_sh) * 2;
+#pragma unroll
+  for (int t = 0; t < QT; ++t) {
+    const float lt = pair_reduce(l[t], false);  // both lane halves of the row
+    const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+    const int qi = wq0 + t * 32 + l32;
+    if (qi < seq_q) {
+      char* row = oh + (int64_t)qi * o_ss * 2;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int d = dt * 32 + 8 * g + 4 * half;
+          typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+          const u32x2 w = {Mf::pack(o[t][dt][4 * g + 0] * inv, o[t][dt][4 * g + 1] * inv),
+                           Mf::pack(o[t][dt][4 * g + 2] * inv, o[t][dt][4 * g + 3] * inv)};
+          *(u32x2*)(row + d * 2) = w;
+        }
+      if (LSE && half == 0)
+        LSE[(int64_t)bh * seq_q + qi] = lt > 0.0f ? (m[t] + __log2f(lt)) * kLn2 : -__builtin_inff();
+    }
+  }
+#endif  // __HIP_DEVICE_COMPILE__
+}
+
+#ifndef FRISK_ATTN_QT
+#define FRISK_ATTN_QT 1
+#endif
+#ifndef FRISK_ATTN_NW
+#define FRISK_ATTN_NW 4
+#endif
+
+template <Elt T, bool CAUSAL>
+static hipError_t launch_attn(const AttnArgs& a, hipStream_t stream) {
+  constexpr int QT = FRISK_ATTN_QT, NW = FRISK_ATTN_NW, BM = 32 * QT * NW;
+  auto kern = attn_fwd_kernel<T, QT, NW, CAUSAL>;
+  constexpr int lds = 2 * kBuf;
+  static const hipError_t attr =
+      hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+  if (attr != hipSuccess) return attr;
+  const int q_blocks = (int)((a.seq_q + BM - 1) / BM);
+  const int64_t blocks = (int64_t)q_blocks * a.batch * a.heads;
+  const float scale_log2 = a.sm_scale * kLog2e;
+  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(64 * NW), lds, stream, (const char*)a.q,
+                     (const char*)a.k, (const char*)a.v, (char*)a.o, a.lse, (int)a.heads,
+                     (int)a.seq_q, (int)a.seq_k, a.q_sb, a.q_sh, a.q_ss, a.k_sb, a.k_sh, a.k_ss,
+                     a.v_sb, a.v_sh, a.v_ss, a.o_sb, a.o_sh, a.o_ss, scale_log2, q_blocks);
+  return hipGetLastError();
+}
+
+hipError_t attn_fwd_d128(const AttnArgs& a, hipStream_t s) {
+  if (a.dtype == Elt::BF16)
+    return a.causal ? launch_attn<Elt::BF16, true>(a, s) : launch_attn<Elt::BF16, false>(a, s);
+  if (a.dtype == Elt::F16)
+    return a.causal ? launch_attn<Elt::F16, true>(a, s) : launch_attn<Elt::F16, false>(a, s);
+  return hipErrorInvalidValue;
+}
+
 }  // namespace frisk
