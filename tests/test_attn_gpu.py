@@ -1,0 +1,149 @@
+"""Flash-attention forward parity on the GPU through the C-ABI
+(frisk_attn_fwd) against the fp64 oracle, plus the reference's exact
+fixtures carried over to head_dim 128.  Tolerance:
+max|err| <= 1e-2 * ||ref row||_inf for bf16/f16 outputs; LSE within 1e-3."""
+import numpy as np
+import pytest
+import torch
+
+from frisk_amd import runtime as rt
+from oracle import attention as A
+from oracle import gemm as G
+from tests.gpu_util import Guarded, gen
+
+pytestmark = pytest.mark.gpu
+
+D = 128
+SCALE = D ** -0.5
+
+
+def qkv(b, h, sq, sk, dt, seed):
+    g = gen(seed)
+    q = torch.randn(b, h, sq, D, generator=g, device="cuda").to(dt)
+    k = torch.randn(b, h, sk, D, generator=g, device="cuda").to(dt)
+    v = torch.randn(b, h, sk, D, generator=g, device="cuda").to(dt)
+    return q, k, v
+
+
+def run(q, k, v, causal, with_lse=True):
+    o = torch.empty_like(q)
+    lse = torch.empty(q.shape[:3], device="cuda") if with_lse else None
+    rt.attn_fwd(q, k, v, o, causal=causal, sm_scale=SCALE, lse=lse)
+    torch.cuda.synchronize()
+    return o, lse
+
+
+CASES = [(1, 1, 64, 64), (1, 2, 128, 128), (2, 2, 200, 333), (1, 2, 300, 300), (1, 1, 100, 260),
+         (2, 4, 512, 512), (1, 2, 1, 70), (1, 1, 65, 64), (1, 2, 1024, 1024)]
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
+@pytest.mark.parametrize("b,h,sq,sk", CASES)
+def test_parity_small(b, h, sq, sk, causal, dt):
+    print(f"case attn b{b} h{h} sq{sq} sk{sk} causal={causal} {dt}", flush=True)
+    q, k, v = qkv(b, h, sq, sk, dt, seed=sq * 7 + sk)
+    o, lse = run(q, k, v, causal)
+    ref, rlse = A.attention_fp64(q.double().cpu().numpy(), k.double().cpu().numpy(),
+                                 v.double().cpu().numpy(), causal=causal, scale=SCALE)
+    got = o.double().cpu().numpy()
+    live = np.isfinite(rlse)
+    assert G.row_scaled_error(got[live], ref[live]) <= 1e-2
+    assert np.all(got[~live] == 0)
+    l = lse.cpu().numpy()
+    assert np.abs(l[live] - rlse[live]).max() <= 1e-3
+    assert np.all(np.isneginf(l[~live]))
+
+
+@pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
+def test_config_c5_full_size_sampled_heads(native_oracle, causal):
+    # b4 h32 s4096 d128 bf16, scale 1/sqrt(128); every head is
+    # computed on the GPU, two heads are checked against the fp64 C oracle.
+    b, h, s = 4, 32, 4096
+    q, k, v = qkv(b, h, s, s, torch.bfloat16, seed=5)
+    o, lse = run(q, k, v, causal)
+    for bi, hi in ((0, 0), (3, 31)):
+        ro, rl = native_oracle.attn_f64(q[bi, hi].double().cpu().numpy(),
+                                        k[bi, hi].double().cpu().numpy(),
+                                        v[bi, hi].double().cpu().numpy(), causal=causal,
+                                        scale=SCALE)
+        assert G.row_scaled_error(o[bi, hi].double().cpu().numpy(), ro) <= 1e-2
+        assert np.abs(lse[bi, hi].cpu().numpy() - rl).max() <= 1e-3
+    assert torch.isfinite(o.float()).all()
+
+
+def fixture(n, name, dt=torch.bfloat16):
+    q, k, v = A.fixture_inputs((1, 2, n, D), name, dtype=np.float32)
+    to = lambda x: torch.from_numpy(x).to(dt).cuda()
+    return to(q), to(k), to(v)
+
+
+@pytest.mark.parametrize("n", [64, 128, 256, 1024])
+def test_uniform_sparse_value_exact(n):
+    # Q = K = 0: every weight is exactly 1, l = n (a power of two), so each
+    # output is the single nonzero V of its feature divided by n, exactly.
+    q, k, v = fixture(n, "uniform-sparse-value")
+    o, lse = run(q, k, v, False)
+    expect = (v.double().sum(dim=2, keepdim=True) / n).expand_as(o).to(torch.bfloat16)
+    assert torch.equal(o, expect)
+    assert torch.allclose(lse, torch.full_like(lse, float(np.log(n))), atol=1e-6, rtol=0)
+
+
+@pytest.mark.parametrize("n", [64, 65, 129, 513])
+def test_last_key_dominant_exact(n):
+    # Queries 0..n-2 see one key with weight 1 (the others underflow to 0):
+    # O = V[last] bit for bit.
+    q, k, v = fixture(n, "last-key-dominant")
+    o, _ = run(q, k, v, False)
+    assert torch.equal(o[..., :-1, :], v[..., -1:, :].expand_as(o[..., :-1, :]))
+
+
+def test_cancel_v_is_exactly_zero():
+    # test_numerical_cases.py:5-9 at D = 128: uniform P, V = +-1 alternating.
+    q = torch.zeros(1, 1, 64, D, dtype=torch.bfloat16, device="cuda")
+    v = torch.tensor([1.0, -1.0], device="cuda").repeat(32)[:, None].expand(64, D)
+    v = v.contiguous().to(torch.bfloat16)[None, None]
+    o, _ = run(q, q.clone(), v, False)
+    assert torch.count_nonzero(o) == 0
+
+
+@pytest.mark.parametrize("base,tail", [(128, 129), (192, 193), (512, 513), (64, 200)])
+def test_neutral_extension_bitwise(base, tail):
+    # Keys whose logit is -8192/sqrt(128) below every live key contribute
+    # exact zeros: outputs of the first `base` queries are bit-identical.
+    q, k, v = qkv(1, 2, tail, tail, torch.bfloat16, seed=base)
+    q[..., 0] = 1
+    k[..., :base, 0] = 0
+    k[..., base:, 0] = -8192
+    v[..., base:, :] = -32768
+    o_full, _ = run(q, k, v, False)
+    o_short, _ = run(q[..., :base, :].contiguous(), k[..., :base, :].contiguous(),
+                     v[..., :base, :].contiguous(), False)
+    assert torch.equal(o_full[..., :base, :], o_short)
+
+
+def test_duplicated_queries_and_causal_row0():
+    q, k, v = qkv(1, 2, 512, 512, torch.bfloat16, seed=77)
+    q[..., 300:, :] = q[..., 5:6, :]
+    o, _ = run(q, k, v, False)
+    assert torch.equal(o[..., 300:, :], o[..., 5:6, :].expand_as(o[..., 300:, :]))
+    o, _ = run(q, k, v, True)
+    assert torch.equal(o[..., 0, :], v[..., 0, :])  # causal row 0 sees key 0 only
+
+
+def test_sentinel_guards_strides_and_unchanged_inputs():
+    b, h, s = 2, 3, 200
+    q, k, v = qkv(b, h, s, s, torch.bfloat16, seed=3)
+    q0, k0, v0 = q.clone(), k.clone(), v.clone()
+    go = Guarded((b, h, s, D), torch.bfloat16)
+    gl = Guarded((b, h, s), torch.float32)
+    rt.attn_fwd(q, k, v, go.t, causal=True, sm_scale=SCALE, lse=gl.t)
+    torch.cuda.synchronize()
+    assert go.guards_intact() and gl.guards_intact()
+    assert torch.equal(q, q0) and torch.equal(k, k0) and torch.equal(v, v0)
+    # BSHD-strided views (heads interleaved) give the same result as BHSD.
+    qs, ks, vs = (x.transpose(1, 2).contiguous().transpose(1, 2) for x in (q, k, v))
+    o2 = torch.empty(b, s, h, D, dtype=torch.bfloat16, device="cuda").transpose(1, 2)
+    rt.attn_fwd(qs, ks, vs, o2, causal=True, sm_scale=SCALE)
+    torch.cuda.synchronize()
+    assert torch.equal(o2, go.t)

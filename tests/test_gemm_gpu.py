@@ -1,0 +1,182 @@
+"""GEMM parity on the GPU through the C-ABI (frisk_gemm), against the fp64 /
+exact-integer oracle.  Tolerances: int8 -> int32
+bit-exact; f16/bf16 max|err| <= 1e-2 * ||ref row||_inf; fp8 max|err| <=
+2e-2 * ||ref row||_inf and relative Frobenius <= 2e-2; f32 outputs of
+16-bit inputs 1e-5 (no output rounding)."""
+import itertools
+
+import numpy as np
+import pytest
+import torch
+
+from frisk_amd import runtime as rt
+from oracle import gemm as G
+from tests.gpu_util import Guarded, decode, fp8_per_tensor, randn, sample_rows
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.bfloat16: 1e-2, torch.float16: 1e-2, torch.float32: 1e-5}
+FP8 = torch.float8_e4m3fn
+
+
+def make_operands(m, n, k, dt, ta, tb, seed):
+    a_shape = (k, m) if ta else (m, k)
+    b_shape = (n, k) if tb else (k, n)
+    if dt == torch.int8:
+        g = torch.Generator(device="cuda")
+        g.manual_seed(seed)
+        a = torch.randint(-127, 128, a_shape, generator=g, device="cuda", dtype=torch.int8)
+        b = torch.randint(-127, 128, b_shape, generator=g, device="cuda", dtype=torch.int8)
+        return a, b, 1.0, 1.0
+    if dt == FP8:
+        a, sa = fp8_per_tensor(randn(a_shape, seed))
+        b, sb = fp8_per_tensor(randn(b_shape, seed + 1))
+        return a, b, sa, sb
+    return randn(a_shape, seed).to(dt), randn(b_shape, seed + 1).to(dt), 1.0, 1.0
+
+
+def reference(a, b, ta, tb, sa, sb, rows=None):
+    A = decode(a)
+    B = decode(b)
+    A = A.T if ta else A
+    B = B.T if tb else B
+    if rows is not None:
+        A = A[rows]
+    if a.dtype == torch.int8:
+        return A @ B
+    return (A @ B) * (sa * sb)
+
+
+def check(got, ref, in_dt, out_dt):
+    if in_dt == torch.int8:
+        assert np.array_equal(got.astype(np.int64), ref), "int8 GEMM must be bit-exact"
+        return
+    err = G.row_scaled_error(got, ref)
+    if in_dt == FP8:
+        fro = np.linalg.norm(got - ref) / np.linalg.norm(ref)
+        assert err <= 2e-2 and fro <= 2e-2, (err, fro)
+    else:
+        tol = TOL[out_dt] if out_dt != torch.float32 else TOL[torch.float32]
+        assert err <= tol, err
+
+
+PAIRS = [(torch.bfloat16, torch.bfloat16), (torch.bfloat16, torch.float32),
+         (torch.float16, torch.float16), (torch.float16, torch.float32),
+         (FP8, torch.bfloat16), (FP8, torch.float16), (FP8, torch.float32),
+         (torch.int8, torch.int32), (torch.float32, torch.float32)]
+SHAPES = [(64, 64, 64), (256, 256, 128), (300, 264, 136), (100, 72, 48), (33, 17, 40),
+          (512, 256, 1024)]
+
+
+@pytest.mark.parametrize("in_dt,out_dt", PAIRS, ids=lambda x: str(x).replace("torch.", ""))
+@pytest.mark.parametrize("ta,tb", list(itertools.product([False, True], repeat=2)))
+def test_small_shapes_every_type_and_layout(in_dt, out_dt, ta, tb):
+    for i, (m, n, k) in enumerate(SHAPES):
+        print(f"case {in_dt}->{out_dt} ta={ta} tb={tb} m={m} n={n} k={k}", flush=True)
+        a, b, sa, sb = make_operands(m, n, k, in_dt, ta, tb, seed=100 + i)
+        c = torch.zeros(m, n, dtype=out_dt, device="cuda")
+        rt.gemm(a, b, c, trans_a=ta, trans_b=tb, scale_a=sa, scale_b=sb)
+        torch.cuda.synchronize()
+        got = decode(c).astype(np.float64)
+        ref = reference(a, b, ta, tb, sa, sb)
+        ref = np.asarray(ref, dtype=np.float64) if in_dt != torch.int8 else ref
+        # f32 outputs of fp32 inputs see fp32 accumulation over K.
+        check(got if in_dt != torch.int8 else decode(c), ref, in_dt, out_dt)
+
+
+@pytest.mark.parametrize("in_dt,out_dt", [(torch.bfloat16, torch.bfloat16),
+                                          (torch.bfloat16, torch.float32),
+                                          (torch.int8, torch.int32), (FP8, torch.float32)],
+                         ids=lambda x: str(x).replace("torch.", ""))
+def test_accumulate_into_c(in_dt, out_dt):
+    m, n, k = 256, 264, 192
+    a, b, sa, sb = make_operands(m, n, k, in_dt, False, True, seed=7)
+    if out_dt == torch.int32:
+        c0 = torch.randint(-1000, 1000, (m, n), dtype=torch.int32, device="cuda")
+    else:
+        c0 = randn((m, n), 9).to(out_dt)
+    c = c0.clone()
+    rt.gemm(a, b, c, trans_b=True, clear_accum=False, scale_a=sa, scale_b=sb)
+    torch.cuda.synchronize()
+    ref = reference(a, b, False, True, sa, sb) + decode(c0)
+    check(decode(c), ref, in_dt, out_dt)
+
+
+def test_sentinel_guards_and_unchanged_inputs():
+    m, n, k = 300, 264, 136
+    for dt, odt in [(torch.bfloat16, torch.bfloat16), (torch.int8, torch.int32)]:
+        a, b, _, _ = make_operands(m, n, k, dt, False, True, seed=11)
+        a0, b0 = a.clone(), b.clone()
+        gc = Guarded((m, n), odt)
+        rt.gemm(a, b, gc.t, trans_b=True)
+        torch.cuda.synchronize()
+        assert gc.guards_intact()
+        assert torch.equal(a, a0) and torch.equal(b, b0)
+
+
+def run_sampled(m, n, k, in_dt, out_dt, seed, rows=48, std_a=1.0, std_b=1.0):
+    if in_dt in (torch.bfloat16, torch.float16):
+        a = randn((m, k), seed, std_a).to(in_dt)
+        b = randn((n, k), seed + 1, std_b).to(in_dt)
+        sa = sb = 1.0
+    else:
+        a, b, sa, sb = make_operands(m, n, k, in_dt, False, True, seed)
+    c = torch.empty(m, n, dtype=out_dt, device="cuda")
+    rt.gemm(a, b, c, trans_b=True, scale_a=sa, scale_b=sb)
+    torch.cuda.synchronize()
+    r = sample_rows(m, rows, seed)
+    got = decode(c[torch.from_numpy(r).cuda()])
+    ref = reference(a, b, False, True, sa, sb, rows=r)
+    check(got, ref, in_dt, out_dt)
+    return a, b, c, sa, sb
+
+
+def test_config_c1_fp32_512():
+    # fp32 C = A.B, row-major A and B, U[-1, 1].
+    rng = np.random.default_rng(0)
+    a_np = rng.uniform(-1, 1, (512, 512)).astype(np.float32)
+    b_np = rng.uniform(-1, 1, (512, 512)).astype(np.float32)
+    a, b = torch.from_numpy(a_np).cuda(), torch.from_numpy(b_np).cuda()
+    c = torch.empty(512, 512, device="cuda")
+    rt.gemm(a, b, c)
+    torch.cuda.synchronize()
+    got = c.cpu().numpy().astype(np.float64)
+    assert G.row_scaled_error(got, G.gemm_fp64(a_np, b_np)) <= 1e-5
+    # The reference's fp32 rank-1 oracle agrees to fp32 summation error.
+    assert G.row_scaled_error(got, G.gemm_fp32_rank1(a_np, b_np)) <= 1e-5
+
+
+def test_config_c2_fp16_4096_nt():
+    a, b, c, _, _ = run_sampled(4096, 4096, 4096, torch.float16, torch.float16, seed=2)
+    # Row checksums of every row: C.1 against A.(B^T.1) in fp64.
+    ones = torch.ones(4096, 1, dtype=torch.float64, device="cuda")
+    lhs = (c.double() @ ones)[:, 0]
+    rhs = (a.double() @ (b.double().t() @ ones))[:, 0]
+    scale = (a.double().abs() @ (b.double().abs().t() @ ones))[:, 0]
+    assert float(((lhs - rhs).abs() / scale).max()) < 1e-2
+
+
+@pytest.mark.parametrize("n,k", [(4096, 4096), (14336, 4096), (4096, 14336)])
+@pytest.mark.parametrize("m", [16, 128, 1024, 8192])
+def test_config_c3_projection_sweep(m, n, k):
+    # W[N, K] ~ N(0, 0.02), X[M, K] ~ N(0, 1), Y = X.W^T, bf16.
+    print(f"case projection m={m} n={n} k={k}", flush=True)
+    run_sampled(m, n, k, torch.bfloat16, torch.bfloat16, seed=3 + m, rows=32, std_b=0.02)
+
+
+def test_config_c4_fp8():
+    # e4m3 A[4096, 8192] . B[8192, 8192] (B stored [N, K]),
+    # per-tensor fp32 scales, bf16 output.
+    run_sampled(4096, 8192, 8192, FP8, torch.bfloat16, seed=4, rows=32)
+
+
+def test_config_c4_int8_exact_with_row_checksums():
+    a, b, c, _, _ = run_sampled(4096, 4096, 4096, torch.int8, torch.int32, seed=5, rows=32)
+    # Every row, exactly: C.1 == A.(B^T.1) in int64 (a checksum of the whole
+    # product), and the checksum of checksums 1^T.C.1.
+    c64 = c.cpu().numpy().astype(np.int64)
+    a64 = a.cpu().numpy().astype(np.int64)
+    bsum = b.cpu().numpy().astype(np.int64).sum(axis=0)
+    assert np.array_equal(c64.sum(axis=1), a64 @ bsum)
+    assert int(c64.sum()) == int(a64.sum(axis=0) @ b.cpu().numpy().astype(np.int64).sum(axis=0))
+    assert np.array_equal(c64.sum(axis=0), (a64.sum(axis=0) @ b.cpu().numpy().astype(np.int64).T))
