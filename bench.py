@@ -1,0 +1,222 @@
+#!/usr/bin/env python3
+"""Benchmark of the GEMM + attention hot path on one MI355X.
+
+A step is one launch of the headline kernel over one batch of synthetic,
+HBM-resident input: the bf16 GEMM C[4096, 4096] = A[4096, 4096] . B^T with
+B stored [N, K] (A and B ~ N(0, 1), f32 accumulation, bf16 output), the
+"bf16 4096^3" of BASELINE.json's metric.  `value` is its TFLOP/s
+(2*M*N*K per launch).  The same JSON line carries the other workloads the
+metric names, each timed the same way (W warm-up launches, then K timed
+launches between device synchronisations): fp16 4096^3 NT,
+fp8-e4m3 4096x8192x8192 with per-tensor scales, int8 4096^3,
+and the flash-attention forward at b4 h32 s4096 d128 bf16, non-causal and
+causal (configs[4]; causal FLOPs counted as half).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+       python bench.py --only NAME --steps K   (one workload, for rocprofv3)
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK = {"bf16": 2500.0, "f16": 2500.0, "fp8": 5000.0, "int8": 5000.0}  # dense TFLOP/s (TOP/s)
+HBM_PEAK_GBS = 8000.0
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--only", default=None, help="run a single workload (for profilers)")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    return p.parse_args()
+
+
+def make_workloads(torch, rt):
+    """name -> (dtype label, flops per launch, setup() -> launch callable)."""
+    dev = "cuda"
+
+    def gen(seed):
+        g = torch.Generator(device=dev)
+        g.manual_seed(seed)
+        return g
+
+    def gemm(m, n, k, kind):
+        def setup():
+            if kind == "int8":
+                a = torch.randint(-127, 128, (m, k), generator=gen(1), device=dev, dtype=torch.int8)
+                b = torch.randint(-127, 128, (n, k), generator=gen(2), device=dev, dtype=torch.int8)
+                c = torch.empty(m, n, dtype=torch.int32, device=dev)
+                return lambda: rt.gemm(a, b, c, trans_b=True)
+            if kind == "fp8":
+                a = torch.randn(m, k, generator=gen(1), device=dev)
+                b = torch.randn(n, k, generator=gen(2), device=dev)
+                sa, sb = 448.0 / float(a.abs().max()), 448.0 / float(b.abs().max())
+                a8, b8 = (a * sa).to(torch.float8_e4m3fn), (b * sb).to(torch.float8_e4m3fn)
+                del a, b
+                c = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+                return lambda: rt.gemm(a8, b8, c, trans_b=True, scale_a=1 / sa, scale_b=1 / sb)
+            dt = torch.bfloat16 if kind == "bf16" else torch.float16
+            a = torch.randn(m, k, generator=gen(1), device=dev).to(dt)
+            b = torch.randn(n, k, generator=gen(2), device=dev).to(dt)
+            c = torch.empty(m, n, dtype=dt, device=dev)
+            return lambda: rt.gemm(a, b, c, trans_b=True)
+        return setup
+
+    def attn(causal):
+        def setup():
+            shape = (4, 32, 4096, 128)
+            q = torch.randn(shape, generator=gen(5), device=dev).to(torch.bfloat16)
+            k = torch.randn(shape, generator=gen(6), device=dev).to(torch.bfloat16)
+            v = torch.randn(shape, generator=gen(7), device=dev).to(torch.bfloat16)
+            o = torch.empty_like(q)
+            return lambda: rt.attn_fwd(q, k, v, o, causal=causal, sm_scale=128 ** -0.5)
+        return setup
+
+    def copy(nbytes):
+        def setup():
+            src = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1)
+            dst = torch.empty_like(src)
+            return lambda: dst.copy_(src)
+        return setup
+
+    fa = 4.0 * 4 * 32 * 4096 * 4096 * 128
+    return {
+        "gemm_bf16_4096": ("bf16", 2.0 * 4096 ** 3, gemm(4096, 4096, 4096, "bf16")),
+        "gemm_f16_4096_nt": ("f16", 2.0 * 4096 ** 3, gemm(4096, 4096, 4096, "f16")),
+        "gemm_fp8_4096x8192x8192": ("fp8", 2.0 * 4096 * 8192 * 8192,
+                                    gemm(4096, 8192, 8192, "fp8")),
+        "gemm_int8_4096": ("int8", 2.0 * 4096 ** 3, gemm(4096, 4096, 4096, "int8")),
+        "fa_fwd_b4h32s4096d128": ("bf16", fa, attn(False)),
+        "fa_fwd_b4h32s4096d128_causal": ("bf16", fa / 2, attn(True)),
+        # Calibration only (--only): a plain 256 MiB device copy, whose
+        # FETCH_SIZE / WRITE_SIZE per dispatch scale the HBM counters.
+        "copy_256mib": ("bytes", 0.0, copy(256 << 20)),
+    }
+
+
+def time_launches(torch, fn, steps, warmup):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps  # ms per launch
+
+
+def cpu_baseline(torch):
+    """fp64 C oracle (oracle/oracle.c) on a bounded sample of the headline
+    workload: 512 of the 4096 output rows of the bf16 4096^3 GEMM, inputs
+    decoded exactly from bf16, all CPU threads of this process."""
+    import numpy as np
+    from oracle import native
+    native.load()
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or native.max_threads()
+    rows, n, k = 512, 4096, 4096
+    g = torch.Generator()
+    g.manual_seed(1)
+    a = torch.randn(rows, k, generator=g).to(torch.bfloat16).double().numpy()
+    b = torch.randn(n, k, generator=g).to(torch.bfloat16).double().numpy()
+    native.gemm_f64(a[:8], b, trans_b=True, threads=threads)  # warm up threads
+    t0 = time.perf_counter()
+    native.gemm_f64(a, b, trans_b=True, threads=threads)
+    dt = time.perf_counter() - t0
+    return {"value": round(2.0 * rows * n * k / dt / 1e12, 6), "unit": "TFLOP/s",
+            "cores": threads, "kind": "port",
+            "sample": f"{rows} of 4096 rows of the 4096^3 GEMM (fp64 oracle/oracle.c, "
+                      f"{dt:.2f} s wall)"}
+
+
+def traffic_from_profile(name):
+    """HBM bytes per launch recorded from rocprofv3 FETCH_SIZE/WRITE_SIZE
+    passes (profiles/hbm_traffic.txt, one JSON object per line)."""
+    path = ROOT / "profiles" / "hbm_traffic.txt"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        line = line.strip()
+        if line.startswith("{"):
+            rec = json.loads(line)
+            if rec.get("kernel_workload") == name:
+                return rec.get("traffic_bytes")
+    return None
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
+              "GEMM and attention shard across GPUs without exchange, see DESIGN.md",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from frisk_amd import runtime as rt
+    rt.load()
+    torch.cuda.set_device(0)
+    work = make_workloads(torch, rt)
+    if args.only:
+        label, flops, setup = work[args.only]
+        fn = setup()
+        ms = time_launches(torch, fn, args.steps, args.warmup)
+        print(json.dumps({"workload": args.only, "ms": ms, "tflops": flops / ms / 1e9}), flush=True)
+        return
+
+    results = {}
+    for name, (label, flops, setup) in work.items():
+        if label == "bytes":
+            continue
+        fn = setup()
+        steps = args.steps
+        ms = time_launches(torch, fn, steps, args.warmup)
+        tf = flops / ms / 1e9
+        results[name] = {"dtype": label, "ms": round(ms, 6), "tflops": round(tf, 2),
+                         "frac_peak": round(tf / PEAK[label], 4)}
+        del fn
+        torch.cuda.empty_cache()
+
+    head = results["gemm_bf16_4096"]
+    flops = 2.0 * 4096 ** 3
+    traffic = traffic_from_profile("gemm_bf16_4096")
+    line = {
+        "metric": "GEMM TFLOP/s & % MFMA peak (bf16/fp8 4096^3); FA-fwd TFLOP/s at s=4096",
+        "value": head["tflops"],
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["ms"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1), HBM-resident before timing)",
+        "config": {"workload": "bf16 GEMM M=N=K=4096, A [M,K] row-major, B [N,K] (NT), "
+                               "f32 accumulate, bf16 out; one launch per step",
+                   "m": 4096, "n": 4096, "k": 4096, "layout": "NT"},
+        "roofline": {"bound": "mfma", "achieved": head["tflops"], "peak": PEAK["bf16"],
+                     "unit": "TFLOP/s", "frac": round(head["tflops"] / PEAK["bf16"], 4),
+                     "traffic": traffic},
+        "workloads": results,
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(torch)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()
