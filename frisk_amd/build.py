@@ -26,6 +26,9 @@ COMMON = [
     "-fPIC",
     # Packed-fp32 VALU forms are kept out of generated code on this platform.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in VGPRs: the softmax rescale and epilogue read them
+    # with VALU ops, which would otherwise copy AGPRs back and forth.
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wno-unused-command-line-argument",
 ]
 

@@ -59,6 +59,12 @@ template <> struct AttnMfma<Elt::BF16> {
     v2 v = {(__bf16)lo, (__bf16)hi};
     return __builtin_bit_cast(uint32_t, v);
   }
+  // acc + lo + hi of a packed pair (v_dot2c_f32_bf16 with (1, 1)).
+  __device__ static inline float dot2_ones(uint32_t w, float acc) {
+    typedef __bf16 v2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2, w),
+                                           __builtin_bit_cast(v2, 0x3f803f80u), acc, false);
+  }
 };
 template <> struct AttnMfma<Elt::F16> {
   __device__ static inline f32x16 run(i32x4 a, i32x4 b, f32x16 c) {
@@ -69,6 +75,11 @@ template <> struct AttnMfma<Elt::F16> {
     typedef _Float16 v2 __attribute__((ext_vector_type(2)));
     v2 v = {(_Float16)lo, (_Float16)hi};
     return __builtin_bit_cast(uint32_t, v);
+  }
+  __device__ static inline float dot2_ones(uint32_t w, float acc) {
+    typedef _Float16 v2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(v2, w), __builtin_bit_cast(v2, 0x3c003c00u),
+                                  acc, false);
   }
 };
 
@@ -237,17 +248,11 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(
     __syncthreads();
   }
 
-  for (int j = 0; j < nkb; ++j) {
-    const int buf = j & 1;
-    const bool more = j + 1 < nkb;
-    if (more) {
-      issue_k(j + 1, buf ^ 1);
-      load_v(j + 1);
-    }
-    const char* ks = smem + buf * kBuf;
-    const char* vt = ks + kKTile;
-
-    // S^T = K . Q^T: two 32-key tiles x QT query tiles, 8 head-dim steps.
+  // One key block: S^T = K.Q^T, online softmax, O^T += V^T.P^T.  Masked
+  // blocks (the sequence tail, and blocks crossing this wave's causal
+  // diagonal) apply the key mask; every other block runs without it.
+  auto key_block = [&](const char* ks, const char* vt, int kbase, bool masked) {
+    // S^T: two 32-key tiles x QT query tiles, 8 head-dim steps.
     f32x16 s[QT][2];
 #pragma unroll
     for (int t = 0; t < QT; ++t) s[t][0] = s[t][1] = f32x16{};
@@ -261,75 +266,81 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(
         for (int t = 0; t < QT; ++t) s[t][kt] = Mf::run(kf, qf[t][ds], s[t][kt]);
       }
     }
-
-    // Online softmax in the exp2 domain.
-    const int kbase = j * kBN;
-    const bool tail = kbase + kBN > seq_k;
+    // Online softmax in the exp2 domain: p = exp2(s * scale_log2 - m).
+    // The max is taken on raw scores (scale_log2 > 0 commutes with max).
+    i32x4 pf[QT][4];
 #pragma unroll
     for (int t = 0; t < QT; ++t) {
-      const int qi = wq0 + t * 32 + l32;
-      const bool diag_blk = CAUSAL && (kbase + kBN - 1 > wq0 + t * 32 + diag);
-      float mb = -__builtin_inff();
+      if (masked) {  // wave-uniform branch
+        const int qi = wq0 + t * 32 + l32;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int key = kbase + kt * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+            if (key >= seq_k || (CAUSAL && key > qi + diag)) s[t][kt][r] = -__builtin_inff();
+          }
+      }
+      float mraw = -__builtin_inff();
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          float x = s[t][kt][r] * scale_log2;
-          if (tail || diag_blk) {
-            const int key = kbase + kt * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-            if (key >= seq_k || (CAUSAL && key > qi + diag)) x = -__builtin_inff();
-          }
-          s[t][kt][r] = x;
-          mb = fmaxf(mb, x);
-        }
-      mb = pair_reduce(mb, true);
+        for (int r = 0; r < 16; ++r) mraw = fmaxf(mraw, s[t][kt][r]);
+      const float mb = pair_reduce(mraw, true) * scale_log2;
       const bool move = mb > m[t] + kRescaleSlack;
       if (__builtin_amdgcn_ballot_w64(move)) {
-        const float mn = move ? mb : m[t];
         // exp2(-inf) = 0 on a row's first visible block; rows that do not
         // move keep alpha = 1 (m - mn would be NaN for m = mn = -inf).
-        const float alpha = move ? __builtin_amdgcn_exp2f(m[t] - mn) : 1.0f;
-        m[t] = mn;
+        const float alpha = move ? __builtin_amdgcn_exp2f(m[t] - mb) : 1.0f;
+        m[t] = move ? mb : m[t];
         l[t] *= alpha;
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt) o[t][dt] *= alpha;
       }
-      // A row with every key masked so far keeps m = -inf; use 0 as the
-      // subtrahend so its (all -inf) scores give p = 0 instead of NaN.
-      const float msub = m[t] == -__builtin_inff() ? 0.0f : m[t];
-      float rs = 0.0f;
+      // A row with every key masked so far keeps m = -inf; subtracting 0
+      // instead gives its (all -inf) scores p = 0 rather than NaN.
+      const float nm = m[t] == -__builtin_inff() ? 0.0f : -m[t];
+      float rs = l[t];
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
+      for (int kk = 0; kk < 4; ++kk) {
+        const int kt = kk >> 1, r0 = 8 * (kk & 1);
+        uint32_t w[4];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float p = __builtin_amdgcn_exp2f(s[t][kt][r] - msub);
-          s[t][kt][r] = p;
-          rs += p;
+        for (int e = 0; e < 4; ++e) {
+          const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][kt][r0 + 2 * e], scale_log2, nm));
+          const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][kt][r0 + 2 * e + 1], scale_log2, nm));
+          w[e] = Mf::pack(p0, p1);
+          rs = Mf::dot2_ones(w[e], rs);  // the row sum uses the rounded P of the PV product
         }
-      l[t] += rs;
+        pf[t][kk] = i32x4{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+      }
+      l[t] = rs;
     }
-
     // O^T += V^T . P^T over 4 key steps of 16.
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-      i32x4 pf[QT];
-#pragma unroll
-      for (int t = 0; t < QT; ++t) {
-        const int kt = kk >> 1, r0 = 8 * (kk & 1);
-        pf[t] = i32x4{(int)Mf::pack(s[t][kt][r0 + 0], s[t][kt][r0 + 1]),
-                      (int)Mf::pack(s[t][kt][r0 + 2], s[t][kt][r0 + 3]),
-                      (int)Mf::pack(s[t][kt][r0 + 4], s[t][kt][r0 + 5]),
-                      (int)Mf::pack(s[t][kt][r0 + 6], s[t][kt][r0 + 7])};
-      }
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
         const int d = dt * 32 + l32;
         const i32x4 vf = *(const i32x4*)(vt + d * 128 + (((2 * kk + half) ^ (d & 7)) << 4));
 #pragma unroll
-        for (int t = 0; t < QT; ++t) o[t][dt] = Mf::run(vf, pf[t], o[t][dt]);
+        for (int t = 0; t < QT; ++t) o[t][dt] = Mf::run(vf, pf[t][kk], o[t][dt]);
       }
     }
+  };
 
+  for (int j = 0; j < nkb; ++j) {
+    const int buf = j & 1;
+    const bool more = j + 1 < nkb;
+    if (more) {
+      issue_k(j + 1, buf ^ 1);
+      load_v(j + 1);
+    }
+    const char* ks = smem + buf * kBuf;
+    const int kbase = j * kBN;
+    // Wave-uniform: does any key of this block need masking for this wave?
+    const bool masked = kbase + kBN > seq_k || (CAUSAL && kbase + kBN - 1 > wq0 + diag);
+    key_block(ks, ks + kKTile, kbase, masked);
     if (more) {
       FRISK_WAIT_VMCNT0();
       store_vt(buf ^ 1);

@@ -86,14 +86,17 @@ template <> struct Mfma32<Elt::I8> {
 // flight while one stage is multiplied.
 //
 // LDS row = 4 chunks of 16 B.  Chunk c of row r is stored at physical chunk
-// c ^ swz(r), swz(r) = ((r >> 1) ^ (r >> 3)) & 3.  A 32x32 MFMA fragment
-// read has lanes 0-31 read one logical chunk of 32 consecutive rows; with
-// 128 B bank lines (32 banks) the 8 rows of a lane octet land on (r & 1,
-// swz) = 8 distinct 16 B bank groups, and with 256 B lines (64 banks) the
-// 16 rows of a lane group land on (r & 3, swz) = 16 distinct groups.  swz is
-// linear over GF(2) in the row bits, i.e. a bit-linear shared layout.
+// c ^ swz(r), swz(r) = (r >> 2) & 3.  A 32x32 MFMA fragment read has lanes
+// 0-31 read one logical chunk of 32 consecutive rows (lanes 32-63 the next
+// chunk).  gfx950 serves ds_read_b128 at 256 B/clk (64 banks of 4 B, 16
+// lanes per cycle); under this map the 16 rows of a lane group cover the 16
+// distinct 16 B bank groups of a 256 B line ((r & 3) picks the quarter,
+// swz the chunk), and rocprofv3 counts SQ_LDS_BANK_CONFLICT = 0 for it,
+// where ((r >> 1) ^ (r >> 3)) & 3 measured 2-way conflicts and no swizzle
+// 4-way.  swz is linear over GF(2) in the row bits (a bit-linear shared
+// layout); the DMA side applies it by choosing which chunk a lane fetches.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ int swz(int row) { return ((row >> 1) ^ (row >> 3)) & 3; }
+__device__ __forceinline__ int swz(int row) { return (row >> 2) & 3; }
 
 constexpr int kBM = 256, kBN = 256, kRow = 64;
 constexpr int kTileBytes = kBM * kRow;    // 16 KiB per operand per stage

@@ -1,7 +1,10 @@
 """Flash-attention forward parity on the GPU through the C-ABI
 (frisk_attn_fwd) against the fp64 oracle, plus the reference's exact
 fixtures carried over to head_dim 128.  Tolerance:
-max|err| <= 1e-2 * ||ref row||_inf for bf16/f16 outputs; LSE within 1e-3."""
+max|err| <= 1e-2 * ||ref row||_inf for bf16/f16 outputs.  The kernel's row
+sum (hence LSE) adds the probabilities as rounded for the P.V product, so
+LSE is held to the rounding of one probability: 4e-3 (bf16, 2^-8) and 1e-3
+(f16)."""
 import numpy as np
 import pytest
 import torch
@@ -15,6 +18,7 @@ pytestmark = pytest.mark.gpu
 
 D = 128
 SCALE = D ** -0.5
+LSE_TOL = {torch.bfloat16: 4e-3, torch.float16: 1e-3}
 
 
 def qkv(b, h, sq, sk, dt, seed):
@@ -51,7 +55,7 @@ def test_parity_small(b, h, sq, sk, causal, dt):
     assert G.row_scaled_error(got[live], ref[live]) <= 1e-2
     assert np.all(got[~live] == 0)
     l = lse.cpu().numpy()
-    assert np.abs(l[live] - rlse[live]).max() <= 1e-3
+    assert np.abs(l[live] - rlse[live]).max() <= LSE_TOL[dt]
     assert np.all(np.isneginf(l[~live]))
 
 
@@ -68,7 +72,7 @@ def test_config_c5_full_size_sampled_heads(native_oracle, causal):
                                         v[bi, hi].double().cpu().numpy(), causal=causal,
                                         scale=SCALE)
         assert G.row_scaled_error(o[bi, hi].double().cpu().numpy(), ro) <= 1e-2
-        assert np.abs(lse[bi, hi].cpu().numpy() - rl).max() <= 1e-3
+        assert np.abs(lse[bi, hi].cpu().numpy() - rl).max() <= LSE_TOL[torch.bfloat16]
     assert torch.isfinite(o.float()).all()
 
 
