@@ -16,18 +16,18 @@
 //  * The S^T accumulator element r of lane (l32, h) is key 8(r/4)+4h+r%4.
 //    Converted to bf16 it is used unchanged as the B operand (P^T) of
 //    O^T = V^T.P^T: MFMA k-slot (h, e) then means key
-//    16ks + (e < 4 ? 4h+e : 8+4h+e-4).  V is stored transposed in LDS (V^T,
-//    one 128 B row per head-dim index) with keys permuted inside every group
-//    of 16 the same way, so a lane's 8 keys are one 16 B chunk.
+//    16ks + (e < 4 ? 4h+e : 8+4h+e-4).  V stays row-major in LDS; its
+//    V^T fragments, in exactly that key order, come from the gfx950
+//    transposing LDS read ds_read_b64_tr_b16 (two per fragment).
 //  * O^T accumulators also keep query = lane%32, so the softmax rescale is a
 //    per-lane scalar.  Rescaling is lazy: the running max only moves when a
 //    block's max exceeds it by more than 2^8 in the exp2 domain, keeping
 //    every p <= 256 (exact in the final O / l, representable in bf16/f16).
-//  * K tiles (64 keys x 256 B) arrive by LDS-DMA with a 16-chunk XOR
-//    swizzle; V tiles go through registers, are transposed 4x8 in
-//    registers and written as 8 B pieces of V^T (8-chunk XOR swizzle).
-//  * Both tiles are double-buffered: the loads of key block j+1 are in
-//    flight during the MFMAs and softmax of block j.
+//  * K and V tiles (64 keys x 256 B each) arrive by LDS-DMA with XOR
+//    swizzles chosen for their read patterns, double-buffered: the loads of
+//    key block j+1 are in flight during the MFMAs and softmax of block j.
+//  * Key blocks that need no mask run in a loop without mask code; the few
+//    blocks at the sequence end / causal diagonal run a masked copy.
 
 #include "common.h"
 #include "kernels.h"
@@ -39,7 +39,7 @@ namespace {
 constexpr int kD = 128;       // head dim
 constexpr int kBN = 64;       // keys per block
 constexpr int kKTile = kBN * kD * 2;  // 16 KiB
-constexpr int kVTile = kBN * kD * 2;  // 16 KiB (as V^T)
+constexpr int kVTile = kBN * kD * 2;  // 16 KiB
 constexpr int kBuf = kKTile + kVTile;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
@@ -152,82 +152,59 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(
     for (int ds = 0; ds < 8; ++ds) qf[t][ds] = *(const i32x4*)(row + ds * 32);
   }
 
-  // ---- K tile by LDS-DMA ------------------------------------------------
+  // ---- K and V tiles by LDS-DMA -------------------------------------------
   // One DMA instruction writes 1 KiB = 4 key rows of 256 B; lane L lands in
-  // row L/16, physical chunk L%16 and fetches logical chunk (L%16)^(row&15).
-  // Rows past seq_k read zeros (buffer range check).
+  // row L/16, physical chunk L%16 and fetches logical chunk
+  // (L%16) ^ swz(row) of that row: swz = row & 15 for K (16 consecutive
+  // rows of one fragment read hit 16 distinct bank groups), 4 * (row & 3)
+  // for V (the 4 key rows of one transposed read, below, hit disjoint
+  // chunk sets).  Rows past seq_k read zeros (buffer range check).
   const __amdgpu_buffer_rsrc_t rsk = __builtin_amdgcn_make_buffer_rsrc(
       (void*)kh, (short)0, (int)min((int64_t)(seq_k - 1) * k_ss * 2 + kD * 2, (int64_t)0x7fffffff),
       0x00020000);
   const __amdgpu_buffer_rsrc_t rsv = __builtin_amdgcn_make_buffer_rsrc(
       (void*)vh, (short)0, (int)min((int64_t)(seq_k - 1) * v_ss * 2 + kD * 2, (int64_t)0x7fffffff),
       0x00020000);
-  constexpr int kKInst = 16 / NW;  // DMA instructions per wave per K tile
-  uint32_t k_off[kKInst];
+  constexpr int kKInst = 16 / NW;  // DMA instructions per wave per tile
+  uint32_t k_off[kKInst], v_off[kKInst];
 #pragma unroll
   for (int i = 0; i < kKInst; ++i) {
     const int r = (wave * kKInst + i) * 4 + (lane >> 4);
-    const int c = (lane & 15) ^ (r & 15);
-    k_off[i] = (uint32_t)(r * k_ss * 2) + c * 16;
+    k_off[i] = (uint32_t)(r * k_ss * 2) + (((lane & 15) ^ (r & 15)) << 4);
+    v_off[i] = (uint32_t)(r * v_ss * 2) + (((lane & 15) ^ (4 * (r & 3))) << 4);
   }
-  auto issue_k = [&](int kb, int buf) {
+  auto issue_kv = [&](int kb, int buf) {
     char* dst = smem + buf * kBuf + wave * kKInst * 1024;
-    const uint32_t base = (uint32_t)((int64_t)kb * kBN * k_ss * 2);
+    const uint32_t kbase = (uint32_t)((int64_t)kb * kBN * k_ss * 2);
+    const uint32_t vbase = (uint32_t)((int64_t)kb * kBN * v_ss * 2);
 #pragma unroll
     for (int i = 0; i < kKInst; ++i) {
       const int r = kb * kBN + (wave * kKInst + i) * 4 + (lane >> 4);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rsk, (lds_ptr_t)(dst + i * 1024), 16,
-                                               r < seq_k ? base + k_off[i] : 0x80000000u, 0, 0,
-                                               0);
+                                               r < seq_k ? kbase + k_off[i] : 0x80000000u, 0,
+                                               0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsv, (lds_ptr_t)(dst + kKTile + i * 1024), 16,
+                                               r < seq_k ? vbase + v_off[i] : 0x80000000u, 0,
+                                               0, 0);
     }
   };
 
-  // ---- V tile through registers, transposed -----------------------------
-  // Unit u = (g, hh, sub, dc): keys 16g + 8sub + 4hh + 0..3, head dims
-  // 8dc..8dc+7.  Its 4 key rows x 8 dims become 8 V^T pieces of 4 keys
-  // (8 B), stored in V^T row d, logical chunk 2g+hh, byte 8*sub.
-  static_assert(kThreads <= 256 && 256 % kThreads == 0, "V transpose units per thread");
-  constexpr int kVUnits = 256 / kThreads;  // units per thread
-  i32x4 vr[kVUnits][4];
-  auto load_v = [&](int kb) {
+  // ---- V^T fragments by transposing LDS reads ------------------------------
+  // ds_read_b64_tr_b16: inside each 16-lane group, lane j receives element
+  // j%4 of the 8 B read by lanes j/4 + 4e, e = 0..3.  Lane 4e+q of group G
+  // (h = G/2, dg = G%2) reads V[16kk + 4h + e (+8)][32dt + 16dg + 4q .. +3],
+  // so lane l receives V[16kk + 4h + 0..3 (+8)][32dt + l%32]: the A operand
+  // of O^T = V^T.P^T with k-slots (h, e) -> key 16kk + (e < 4 ? 4h+e :
+  // 8+4h+e-4), the key order of P taken from the S^T accumulators.
+  int vt_off[4];
+  {
+    const int g = lane >> 4, hh = g >> 1, dg = g & 1, e = (lane >> 2) & 3, q = lane & 3;
 #pragma unroll
-    for (int u = 0; u < kVUnits; ++u) {
-      const int unit = tid + u * kThreads;
-      const int dc = unit & 15, sub = (unit >> 4) & 1, hh = (unit >> 5) & 1, g = unit >> 6;
-      const int key0 = kb * kBN + 16 * g + 8 * sub + 4 * hh;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int key = key0 + i;
-        vr[u][i] = __builtin_amdgcn_raw_buffer_load_b128(
-            rsv, key < seq_k ? (uint32_t)((int64_t)key * v_ss * 2) + dc * 16 : 0x80000000u, 0, 0);
-      }
+    for (int dt = 0; dt < 4; ++dt) {
+      const int chunk = (4 * dt + 2 * dg + (q >> 1)) ^ (4 * e);  // (key & 3) == e
+      vt_off[dt] = kKTile + (4 * hh + e) * 256 + (chunk << 4) + 8 * (q & 1);
     }
-  };
-  auto store_vt = [&](int buf) {
-    char* vt = smem + buf * kBuf + kKTile;
-#pragma unroll
-    for (int u = 0; u < kVUnits; ++u) {
-      const int unit = tid + u * kThreads;
-      const int dc = unit & 15, sub = (unit >> 4) & 1, hh = (unit >> 5) & 1, g = unit >> 6;
-      const uint32_t* w0 = (const uint32_t*)&vr[u][0];
-      const uint32_t* w1 = (const uint32_t*)&vr[u][1];
-      const uint32_t* w2 = (const uint32_t*)&vr[u][2];
-      const uint32_t* w3 = (const uint32_t*)&vr[u][3];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        // dims 8dc+2j (low halves) and 8dc+2j+1 (high halves) of keys 0..3
-        const uint32_t lo01 = (w0[j] & 0xffffu) | (w1[j] << 16);
-        const uint32_t lo23 = (w2[j] & 0xffffu) | (w3[j] << 16);
-        const uint32_t hi01 = (w0[j] >> 16) | (w1[j] & 0xffff0000u);
-        const uint32_t hi23 = (w2[j] >> 16) | (w3[j] & 0xffff0000u);
-        const int d0 = 8 * dc + 2 * j, d1 = d0 + 1;
-        const int c = 2 * g + hh;
-        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-        *(u32x2*)(vt + d0 * 128 + ((c ^ (d0 & 7)) << 4) + 8 * sub) = u32x2{lo01, lo23};
-        *(u32x2*)(vt + d1 * 128 + ((c ^ (d1 & 7)) << 4) + 8 * sub) = u32x2{hi01, hi23};
-      }
-    }
-  };
+  }
 
   // ---- state ---------------------------------------------------------------
   f32x16 o[QT][4];
@@ -241,37 +218,73 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(
   }
 
   if (nkb > 0) {
-    issue_k(0, 0);
-    load_v(0);
+    issue_kv(0, 0);
     FRISK_WAIT_VMCNT0();
-    store_vt(0);
     __syncthreads();
   }
 
   // One key block: S^T = K.Q^T, online softmax, O^T += V^T.P^T.  Masked
   // blocks (the sequence tail, and blocks crossing this wave's causal
   // diagonal) apply the key mask; every other block runs without it.
-  auto key_block = [&](const char* ks, const char* vt, int kbase, bool masked) {
-    // S^T: two 32-key tiles x QT query tiles, 8 head-dim steps.
+  auto key_block = [&](const char* ks, int kbase, auto masked_tag) {
+    constexpr bool kMasked = decltype(masked_tag)::value;
+    // S^T: two 32-key tiles x QT query tiles, 8 head-dim steps, in two
+    // halves of 4 steps: the 8 K fragments of a half are read together
+    // (one LDS latency per half, not per MFMA) and the second half's reads
+    // issue under the first half's MFMAs.  The first half of the V^T
+    // fragments is read before the softmax, whose VALU work hides it.
+    auto read_k = [&](int h0, i32x4 (&kf)[2][4]) {
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        const int r = kt * 32 + l32;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          kf[kt][i] = *(const i32x4*)(ks + r * 256 + (((2 * (h0 + i) + half) ^ (r & 15)) << 4));
+      }
+    };
+    auto read_v = [&](int k0, i32x4 (&vf)[2][4]) {
+      typedef short s16x4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) {
+          const char* p = ks + vt_off[dt] + (k0 + i) * 16 * 256;
+          const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((s16x4*)p);
+          const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((s16x4*)(p + 8 * 256));
+          typedef int i32x2 __attribute__((ext_vector_type(2)));
+          const i32x2 a = __builtin_bit_cast(i32x2, lo), b = __builtin_bit_cast(i32x2, hi);
+          vf[i][dt] = i32x4{a[0], a[1], b[0], b[1]};
+        }
+    };
     f32x16 s[QT][2];
 #pragma unroll
     for (int t = 0; t < QT; ++t) s[t][0] = s[t][1] = f32x16{};
+    i32x4 kf0[2][4], kf1[2][4];
+    read_k(0, kf0);
+    __builtin_amdgcn_sched_barrier(0);
+    read_k(4, kf1);
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-      const int r = kt * 32 + l32;
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int ds = 0; ds < 8; ++ds) {
-        const i32x4 kf = *(const i32x4*)(ks + r * 256 + (((2 * ds + half) ^ (r & 15)) << 4));
+      for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-        for (int t = 0; t < QT; ++t) s[t][kt] = Mf::run(kf, qf[t][ds], s[t][kt]);
-      }
-    }
+        for (int t = 0; t < QT; ++t) s[t][kt] = Mf::run(kf0[kt][i], qf[t][i], s[t][kt]);
+    __builtin_amdgcn_sched_barrier(0);
+    i32x4 vf0[2][4], vf1[2][4];
+    read_v(0, vf0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int t = 0; t < QT; ++t) s[t][kt] = Mf::run(kf1[kt][i], qf[t][4 + i], s[t][kt]);
+    __builtin_amdgcn_sched_barrier(0);
     // Online softmax in the exp2 domain: p = exp2(s * scale_log2 - m).
     // The max is taken on raw scores (scale_log2 > 0 commutes with max).
     i32x4 pf[QT][4];
 #pragma unroll
     for (int t = 0; t < QT; ++t) {
-      if (masked) {  // wave-uniform branch
+      if constexpr (kMasked) {
         const int qi = wq0 + t * 32 + l32;
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt)
@@ -316,37 +329,41 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(
       }
       l[t] = rs;
     }
-    // O^T += V^T . P^T over 4 key steps of 16.
+    // O^T += V^T . P^T over 4 key steps of 16; the second half of the V^T
+    // fragments is read under the first half's MFMAs.
+    read_v(2, vf1);
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt) {
-        const int d = dt * 32 + l32;
-        const i32x4 vf = *(const i32x4*)(vt + d * 128 + (((2 * kk + half) ^ (d & 7)) << 4));
+      for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-        for (int t = 0; t < QT; ++t) o[t][dt] = Mf::run(vf, pf[t][kk], o[t][dt]);
-      }
-    }
+        for (int t = 0; t < QT; ++t) o[t][dt] = Mf::run(vf0[i][dt], pf[t][i], o[t][dt]);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int t = 0; t < QT; ++t) o[t][dt] = Mf::run(vf1[i][dt], pf[t][2 + i], o[t][dt]);
   };
 
-  for (int j = 0; j < nkb; ++j) {
+  // Key blocks [0, n_plain) need no mask for any wave of this workgroup
+  // (they end at or before wave 0's causal diagonal and the sequence end);
+  // the remaining few run the masked variant.  Two loops keep the mask code
+  // out of the main loop.
+  int n_plain = seq_k / kBN;
+  if (CAUSAL) n_plain = min(n_plain, max(0, (q0 + diag + 1) / kBN));
+  n_plain = min(n_plain, nkb);
+  auto step = [&](int j, auto masked_tag) {
     const int buf = j & 1;
     const bool more = j + 1 < nkb;
-    if (more) {
-      issue_k(j + 1, buf ^ 1);
-      load_v(j + 1);
-    }
-    const char* ks = smem + buf * kBuf;
-    const int kbase = j * kBN;
-    // Wave-uniform: does any key of this block need masking for this wave?
-    const bool masked = kbase + kBN > seq_k || (CAUSAL && kbase + kBN - 1 > wq0 + diag);
-    key_block(ks, ks + kKTile, kbase, masked);
-    if (more) {
-      FRISK_WAIT_VMCNT0();
-      store_vt(buf ^ 1);
-    }
+    if (more) issue_kv(j + 1, buf ^ 1);
+    key_block(smem + buf * kBuf, j * kBN, masked_tag);
+    if (more) FRISK_WAIT_VMCNT0();
     __syncthreads();
-  }
+  };
+  for (int j = 0; j < n_plain; ++j) step(j, std::false_type{});
+  for (int j = n_plain; j < nkb; ++j) step(j, std::true_type{});
 
   // ---- epilogue: O = O^T / l, LSE -----------------------------------------
   char* oh = O + (b * o_sb + h * o_sh) * 2;
