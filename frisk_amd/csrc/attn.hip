@@ -391,16 +391,17 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(
 #endif  // __HIP_DEVICE_COMPILE__
 }
 
-#ifndef FRISK_ATTN_QT
-#define FRISK_ATTN_QT 1
-#endif
-#ifndef FRISK_ATTN_NW
-#define FRISK_ATTN_NW 4
-#endif
+// Workgroup shape per mask mode (measured on MI355X at b4 h32 s4096 d128):
+// non-causal runs 8 waves x 32 queries (one K/V tile feeds 256 queries);
+// causal runs 4 waves x 32 queries, whose smaller query blocks balance the
+// triangular work better.
+template <bool CAUSAL> struct AttnShape;
+template <> struct AttnShape<false> { static constexpr int QT = 1, NW = 8; };
+template <> struct AttnShape<true> { static constexpr int QT = 1, NW = 4; };
 
 template <Elt T, bool CAUSAL>
 static hipError_t launch_attn(const AttnArgs& a, hipStream_t stream) {
-  constexpr int QT = FRISK_ATTN_QT, NW = FRISK_ATTN_NW, BM = 32 * QT * NW;
+  constexpr int QT = AttnShape<CAUSAL>::QT, NW = AttnShape<CAUSAL>::NW, BM = 32 * QT * NW;
   auto kern = attn_fwd_kernel<T, QT, NW, CAUSAL>;
   constexpr int lds = 2 * kBuf;
   static const hipError_t attr =
