@@ -126,7 +126,9 @@ int frisk_gemm(const frisk_gemm_desc* d, void* stream) {
                       (d->ldb * ies) % 16 == 0 && aligned16(d->a) && aligned16(d->b) &&
                       aligned16(d->c) && (d->ldc * oes) % 16 == 0 && d->n % 8 == 0;
   hipError_t e;
-  if (mfma_type && tn && vec_ok) e = frisk::gemm_tn_mfma(g, (hipStream_t)stream);
+  if (mfma_type && tn && vec_ok && frisk::gemm_skinny_supported(g))
+    e = frisk::gemm_skinny(g, (hipStream_t)stream);
+  else if (mfma_type && tn && vec_ok) e = frisk::gemm_tn_mfma(g, (hipStream_t)stream);
   else e = frisk::gemm_generic_any(g, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "frisk_gemm launch");
   return FRISK_OK;

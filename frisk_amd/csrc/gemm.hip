@@ -98,15 +98,14 @@ template <> struct Mfma32<Elt::I8> {
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ int swz(int row) { return (row >> 2) & 3; }
 
-constexpr int kBM = 256, kBN = 256, kRow = 64;
-constexpr int kTileBytes = kBM * kRow;    // 16 KiB per operand per stage
-constexpr int kStageBytes = 2 * kTileBytes;
+constexpr int kRow = 64;  // bytes of K per row per stage
 #ifndef FRISK_GEMM_STAGES
 #define FRISK_GEMM_STAGES 4
 #endif
 constexpr int kStages = FRISK_GEMM_STAGES;
-constexpr int kLdsBytes = kStages * kStageBytes;
-static_assert(kLdsBytes <= 160 * 1024, "LDS budget of one CU");
+// LDS bytes of a BT x BT tile pipeline: kStages stages of (A, B) tiles.
+constexpr int lds_bytes(int bt) { return kStages * 2 * bt * kRow; }
+static_assert(lds_bytes(256) <= 160 * 1024, "LDS budget of one CU");
 
 // s_waitcnt with only the vector-memory counter limited to n (gfx9 encoding:
 // vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]).
@@ -168,9 +167,9 @@ struct Frags {
   i32x4 b[TN][LC];
 };
 
-// WM x WN waves tile the 256x256 output; each wave owns a
-// (256/WM) x (256/WN) sub-tile as TM x TN 32x32 accumulators.
-template <Elt IN, Elt OUT, int WM, int WN>
+// One workgroup per BT x BT output tile; WM x WN waves tile it, each wave
+// owning a (BT/WM) x (BT/WN) sub-tile as TM x TN 32x32 accumulators.
+template <Elt IN, Elt OUT, int BT, int WM, int WN>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_tn(const char* __restrict__ A,
                                                              const char* __restrict__ B,
                                                              void* __restrict__ C, int M, int N,
@@ -183,6 +182,10 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_tn(const char* __restr
   using Acc = typename Op::Acc;
   using AccS = typename std::conditional<IN == Elt::I8, int32_t, float>::type;
   constexpr int kWaves = WM * WN;
+  constexpr int kBM = BT, kBN = BT;
+  constexpr int kTileBytes = BT * kRow;  // one operand, one stage
+  constexpr int kStageBytes = 2 * kTileBytes;
+  constexpr int kLdsBytes = lds_bytes(BT);
   constexpr int TM = kBM / WM / 32, TN = kBN / WN / 32;
   constexpr int kStepChunks = Op::kBytes / 16;  // 16 B chunks per row per MFMA
   constexpr int kLaneChunks = kStepChunks / 2;  // chunks per lane per MFMA
@@ -458,20 +461,33 @@ __global__ __launch_bounds__(256) void gemm_generic(const void* __restrict__ A,
 #define FRISK_GEMM_WN 4
 #endif
 
-template <Elt IN, Elt OUT>
-static hipError_t launch_tn(const GemmArgs& g, hipStream_t stream) {
+template <Elt IN, Elt OUT, int BT, int WM, int WN>
+static hipError_t launch_tn_cfg(const GemmArgs& g, hipStream_t stream) {
   constexpr int kEsz = EltInfo<IN>::bytes;
-  constexpr int WM = FRISK_GEMM_WM, WN = FRISK_GEMM_WN;
-  auto kern = gemm_mfma_tn<IN, OUT, WM, WN>;
+  constexpr int kLds = lds_bytes(BT);
+  auto kern = gemm_mfma_tn<IN, OUT, BT, WM, WN>;
   // Thread-safe one-time opt-in to more than 64 KiB of dynamic LDS.
-  static const hipError_t attr = hipFuncSetAttribute(
-      (const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+  static const hipError_t attr =
+      hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
   if (attr != hipSuccess) return attr;
-  const int tiles = (int)(((g.m + kBM - 1) / kBM) * ((g.n + kBN - 1) / kBN));
-  hipLaunchKernelGGL(kern, dim3(tiles), dim3(64 * WM * WN), kLdsBytes, stream, (const char*)g.a,
+  const int tiles = (int)(((g.m + BT - 1) / BT) * ((g.n + BT - 1) / BT));
+  hipLaunchKernelGGL(kern, dim3(tiles), dim3(64 * WM * WN), kLds, stream, (const char*)g.a,
                      (const char*)g.b, g.c, (int)g.m, (int)g.n, (int)(g.k * kEsz),
                      g.lda * kEsz, g.ldb * kEsz, g.ldc, g.scale, g.accumulate);
   return hipGetLastError();
+}
+
+// 256x256 tiles (8 waves, 128x64 each) when there are at least half as
+// many as CUs; otherwise 128x128 tiles (4 waves, 64x64 each, two workgroups
+// per CU), which keep more CUs busy (measured on the projection sweep:
+// M=1024, N=4096 runs 2x faster on 128x128 tiles, N=14336 (224 big tiles)
+// runs faster on 256x256).
+constexpr int kCus = 256;
+template <Elt IN, Elt OUT>
+static hipError_t launch_tn(const GemmArgs& g, hipStream_t stream) {
+  const int64_t tiles256 = ((g.m + 255) / 256) * ((g.n + 255) / 256);
+  if (tiles256 >= kCus / 2) return launch_tn_cfg<IN, OUT, 256, FRISK_GEMM_WM, FRISK_GEMM_WN>(g, stream);
+  return launch_tn_cfg<IN, OUT, 128, 2, 2>(g, stream);
 }
 
 template <Elt IN, Elt OUT>

@@ -29,6 +29,14 @@ struct GemmArgs {
 hipError_t gemm_tn_mfma(const GemmArgs& g, hipStream_t s);
 // Any layout / shape; LDS-tiled FMA kernel.
 hipError_t gemm_generic_any(const GemmArgs& g, hipStream_t s);
+// Small-M kernel (M <= kSkinnyMaxM, bf16/f16, trans_a == 0, trans_b == 1,
+// 16 B aligned K-contiguous rows); memory-bound regime.
+#ifndef FRISK_SKINNY_MAX_M
+#define FRISK_SKINNY_MAX_M 128
+#endif
+constexpr int kSkinnyMaxM = FRISK_SKINNY_MAX_M;
+bool gemm_skinny_supported(const GemmArgs& g);
+hipError_t gemm_skinny(const GemmArgs& g, hipStream_t s);
 
 // A validated attention request.
 struct AttnArgs {

@@ -102,9 +102,47 @@ def test_accumulate_into_c(in_dt, out_dt):
     check(decode(c), ref, in_dt, out_dt)
 
 
+SKINNY = [(1, 64, 64), (16, 16, 8), (17, 40, 72), (48, 24, 200), (64, 4096, 512), (100, 136, 1000),
+          (128, 256, 64), (128, 8200, 96)]
+
+
+@pytest.mark.parametrize("in_dt,out_dt", [(torch.bfloat16, torch.bfloat16),
+                                          (torch.bfloat16, torch.float32),
+                                          (torch.float16, torch.float16)],
+                         ids=lambda x: str(x).replace("torch.", ""))
+@pytest.mark.parametrize("m,n,k", SKINNY)
+def test_small_m_kernel(m, n, k, in_dt, out_dt):
+    # M <= 128 with K-contiguous operands runs the skinny kernel: ragged N
+    # (partial last tile), K tails below one 32-element step, wide N.
+    print(f"case skinny m={m} n={n} k={k} {in_dt}->{out_dt}", flush=True)
+    a, b, _, _ = make_operands(m, n, k, in_dt, False, True, seed=m + n + k)
+    c = torch.zeros(m, n, dtype=out_dt, device="cuda")
+    rt.gemm(a, b, c, trans_b=True)
+    torch.cuda.synchronize()
+    check(decode(c), reference(a, b, False, True, 1.0, 1.0), in_dt, out_dt)
+    c0 = randn((m, n), 3).to(out_dt)
+    c = c0.clone()
+    rt.gemm(a, b, c, trans_b=True, clear_accum=False)
+    torch.cuda.synchronize()
+    check(decode(c), reference(a, b, False, True, 1.0, 1.0) + decode(c0), in_dt, out_dt)
+
+
+@pytest.mark.parametrize("m,n,k", [(1024, 4096, 4096), (512, 640, 1000), (300, 1000, 72)])
+def test_mid_size_tiles(m, n, k):
+    # Fewer than 128 tiles of 256x256: the 128x128-tile configuration.
+    print(f"case mid m={m} n={n} k={k}", flush=True)
+    a, b, _, _ = make_operands(m, n, k, torch.bfloat16, False, True, seed=9)
+    c = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+    rt.gemm(a, b, c, trans_b=True)
+    torch.cuda.synchronize()
+    check(decode(c), reference(a, b, False, True, 1.0, 1.0), torch.bfloat16, torch.bfloat16)
+
+
 def test_sentinel_guards_and_unchanged_inputs():
-    m, n, k = 300, 264, 136
-    for dt, odt in [(torch.bfloat16, torch.bfloat16), (torch.int8, torch.int32)]:
+    for (m, n, k), dt, odt in [((300, 264, 136), torch.bfloat16, torch.bfloat16),
+                               ((300, 264, 136), torch.int8, torch.int32),
+                               ((100, 136, 1000), torch.bfloat16, torch.bfloat16),
+                               ((2048, 2048, 256), torch.bfloat16, torch.float32)]:
         a, b, _, _ = make_operands(m, n, k, dt, False, True, seed=11)
         a0, b0 = a.clone(), b.clone()
         gc = Guarded((m, n), odt)
