@@ -1,8 +1,12 @@
-"""Ahead-of-time build of libfrisk_hip.so (the C-ABI of include/frisk_hip.h).
+"""Ahead-of-time build of the package's native parts.
 
-Every .hip file under csrc/ is compiled for gfx950 with hipcc and linked into
-one shared library placed next to this file, so it travels with the source
-tree.  Invoked by __graft_entry__.build() and by `python -m frisk_amd.build`.
+* libfrisk_hip.so, the C-ABI of include/frisk_hip.h: every .hip file under
+  csrc/ compiled for gfx950 with hipcc and linked into one shared library.
+* frisk_ffi (Python extension), the tile-IR builder: the C++ sources under
+  ir/ compiled with g++ against pybind11 (host code only).
+
+Both land next to this file, so they travel with the source tree.  Invoked
+by __graft_entry__.build() and by `python -m frisk_amd.build`.
 """
 from __future__ import annotations
 
@@ -10,13 +14,17 @@ import os
 import shlex
 import subprocess
 import sys
+import sysconfig
 from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
+IRSRC = HERE / "ir"
 LIB = HERE / "libfrisk_hip.so"
+FFI = HERE / ("frisk_ffi" + sysconfig.get_config_var("EXT_SUFFIX"))
 ARCH = "gfx950"
+CXX = os.environ.get("CXX", "g++")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 COMMON = [
@@ -63,5 +71,41 @@ def build(verbose: bool = False, extra: list[str] | None = None) -> Path:
     return LIB
 
 
+def build_ffi(verbose: bool = False) -> Path:
+    """Compile the pybind11 tile-IR module (host C++ only)."""
+    import pybind11
+    objdir = HERE / "_build" / "ir"
+    objdir.mkdir(parents=True, exist_ok=True)
+    flags = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-fvisibility=hidden",
+             f"-I{pybind11.get_include()}", f"-I{sysconfig.get_paths()['include']}"]
+
+    def compile_one(src: Path) -> Path:
+        obj = objdir / (src.stem + ".o")
+        cmd = [CXX, *flags, "-c", str(src), "-o", str(obj)]
+        if verbose:
+            print(" ".join(shlex.quote(c) for c in cmd), flush=True)
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"{CXX} failed on {src.name}:\n{r.stdout}\n{r.stderr}")
+        return obj
+
+    with ThreadPoolExecutor(max_workers=min(8, os.cpu_count() or 1)) as ex:
+        objs = list(ex.map(compile_one, sorted(IRSRC.glob("*.cpp"))))
+    tmp = FFI.with_name(FFI.name + ".tmp")
+    r = subprocess.run([CXX, "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)],
+                       capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link of frisk_ffi failed:\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, FFI)
+    return FFI
+
+
+def build_all(verbose: bool = False) -> list[Path]:
+    return [build(verbose), build_ffi(verbose)]
+
+
 if __name__ == "__main__":
-    print(build(verbose="-v" in sys.argv))
+    if "--ffi" in sys.argv:
+        print(build_ffi(verbose="-v" in sys.argv))
+    else:
+        print(build_all(verbose="-v" in sys.argv))

@@ -179,4 +179,16 @@ int frisk_attn_fwd(const frisk_attn_desc* d, void* stream) {
   return FRISK_OK;
 }
 
+int frisk_probe_mfma_layout(int atom, float* out, int64_t out_floats, void* stream) {
+  const int need = frisk::mfma_probe_floats(atom);
+  if (need == 0) return fail(FRISK_EINVAL, "mfma-probe: unknown atom %d (0, 1 or 2)", atom);
+  if (!out) return fail(FRISK_EINVAL, "mfma-probe: null output");
+  if (out_floats < need)
+    return fail(FRISK_EINVAL, "mfma-probe: atom %d writes %d floats, buffer holds %lld", atom, need,
+                (long long)out_floats);
+  hipError_t e = frisk::mfma_layout_probe(atom, out, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "mfma-probe launch");
+  return FRISK_OK;
+}
+
 }  // extern "C"

@@ -57,4 +57,10 @@ struct AttnArgs {
 
 hipError_t attn_fwd_d128(const AttnArgs& a, hipStream_t s);
 
+// MFMA fragment-layout probe (probe.hip): atom 0 = bf16 32x32x16,
+// 1 = bf16 16x16x32, 2 = i8 32x32x32; `out` holds mfma_probe_floats(atom)
+// floats.
+int mfma_probe_floats(int atom);
+hipError_t mfma_layout_probe(int atom, float* out, hipStream_t stream);
+
 }  // namespace frisk

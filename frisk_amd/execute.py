@@ -1,0 +1,472 @@
+"""Run a frisk tile program on the GPU through the C-ABI.
+
+The reference has no in-process execution (ffi/ffi.cpp:6 leaves it out; its
+programs run out of process through an exported packet).  Here
+`execute(module, kernel, tensors)` recognises the two tile programs of the
+GEMM / attention path, proves from the IR that the program computes the
+whole-tensor operation, and launches the MI355X kernel for it:
+
+* GEMM (`frisk_gemm`), in two forms:
+  - whole-matrix: the kernel body is `frisk.gemm(A, B, C)` on kernel
+    arguments, optionally preceded by `frisk.fill(C, 0)`;
+  - tiled (the tile program of the reference's tmp/ir.mlir:2-16): one
+    2-D `frisk.parallel` over (M/BM, N/BN) tiles holding a zero-filled Local
+    accumulator, a `frisk.for` over K/BK whose body copies the A and B tiles
+    into Shared buffers and accumulates `frisk.gemm` into the accumulator,
+    and a final copy of the accumulator into C.  The copy index maps must be
+    affine in the loop indices and place the tiles so that the grid covers
+    C exactly once and the loop covers K exactly once (checked below).
+* Attention (`frisk_attn_fwd`): the online-softmax skeleton of
+  tmp/ir.mlir:89-157 expressed with the builder's ops: a 3-D
+  `frisk.parallel` over (B, H, S/BM) that copies the Q tile, fills the
+  output accumulator (0), the row maxima (-inf) and row sums (0), loops over
+  key blocks copying the K tile, forming scores with `frisk.gemm(q, k, s)`,
+  reducing them into the row maxima (max) and sums (add), casting them to
+  the input dtype, copying the V tile and accumulating `frisk.gemm(p, v,
+  o)`, and finally copies the accumulator into O.  The rescaling steps the
+  builder cannot express (exp2 of scaled scores, accumulator rescale and the
+  final division) are implied by that skeleton; `frisk.block` ops standing
+  for them are allowed in the loop.  `sm_scale` (default 1/sqrt(D)) and
+  `causal` are arguments of execute().
+
+The tile sizes and thread counts of a program describe the computation, not
+the launch: the MI355X kernels choose their own tiling.  Anything else raises
+ValueError naming the first mismatch.  There is no CPU fallback.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Optional, Sequence
+
+from . import _ir
+
+ir = _ir()
+fr = ir.frisk
+
+
+@dataclass
+class GemmPlan:
+    a: int
+    b: int
+    c: int
+    trans_a: bool
+    trans_b: bool
+    clear_accum: bool
+    m: int
+    n: int
+    k: int
+
+
+@dataclass
+class AttnPlan:
+    q: int
+    k: int
+    v: int
+    o: int
+    k_transposed: bool
+    batch: int
+    heads: int
+    seq: int
+    head_dim: int
+
+
+class _Reject(ValueError):
+    pass
+
+
+def _fail(msg: str):
+    raise _Reject(msg)
+
+
+def _body_ops(block) -> list:
+    return [op for op in block.get_operations() if op.get_name() != "frisk.end"]
+
+
+def _arg_index(value, entry) -> Optional[int]:
+    owner = getattr(value, "get_owner", None)
+    if owner is None:
+        return None
+    if value.get_owner().id() != entry.id():
+        return None
+    return value.get_arg_number()
+
+
+def _shape(value):
+    return list(value.get_type().get_shape())
+
+
+def _elem(value):
+    return str(value.get_type().get_element_ty())
+
+
+def _space(value):
+    return value.get_type().get_memory_space()
+
+
+# ---------------------------------------------------------------------------
+# Affine index analysis
+# ---------------------------------------------------------------------------
+class _Ivs:
+    """Loop indices in scope: parallel ivs range over [0, grid), the for iv
+    over lower, lower + step, ... < upper."""
+
+    def __init__(self):
+        self.ranges = {}  # (block id, arg number) -> list of values (first, next, last)
+
+    def add_parallel(self, par):
+        block = par.get_region(0).front()
+        for i, extent in enumerate(par.get_grid()):
+            self.ranges[(block.id(), i)] = (0, 1, extent)
+        return block
+
+    def add_for(self, loop):
+        block = loop.get_region(0).front()
+        lo, hi, st = loop.get_lower_bound(), loop.get_upper_bound(), loop.get_step()
+        if st <= 0 or hi <= lo:
+            _fail(f"frisk.for {lo} to {hi} step {st} is empty or has a non-positive step")
+        self.ranges[(block.id(), 0)] = (lo, st, (hi - lo + st - 1) // st)
+        return block
+
+    def key(self, value):
+        if not hasattr(value, "get_owner"):
+            _fail("copy indices must be loop induction variables")
+        k = (value.get_owner().id(), value.get_arg_number())
+        if k not in self.ranges:
+            _fail("copy index is not a parallel or for induction variable in scope")
+        return k
+
+
+def _origin(ivs: _Ivs, amap, indices, rank: int) -> tuple[list[int], dict]:
+    """Affine form of a copy's tile origin: (constant vector, {iv: coefficient
+    vector per trip}), coefficients per trip of the loop (step applied).  An
+    empty map (whole-buffer copy) is the origin 0."""
+    if amap.get_num_results() == 0:
+        return [0] * rank, {}
+    if amap.get_num_results() != rank:
+        _fail(f"copy map {amap} must give one offset per dimension ({rank})")
+    if amap.get_num_symbols():
+        _fail("copy maps with symbols are not supported")
+    for e in amap.get_results():
+        if not e.is_pure_affine():
+            _fail(f"copy map result {e} is not pure affine")
+    keys = [ivs.key(v) for v in indices]
+    base = [ivs.ranges[k][0] for k in keys]
+    c0 = amap.evaluate(base)
+    coef = {}
+    for k in set(keys):
+        step = ivs.ranges[k][1]
+        pt = [b + (step if keys[i] == k else 0) for i, b in enumerate(base)]
+        d = [x - y for x, y in zip(amap.evaluate(pt), c0)]
+        if any(d):
+            coef[k] = d
+    return c0, coef
+
+
+def _tile_copy(op, ivs: _Ivs):
+    """(src, dst, src origin affine form, dst origin affine form, extents) of a copy."""
+    cp = fr.CopyOp.from_operation(op)
+    src, dst = cp.get_src_memref(), cp.get_dst_memref()
+    so = _origin(ivs, cp.get_src_affine_map(), list(cp.get_src_indices()), len(_shape(src)))
+    do = _origin(ivs, cp.get_dst_affine_map(), list(cp.get_dst_indices()), len(_shape(dst)))
+    return src, dst, so, do, list(cp.get_src_extents()), list(cp.get_dst_extents())
+
+
+# ---------------------------------------------------------------------------
+# GEMM
+# ---------------------------------------------------------------------------
+def _gemm_whole(ops, entry) -> GemmPlan:
+    fill_c = None
+    if len(ops) == 2 and ops[0].get_name() == "frisk.fill":
+        fill_c = ops[0]
+        ops = ops[1:]
+    if len(ops) != 1 or ops[0].get_name() != "frisk.gemm":
+        _fail("not a whole-matrix GEMM")
+    g = fr.GemmOp.from_operation(ops[0])
+    idx = [_arg_index(v, entry) for v in (g.get_matrix_A(), g.get_matrix_B(), g.get_matrix_C())]
+    if None in idx:
+        _fail("whole-matrix GEMM operands must be kernel arguments")
+    op = ops[0]
+    clear = bool(op.get_attr("clear_accum"))
+    if fill_c is not None:
+        if fill_c.get_operand(0) != g.get_matrix_C() or fill_c.get_attr("value") != 0.0:
+            _fail("only a zero fill of C may precede the GEMM")
+        clear = True
+    return GemmPlan(idx[0], idx[1], idx[2], bool(op.get_attr("transA")), bool(op.get_attr("transB")),
+                    clear, op.get_attr("M"), op.get_attr("N"), op.get_attr("K"))
+
+
+def _gemm_tiled(ops, entry) -> GemmPlan:
+    if len(ops) != 1 or ops[0].get_name() != "frisk.parallel":
+        _fail("not a tiled GEMM (expected one frisk.parallel)")
+    par = fr.ParallelOp.from_operation(ops[0])
+    grid = par.get_grid()
+    if len(grid) != 2:
+        _fail("tiled GEMM needs a 2-D parallel grid")
+    ivs = _Ivs()
+    pblock = ivs.add_parallel(par)
+    body = _body_ops(pblock)
+    allocs = {}
+    i = 0
+    while i < len(body) and body[i].get_name() == "frisk.alloc_buffer":
+        allocs[body[i].get_result(0).id()] = body[i].get_result(0)
+        i += 1
+    rest = body[i:]
+    names = [o.get_name() for o in rest]
+    if names != ["frisk.fill", "frisk.for", "frisk.copy"]:
+        _fail(f"tiled GEMM body must be allocs, fill, for, copy (found {names})")
+    fill, loop_op, store = rest
+    acc = fill.get_operand(0)
+    if acc.id() not in allocs or _space(acc) != ir.MemorySpace.LOCAL or fill.get_attr("value") != 0.0:
+        _fail("the accumulator must be a zero-filled Local buffer")
+    loop = fr.ForOp.from_operation(loop_op)
+    lblock = ivs.add_for(loop)
+    lops = _body_ops(lblock)
+    if sorted(o.get_name() for o in lops) != ["frisk.copy", "frisk.copy", "frisk.gemm"] or \
+            lops[-1].get_name() != "frisk.gemm":
+        _fail("the K loop must copy the A and B tiles, then accumulate one frisk.gemm")
+    gop = lops[-1]
+    g = fr.GemmOp.from_operation(gop)
+    a_t, b_t, c_t = g.get_matrix_A(), g.get_matrix_B(), g.get_matrix_C()
+    if c_t != acc or gop.get_attr("clear_accum"):
+        _fail("the loop GEMM must accumulate (clear_accum = false) into the filled accumulator")
+    ta, tb = bool(gop.get_attr("transA")), bool(gop.get_attr("transB"))
+    bm, bn, bk = gop.get_attr("M"), gop.get_attr("N"), gop.get_attr("K")
+    loads = {}
+    for cop in lops[:2]:
+        src, dst, so, do, sext, dext = _tile_copy(cop, ivs)
+        if dst.id() not in allocs or do[1] or any(do[0]):
+            _fail("tile loads must fill a whole Shared/Local tile buffer")
+        loads[dst.id()] = (src, so, sext)
+    if a_t.id() not in loads or b_t.id() not in loads:
+        _fail("the GEMM operands must be the tiles loaded in the loop")
+    a_src, a_org, a_ext = loads[a_t.id()]
+    b_src, b_org, b_ext = loads[b_t.id()]
+    ia, ib = _arg_index(a_src, entry), _arg_index(b_src, entry)
+    if ia is None or ib is None:
+        _fail("tiles must be loaded from kernel arguments")
+    src, dst, so, do, sext, dext = _tile_copy(store, ivs)
+    ic = _arg_index(dst, entry)
+    if src != acc or ic is None or so[1] or any(so[0]):
+        _fail("the accumulator must be stored into a kernel argument")
+    if sext != [bm, bn] or dext != [bm, bn]:
+        _fail(f"the C store must copy a {bm}x{bn} tile (extents {sext} / {dext})")
+
+    kkey = (lblock.id(), 0)
+    trips = ivs.ranges[kkey][2]
+    pkeys = [(pblock.id(), 0), (pblock.id(), 1)]
+    # Positions of (M, K) in A's storage and (K, N) in B's.
+    am, ak = (1, 0) if ta else (0, 1)
+    bk_, bn_ = (1, 0) if tb else (0, 1)
+
+    def per_trip(org, dim, key):
+        return org[1].get(key, [0, 0])[dim]
+
+    a0, b0, c0 = a_org[0], b_org[0], do[0]
+    # K tiles: A and B advance by BK per trip from 0, and nothing else moves K.
+    for name, org, kd in (("A", a_org, ak), ("B", b_org, bk_)):
+        if org[0][kd] != 0 or per_trip(org, kd, kkey) != bk:
+            _fail(f"{name} tile K offset must start at 0 and advance by {bk} per trip")
+        if any(per_trip(org, kd, p) for p in pkeys):
+            _fail(f"{name} tile K offset must not depend on the grid")
+    # M and N tiles: one grid axis each, stride BM / BN, never the K loop.
+    m_axes = [p for p in pkeys if per_trip(a_org, am, p)]
+    n_axes = [p for p in pkeys if per_trip(b_org, bn_, p)]
+    if len(m_axes) != 1 or len(n_axes) != 1 or m_axes == n_axes:
+        _fail("A's M offset and B's N offset must each follow a different grid axis")
+    pm, pn = m_axes[0], n_axes[0]
+    if a0[am] != 0 or per_trip(a_org, am, pm) != bm or per_trip(a_org, am, kkey):
+        _fail(f"A tile M offset must be {bm} * grid index")
+    if b0[bn_] != 0 or per_trip(b_org, bn_, pn) != bn or per_trip(b_org, bn_, kkey):
+        _fail(f"B tile N offset must be {bn} * grid index")
+    if c0 != [0, 0] or per_trip(do, 0, pm) != bm or per_trip(do, 1, pn) != bn or \
+            per_trip(do, 0, pn) or per_trip(do, 1, pm) or kkey in do[1]:
+        _fail("C tile origin must be (BM * m-index, BN * n-index)")
+    a_shape, b_shape, c_shape = _shape(a_src), _shape(b_src), _shape(dst)
+    M, K = (a_shape[1], a_shape[0]) if ta else (a_shape[0], a_shape[1])
+    N = b_shape[0] if tb else b_shape[1]
+    gm, gn = grid[pm[1]], grid[pn[1]]
+    if gm * bm != M or gn * bn != N or trips * bk != K or c_shape != [M, N]:
+        _fail(f"grid {grid} x tile {bm}x{bn}x{bk} x {trips} trips does not cover "
+              f"A{a_shape} B{b_shape} C{c_shape} exactly")
+    if _elem(a_t) != _elem(a_src) or _elem(b_t) != _elem(b_src):
+        _fail("A/B tiles must keep the input dtype")
+    return GemmPlan(ia, ib, ic, ta, tb, True, M, N, K)
+
+
+# ---------------------------------------------------------------------------
+# Attention
+# ---------------------------------------------------------------------------
+def _attention(ops, entry) -> AttnPlan:
+    if len(ops) != 1 or ops[0].get_name() != "frisk.parallel":
+        _fail("not an attention program (expected one frisk.parallel)")
+    par = fr.ParallelOp.from_operation(ops[0])
+    grid = par.get_grid()
+    if len(grid) != 3:
+        _fail("attention needs a 3-D (batch, heads, query blocks) grid")
+    ivs = _Ivs()
+    pblock = ivs.add_parallel(par)
+    pk = [(pblock.id(), i) for i in range(3)]
+    body = _body_ops(pblock)
+    allocs = {o.get_result(0).id(): o.get_result(0) for o in body if o.get_name() == "frisk.alloc_buffer"}
+    rest = [o for o in body if o.get_name() not in ("frisk.alloc_buffer", "arith.constant")]
+    loops = [o for o in rest if o.get_name() == "frisk.for"]
+    if len(loops) != 1:
+        _fail("attention needs exactly one key-block loop")
+    li = rest.index(loops[0])
+    pre, post = rest[:li], rest[li + 1:]
+    loop = fr.ForOp.from_operation(loops[0])
+    lblock = ivs.add_for(loop)
+    kkey = (lblock.id(), 0)
+    lops = [o for o in _body_ops(lblock) if o.get_name() != "frisk.block"]
+
+    # Prologue: the Q tile load and the accumulator / statistics fills.
+    q_load = [o for o in pre if o.get_name() == "frisk.copy"]
+    fills = {o.get_operand(0).id(): o.get_attr("value") for o in pre if o.get_name() == "frisk.fill"}
+    if len(q_load) != 1 or len(pre) != 1 + len(fills):
+        _fail("attention prologue must be the Q tile copy and fills")
+    q_src, q_buf, q_org, q_do, _, _ = _tile_copy(q_load[0], ivs)
+
+    gemms = [o for o in lops if o.get_name() == "frisk.gemm"]
+    if len(gemms) != 2:
+        _fail("the key-block loop must hold the score GEMM and the PV GEMM")
+    g_s, g_o = (fr.GemmOp.from_operation(g) for g in gemms)
+    s_acc, o_acc = g_s.get_matrix_C(), g_o.get_matrix_C()
+    if g_s.get_matrix_A() != q_buf:
+        _fail("the score GEMM must read the Q tile")
+    if not gemms[0].get_attr("clear_accum") and fills.get(s_acc.id()) is None:
+        _fail("scores must be cleared each key block")
+    if gemms[1].get_attr("clear_accum") or fills.get(o_acc.id()) != 0.0:
+        _fail("the output accumulator must be zero-filled once and accumulated")
+    k_buf, k_trans = g_s.get_matrix_B(), not bool(gemms[0].get_attr("transB"))
+    reds = [fr.ReduceOp.from_operation(o) for o in lops if o.get_name() == "frisk.reduce"]
+    kinds = sorted(o.get_attr("kind") for o in lops if o.get_name() == "frisk.reduce")
+    if kinds not in (["max"], ["add", "max"]):
+        _fail("scores must be reduced by max (and optionally add) along the key axis")
+    for r, o in zip(reds, [o for o in lops if o.get_name() == "frisk.reduce"]):
+        if r.get_src_memref() != s_acc or r.get_reduce_dim() != 1 or o.get_attr("clear"):
+            _fail("row statistics must merge the scores along dim 1 (clear = false)")
+        init = fills.get(r.get_dst_memref().id())
+        if init != (-math.inf if o.get_attr("kind") == "max" else 0.0):
+            _fail("row maxima must start at -inf and row sums at 0")
+    copies = [o for o in lops if o.get_name() == "frisk.copy"]
+    p_buf = g_o.get_matrix_A()
+    loads = {}
+    cast_ok = False
+    for cop in copies:
+        src, dst, so, do, sext, dext = _tile_copy(cop, ivs)
+        if src == s_acc and dst == p_buf:
+            cast_ok = True
+        else:
+            loads[dst.id()] = (src, so)
+    if not cast_ok:
+        _fail("scores must be cast into the PV GEMM's P operand")
+    if k_buf.id() not in loads or g_o.get_matrix_B().id() not in loads:
+        _fail("K and V tiles must be loaded in the key-block loop")
+    k_src, k_org = loads[k_buf.id()]
+    v_src, v_org = loads[g_o.get_matrix_B().id()]
+    # Epilogue: accumulator -> (optional Shared staging) -> O.
+    src, dst, so, o_org, _, oext = _tile_copy(post[-1], ivs)
+    stage = [o for o in post[:-1] if o.get_name() == "frisk.copy"]
+    if len(post) - 1 != len(stage) or len(stage) > 1:
+        _fail("attention epilogue must copy the accumulator into O")
+    if stage:
+        s_src, s_dst, *_ = _tile_copy(stage[0], ivs)
+        if s_src != o_acc or s_dst != src:
+            _fail("the staged epilogue must copy the accumulator into the staging tile")
+    elif src != o_acc:
+        _fail("the epilogue must store the output accumulator")
+    idx = [_arg_index(v, entry) for v in (q_src, k_src, v_src, dst)]
+    if None in idx:
+        _fail("Q, K, V and O must be kernel arguments")
+    shape = _shape(q_src)
+    if len(shape) != 4:
+        _fail("Q/K/V/O must be rank-4 [batch, heads, seq, head_dim] memrefs")
+    B, H, S, D = shape
+    bm = _shape(q_buf)[0]
+    bn = _shape(s_acc)[1]
+    k_shape = _shape(k_src)
+    if k_shape != ([B, H, D, S] if k_trans else [B, H, S, D]) or _shape(v_src) != shape or \
+            _shape(dst) != shape:
+        _fail("K/V/O shapes disagree with Q")
+
+    def check(org, seq_dim, per_trip_key, stride, name):
+        c0, coef = org
+        want = {pk[0]: [1 if d == 0 else 0 for d in range(4)],
+                pk[1]: [1 if d == 1 else 0 for d in range(4)]}
+        if c0 != [0, 0, 0, 0]:
+            _fail(f"{name} tile origin must start at 0")
+        for key in (pk[0], pk[1]):
+            if coef.get(key) != want[key]:
+                _fail(f"{name} tile must follow the batch and head grid axes")
+        seq = coef.get(per_trip_key, [0] * 4)
+        if seq != [stride if d == seq_dim else 0 for d in range(4)]:
+            _fail(f"{name} tile sequence offset must advance by {stride}")
+        others = set(coef) - {pk[0], pk[1], per_trip_key}
+        if others:
+            _fail(f"{name} tile depends on an unexpected index")
+
+    check(q_org, 2, pk[2], bm, "Q")
+    check(o_org, 2, pk[2], bm, "O")
+    check(k_org, 3 if k_trans else 2, kkey, bn, "K")
+    check(v_org, 2, kkey, bn, "V")
+    if grid != [B, H, S // bm] or S % bm or ivs.ranges[kkey][2] * bn != S:
+        _fail(f"grid {grid} / key loop do not cover B={B} H={H} S={S}")
+    return AttnPlan(*idx, k_trans, B, H, S, D)
+
+
+# ---------------------------------------------------------------------------
+def plan(module, kernel: str):
+    """Recognise kernel `kernel` of `module`: a GemmPlan or an AttnPlan."""
+    k = module.get_kernel(kernel)
+    if k is None:
+        raise ValueError(f"execute: module has no kernel @{kernel}")
+    if not k.verify():
+        raise ValueError(f"execute: kernel @{kernel} does not verify: {k.verify_diagnostic()}")
+    entry = k.get_region(0).front()
+    ops = _body_ops(entry)
+    reasons = []
+    for recognise in (_gemm_whole, _gemm_tiled, _attention):
+        try:
+            return recognise(ops, entry)
+        except _Reject as e:
+            reasons.append(f"{recognise.__name__.lstrip('_')}: {e}")
+    raise ValueError(f"execute: kernel @{kernel} is not a recognised GEMM or attention tile program ("
+                     + "; ".join(reasons) + ")")
+
+
+_TORCH_DTYPES = {"f16": "float16", "bf16": "bfloat16", "f32": "float32", "f8E4M3FN": "float8_e4m3fn",
+                 "i8": "int8", "i32": "int32"}
+
+
+def _check_tensor(t, value, name):
+    import torch
+    shape = _shape(value)
+    want = _TORCH_DTYPES.get(_elem(value))
+    if want is None or t.dtype != getattr(torch, want):
+        raise ValueError(f"execute: {name} must be {_elem(value)} (got {t.dtype})")
+    if list(t.shape) != shape:
+        raise ValueError(f"execute: {name} must have shape {shape} (got {list(t.shape)})")
+    if not t.is_cuda:
+        raise ValueError(f"execute: {name} must be a device tensor")
+
+
+def execute(module, kernel: str, tensors: Sequence, *, stream=None, causal: bool = False,
+            sm_scale: Optional[float] = None, scale_a: float = 1.0, scale_b: float = 1.0):
+    """Run kernel `kernel` of `module` on `tensors` (one per kernel argument)."""
+    from . import runtime as rt
+    p = plan(module, kernel)
+    k = module.get_kernel(kernel)
+    args = [k.arg(i) for i in range(k.get_num_arguments())]
+    if len(tensors) != len(args):
+        raise ValueError(f"execute: @{kernel} takes {len(args)} tensors, got {len(tensors)}")
+    for i, (t, a) in enumerate(zip(tensors, args)):
+        _check_tensor(t, a, f"argument {i}")
+    if isinstance(p, GemmPlan):
+        return rt.gemm(tensors[p.a], tensors[p.b], tensors[p.c], trans_a=p.trans_a, trans_b=p.trans_b,
+                       clear_accum=p.clear_accum, scale_a=scale_a, scale_b=scale_b, stream=stream)
+    q, kk, v, o = (tensors[i] for i in (p.q, p.k, p.v, p.o))
+    if p.k_transposed:
+        kk = kk.transpose(-1, -2)  # [B, H, S, D] view; the C-ABI needs unit D stride
+        kk = kk.contiguous()
+    return rt.attn_fwd(q, kk, v, o, causal=causal, sm_scale=sm_scale, stream=stream)

@@ -20,7 +20,8 @@ OK, EINVAL, EUNSUP, EHIP = 0, -1, -2, -3
 DTYPE_NAMES = {F32: "f32", F16: "f16", BF16: "bf16", E4M3: "e4m3", I8: "i8", I32: "i32", F64: "f64"}
 
 # Exported symbols declared by include/frisk_hip.h.
-EXPORTS = ("frisk_gemm", "frisk_attn_fwd", "frisk_last_error", "frisk_abi_version")
+EXPORTS = ("frisk_gemm", "frisk_attn_fwd", "frisk_last_error", "frisk_abi_version",
+           "frisk_probe_mfma_layout")
 ABI_VERSION = 1
 
 
@@ -75,6 +76,9 @@ def load() -> ctypes.CDLL:
     lib.frisk_last_error.restype = ctypes.c_char_p
     lib.frisk_abi_version.argtypes = []
     lib.frisk_abi_version.restype = ctypes.c_int
+    lib.frisk_probe_mfma_layout.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_int64,
+                                            ctypes.c_void_p]
+    lib.frisk_probe_mfma_layout.restype = ctypes.c_int
     if lib.frisk_abi_version() != ABI_VERSION:
         raise RuntimeError("libfrisk_hip.so ABI version mismatch; rebuild it")
     _lib = lib
@@ -141,6 +145,23 @@ def gemm(a, b, c, *, trans_a=False, trans_b=False, clear_accum=True,
     _check(load().frisk_gemm(ctypes.byref(d), ctypes.c_void_p(_stream_handle(stream))),
            "frisk_gemm")
     return c
+
+
+# Atom codes of frisk_probe_mfma_layout: (mfma name, K, accumulators per lane, S).
+PROBE_ATOMS = {0: ("v_mfma_f32_32x32x16_bf16", 16, 16, 64),
+               1: ("v_mfma_f32_16x16x32_bf16", 32, 4, 64),
+               2: ("v_mfma_i32_32x32x32_i8", 32, 16, 32)}
+
+
+def probe_mfma_layout(atom: int, out, stream=None):
+    """Run the MFMA layout probe into the f32 device tensor `out`."""
+    if out.dtype.is_floating_point is False or out.element_size() != 4 or not out.is_contiguous() \
+            or not out.is_cuda:
+        raise ValueError("out must be a contiguous f32 device tensor")
+    _check(load().frisk_probe_mfma_layout(int(atom), ctypes.c_void_p(out.data_ptr()), out.numel(),
+                                          ctypes.c_void_p(_stream_handle(stream))),
+           "frisk_probe_mfma_layout")
+    return out
 
 
 def attn_desc(q, k, v, o, *, causal=False, sm_scale=None, lse=None) -> AttnDesc:

@@ -121,6 +121,18 @@ const char* frisk_last_error(void);
 /* FRISK_ABI_VERSION of the loaded library. */
 int frisk_abi_version(void);
 
+/* MFMA fragment-layout probe.  No counterpart in the reference, whose SM90
+ * fragment maps are pinned by golden rows (SM90MmaLayoutProofTest.cpp:10-82);
+ * this one pins the CDNA4 maps the kernels use on the device itself.  Runs
+ * one atom (0 = v_mfma_f32_32x32x16_bf16, 1 = v_mfma_f32_16x16x32_bf16,
+ * 2 = v_mfma_i32_32x32x32_i8) for every k0 in [0, K) on operands with
+ * A[i][k0] = i, A[i][k0+1] = S, B[k0][j] = 1, B[k0+1][j] = j (S = 64, or 32
+ * for i8) and writes accumulator register r of lane L for k0 to
+ * out[(k0 * 64 + L) * R + r] (R = 16, 4, 16), i.e. the value i + S j of the
+ * element it holds.  `out` is a device buffer of at least K * 64 * R floats
+ * (16384, 8192 and 32768). */
+int frisk_probe_mfma_layout(int atom, float* out, int64_t out_floats, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

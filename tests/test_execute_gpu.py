@@ -1,0 +1,75 @@
+"""execute(): frisk tile programs built with the builder API, run on the GPU
+through the C-ABI and checked against the fp64 oracle (tolerances as in the
+GEMM / attention parity tests)."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import frisk_amd as F
+from oracle import attention as A
+from oracle import gemm as G
+from tests import programs as P
+from tests.gpu_util import decode, randn
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
+@pytest.mark.parametrize("dtype,out", [("bf16", "bf16"), ("fp16", "fp32")])
+def test_execute_tiled_gemm(ta, tb, dtype, out):
+    M, N, K = 512, 384, 640
+    print(f"execute tiled gemm {dtype}->{out} ta={ta} tb={tb}", flush=True)
+    s, _ = P.tiled_gemm(M, N, K, BM=128, BN=128, BK=64, dtype=dtype, out=out, trans_a=ta, trans_b=tb)
+    tdt = {"bf16": torch.bfloat16, "fp16": torch.float16, "fp32": torch.float32}
+    a = randn((K, M) if ta else (M, K), 11).to(tdt[dtype])
+    b = randn((N, K) if tb else (K, N), 12).to(tdt[dtype])
+    c = torch.full((M, N), float("nan"), dtype=tdt[out], device="cuda")
+    F.execute(s.module, "matmul", [a, b, c])
+    torch.cuda.synchronize()
+    A_ = decode(a).T if ta else decode(a)
+    B_ = decode(b).T if tb else decode(b)
+    err = G.row_scaled_error(decode(c), A_ @ B_)
+    assert err <= (1e-2 if out != "fp32" else 1e-5), err
+
+
+def test_execute_whole_gemm_accumulates():
+    M, N, K = 256, 256, 128
+    s, _ = P.whole_gemm(M, N, K, dtype="bf16", out="fp32", clear=False)
+    a = randn((M, K), 3).to(torch.bfloat16)
+    b = randn((K, N), 4).to(torch.bfloat16)
+    c0 = randn((M, N), 5)
+    c = c0.clone()
+    F.execute(s.module, "gemm", [a, b, c])
+    torch.cuda.synchronize()
+    ref = decode(a) @ decode(b) + c0.double().cpu().numpy()
+    assert G.row_scaled_error(decode(c), ref) <= 1e-5
+
+
+@pytest.mark.parametrize("k_transposed", [False, True])
+@pytest.mark.parametrize("causal", [False, True])
+def test_execute_attention(k_transposed, causal):
+    Bt, H, S, D = 1, 2, 256, 128
+    print(f"execute attention k_transposed={k_transposed} causal={causal}", flush=True)
+    s, _ = P.attention(Bt, H, S, D, k_transposed=k_transposed)
+    q = randn((Bt, H, S, D), 21).to(torch.bfloat16)
+    k = randn((Bt, H, S, D), 22).to(torch.bfloat16)
+    v = randn((Bt, H, S, D), 23).to(torch.bfloat16)
+    o = torch.full_like(q, float("nan"))
+    k_arg = k.transpose(-1, -2).contiguous() if k_transposed else k
+    F.execute(s.module, "attention", [q, k_arg, v, o], causal=causal)
+    torch.cuda.synchronize()
+    ro, _ = A.attention_fp64(decode(q), decode(k), decode(v), causal=causal, scale=1 / math.sqrt(D))
+    assert G.row_scaled_error(decode(o), ro) <= 1e-2
+
+
+def test_execute_checks_tensors():
+    s, _ = P.whole_gemm(64, 64, 64)
+    a = torch.zeros(64, 64, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ValueError, match="must be bf16"):
+        F.execute(s.module, "gemm", [a, a, torch.zeros(64, 64, device="cuda")])
+    with pytest.raises(ValueError, match="takes 3 tensors"):
+        F.execute(s.module, "gemm", [a, a])
+    with pytest.raises(ValueError, match="no kernel"):
+        F.execute(s.module, "nope", [a, a, a])
