@@ -46,7 +46,7 @@ def __getattr__(name: str):
         from .common import utils
         return getattr(utils, name)
     if name == "execute":
-        from .execute import execute
+        from .executor import execute
         return execute
     if name.startswith("__") or name == "frisk_ffi":
         raise AttributeError(name)

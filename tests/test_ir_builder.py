@@ -610,7 +610,7 @@ def test_sm90_swizzle_form():
 # execute(): program recognition (host side)
 # ---------------------------------------------------------------------------
 def test_plan_recognises_tiled_gemm():
-    from frisk_amd.execute import GemmPlan, plan
+    from frisk_amd.executor import GemmPlan, plan
     for ta, tb in itertools.product([False, True], repeat=2):
         s, _ = P.tiled_gemm(512, 256, 1024, trans_a=ta, trans_b=tb)
         assert plan(s.module, "matmul") == GemmPlan(0, 1, 2, ta, tb, True, 512, 256, 1024)
@@ -621,7 +621,7 @@ def test_plan_recognises_tiled_gemm():
 
 
 def test_plan_recognises_attention():
-    from frisk_amd.execute import AttnPlan, plan
+    from frisk_amd.executor import AttnPlan, plan
     s, _ = P.attention(2, 4, 256, 128)
     assert plan(s.module, "attention") == AttnPlan(0, 1, 2, 3, False, 2, 4, 256, 128)
     s, _ = P.attention(1, 2, 128, 64, k_transposed=True, staged=False, with_sum=False)
@@ -667,7 +667,7 @@ def _mutated_gemm(mutation):
 
 @pytest.mark.parametrize("mutation", ["grid", "nofill", "kstride", "bswap", "clear", "cswap"])
 def test_plan_rejects_wrong_programs(mutation):
-    from frisk_amd.execute import plan
+    from frisk_amd.executor import plan
     assert plan(_mutated_gemm("none").module, "matmul").m == 256
     with pytest.raises(ValueError, match="not a recognised GEMM or attention tile program"):
         plan(_mutated_gemm(mutation).module, "matmul")
