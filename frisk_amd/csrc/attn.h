@@ -1,4 +1,7 @@
-// Flash-attention forward for gfx950 (MI355X), head_dim 128, bf16 / f16.
+// Flash-attention forward for gfx950 (MI355X): head_dim 16, 32, 64 or 128,
+// bf16 / f16 inputs, output in the input dtype or f32.  This header holds
+// the kernel template; attn_d*.hip instantiate it per head_dim (so the
+// variants compile in parallel).
 //
 // Semantics: the attention tile program of the reference
 // (tmp/ir.mlir:89-157: S = Q.K^T per K tile, running row max, exp2 of the
@@ -23,11 +26,16 @@
 //    per-lane scalar.  Rescaling is lazy: the running max only moves when a
 //    block's max exceeds it by more than 2^8 in the exp2 domain, keeping
 //    every p <= 256 (exact in the final O / l, representable in bf16/f16).
-//  * K and V tiles (64 keys x 256 B each) arrive by LDS-DMA with XOR
+//  * K and V tiles (64 keys x 2D bytes each) arrive by LDS-DMA with XOR
 //    swizzles chosen for their read patterns, double-buffered: the loads of
 //    key block j+1 are in flight during the MFMAs and softmax of block j.
+//    Below head_dim 32 the V rows are padded to 32 dims in LDS (the DMA
+//    writes zeros there), so O^T keeps its 32-row MFMA tile; the padded rows
+//    are never stored.
 //  * Key blocks that need no mask run in a loop without mask code; the few
 //    blocks at the sequence end / causal diagonal run a masked copy.
+
+#pragma once
 
 #include "common.h"
 #include "kernels.h"
@@ -36,11 +44,7 @@ namespace frisk {
 
 namespace {
 
-constexpr int kD = 128;       // head dim
 constexpr int kBN = 64;       // keys per block
-constexpr int kKTile = kBN * kD * 2;  // 16 KiB
-constexpr int kVTile = kBN * kD * 2;  // 16 KiB
-constexpr int kBuf = kKTile + kVTile;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kRescaleSlack = 8.0f;  // log2 headroom before the running max moves
@@ -83,6 +87,36 @@ template <> struct AttnMfma<Elt::F16> {
   }
 };
 
+// LDS geometry of one key block for head_dim D.
+//  K: 64 rows of 2D bytes; chunk c of row r stored at c ^ swz_k(r), with
+//     swz_k(r) = (r >> log2(16 / kc)) & (kc - 1) (kc = 2D / 16 chunks): the 16
+//     rows one fragment read touches at one logical chunk land in 16
+//     distinct 16-B bank groups.
+//  V: 64 rows of 2 max(D, 32) bytes; the 4 rows (key & 3) of one transposed
+//     read hit disjoint chunk pairs (swz_v).
+template <int D> struct AttnGeom {
+  static_assert(D == 16 || D == 32 || D == 64 || D == 128, "head_dim 16/32/64/128");
+  static constexpr int kRB = 2 * D;                  // K row bytes
+  static constexpr int kKC = kRB / 16;               // K chunks per row
+  static constexpr int kKShift = D == 128 ? 0 : D == 64 ? 1 : D == 32 ? 2 : 3;
+  static constexpr int kDP = D < 32 ? 32 : D;        // padded dims of V / O^T
+  static constexpr int kRV = 2 * kDP;                // V row bytes
+  static constexpr int kVC = kRV / 16;               // V chunks per row
+  static constexpr int kKTile = kBN * kRB;
+  static constexpr int kVTile = kBN * kRV;
+  static constexpr int kBuf = kKTile + kVTile;
+  static constexpr int kKSteps = D / 16;             // S^T MFMA k-steps
+  static constexpr int kH1 = (kKSteps + 1) / 2;      // first half of them
+  static constexpr int kH2 = kKSteps - kH1;
+  static constexpr int kDT = kDP / 32;               // O^T tiles of 32 dims
+  __device__ static int swz_k(int r) { return (r >> kKShift) & (kKC - 1); }
+  __device__ static int swz_v(int r) {
+    if constexpr (kVC == 16) return 4 * (r & 3);
+    else if constexpr (kVC == 8) return 2 * ((r >> 1) & 1);
+    else return 0;
+  }
+};
+
 __device__ __forceinline__ float pair_reduce(float x, bool max_op) {
   // Combines lane l with lane l^32 (ds_bpermute).  The v_permlane32_swap
   // builtin of this toolchain returns the vdst register for both of its
@@ -94,8 +128,8 @@ __device__ __forceinline__ float pair_reduce(float x, bool max_op) {
 }  // namespace
 
 // QT query tiles of 32 per wave, NW waves per workgroup:
-// BM = 32 * QT * NW queries per workgroup.
-template <Elt T, int QT, int NW, bool CAUSAL>
+// BM = 32 * QT * NW queries per workgroup.  OUT is T or F32.
+template <Elt T, Elt OUT, int D, int QT, int NW, bool CAUSAL>
 __global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(
     const char* __restrict__ Q, const char* __restrict__ K, const char* __restrict__ V,
     char* __restrict__ O, float* __restrict__ LSE, int heads, int seq_q, int seq_k,
@@ -104,7 +138,7 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(
     float scale_log2, int q_blocks) {
 #if defined(__HIP_DEVICE_COMPILE__)
   using Mf = AttnMfma<T>;
-  constexpr int kThreads = 64 * NW;
+  using G = AttnGeom<D>;
   constexpr int BM = 32 * QT * NW;
   extern __shared__ __attribute__((aligned(1024))) char smem[];
 
@@ -143,49 +177,63 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(
 
   // ---- Q fragments (B operand of S^T = K.Q^T), loaded once -------------
   const int wq0 = q0 + wave * 32 * QT;  // first query of this wave
-  i32x4 qf[QT][8];
+  i32x4 qf[QT][G::kKSteps];
 #pragma unroll
   for (int t = 0; t < QT; ++t) {
     const int qi = min(wq0 + t * 32 + l32, seq_q - 1);
     const char* row = qh + (int64_t)qi * q_ss * 2 + half * 16;
 #pragma unroll
-    for (int ds = 0; ds < 8; ++ds) qf[t][ds] = *(const i32x4*)(row + ds * 32);
+    for (int ds = 0; ds < G::kKSteps; ++ds) qf[t][ds] = *(const i32x4*)(row + ds * 32);
   }
 
   // ---- K and V tiles by LDS-DMA -------------------------------------------
-  // One DMA instruction writes 1 KiB = 4 key rows of 256 B; lane L lands in
-  // row L/16, physical chunk L%16 and fetches logical chunk
-  // (L%16) ^ swz(row) of that row: swz = row & 15 for K (16 consecutive
-  // rows of one fragment read hit 16 distinct bank groups), 4 * (row & 3)
-  // for V (the 4 key rows of one transposed read, below, hit disjoint
-  // chunk sets).  Rows past seq_k read zeros (buffer range check).
+  // One DMA instruction writes 1 KiB: lane L lands in row L / chunks-per-row,
+  // physical chunk L % chunks-per-row, and fetches the logical chunk that
+  // the row's swizzle puts there.  Rows past seq_k and the V padding dims
+  // (head_dim < 32) read zeros (offsets past the buffer range).
   const __amdgpu_buffer_rsrc_t rsk = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)kh, (short)0, (int)min((int64_t)(seq_k - 1) * k_ss * 2 + kD * 2, (int64_t)0x7fffffff),
+      (void*)kh, (short)0, (int)min((int64_t)(seq_k - 1) * k_ss * 2 + D * 2, (int64_t)0x7fffffff),
       0x00020000);
   const __amdgpu_buffer_rsrc_t rsv = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)vh, (short)0, (int)min((int64_t)(seq_k - 1) * v_ss * 2 + kD * 2, (int64_t)0x7fffffff),
+      (void*)vh, (short)0, (int)min((int64_t)(seq_k - 1) * v_ss * 2 + D * 2, (int64_t)0x7fffffff),
       0x00020000);
-  constexpr int kKInst = 16 / NW;  // DMA instructions per wave per tile
-  uint32_t k_off[kKInst], v_off[kKInst];
+  constexpr int kKIns = G::kKTile / 1024, kVIns = G::kVTile / 1024;  // per tile
+  constexpr int kKI = (kKIns + NW - 1) / NW, kVI = (kVIns + NW - 1) / NW;  // per wave
+  uint32_t k_off[kKI], v_off[kVI];
+  int k_row[kKI], v_row[kVI];
 #pragma unroll
-  for (int i = 0; i < kKInst; ++i) {
-    const int r = (wave * kKInst + i) * 4 + (lane >> 4);
-    k_off[i] = (uint32_t)(r * k_ss * 2) + (((lane & 15) ^ (r & 15)) << 4);
-    v_off[i] = (uint32_t)(r * v_ss * 2) + (((lane & 15) ^ (4 * (r & 3))) << 4);
+  for (int i = 0; i < kKI; ++i) {
+    const int r = (wave * kKI + i) * (1024 / G::kRB) + lane / G::kKC;
+    const int c = (lane % G::kKC) ^ G::swz_k(r);
+    k_row[i] = (wave * kKI + i) < kKIns ? r : 1 << 30;
+    k_off[i] = (uint32_t)(r * k_ss * 2) + (c << 4);
+  }
+#pragma unroll
+  for (int i = 0; i < kVI; ++i) {
+    const int r = (wave * kVI + i) * (1024 / G::kRV) + lane / G::kVC;
+    const int c = (lane % G::kVC) ^ G::swz_v(r);
+    v_row[i] = ((wave * kVI + i) < kVIns && c * 8 < D) ? r : 1 << 30;
+    v_off[i] = (uint32_t)(r * v_ss * 2) + (c << 4);
   }
   auto issue_kv = [&](int kb, int buf) {
-    char* dst = smem + buf * kBuf + wave * kKInst * 1024;
+    char* dst = smem + buf * G::kBuf;
     const uint32_t kbase = (uint32_t)((int64_t)kb * kBN * k_ss * 2);
     const uint32_t vbase = (uint32_t)((int64_t)kb * kBN * v_ss * 2);
 #pragma unroll
-    for (int i = 0; i < kKInst; ++i) {
-      const int r = kb * kBN + (wave * kKInst + i) * 4 + (lane >> 4);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsk, (lds_ptr_t)(dst + i * 1024), 16,
+    for (int i = 0; i < kKI; ++i) {
+      if ((wave * kKI + i) >= kKIns) continue;  // wave-uniform
+      const int r = kb * kBN + k_row[i];
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsk, (lds_ptr_t)(dst + (wave * kKI + i) * 1024), 16,
                                                r < seq_k ? kbase + k_off[i] : 0x80000000u, 0,
                                                0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsv, (lds_ptr_t)(dst + kKTile + i * 1024), 16,
-                                               r < seq_k ? vbase + v_off[i] : 0x80000000u, 0,
-                                               0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < kVI; ++i) {
+      if ((wave * kVI + i) >= kVIns) continue;  // wave-uniform
+      const int r = kb * kBN + v_row[i];
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rsv, (lds_ptr_t)(dst + G::kKTile + (wave * kVI + i) * 1024), 16,
+          r < seq_k ? vbase + v_off[i] : 0x80000000u, 0, 0, 0);
     }
   };
 
@@ -196,25 +244,26 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(
   // so lane l receives V[16kk + 4h + 0..3 (+8)][32dt + l%32]: the A operand
   // of O^T = V^T.P^T with k-slots (h, e) -> key 16kk + (e < 4 ? 4h+e :
   // 8+4h+e-4), the key order of P taken from the S^T accumulators.
-  int vt_off[4];
+  int vt_off[G::kDT];
   {
     const int g = lane >> 4, hh = g >> 1, dg = g & 1, e = (lane >> 2) & 3, q = lane & 3;
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
-      const int chunk = (4 * dt + 2 * dg + (q >> 1)) ^ (4 * e);  // (key & 3) == e
-      vt_off[dt] = kKTile + (4 * hh + e) * 256 + (chunk << 4) + 8 * (q & 1);
+    for (int dt = 0; dt < G::kDT; ++dt) {
+      // The row is 16kk + 4hh + e (+8): its swizzle only depends on e.
+      const int chunk = (4 * dt + 2 * dg + (q >> 1)) ^ G::swz_v(4 * hh + e);
+      vt_off[dt] = G::kKTile + (4 * hh + e) * G::kRV + (chunk << 4) + 8 * (q & 1);
     }
   }
 
   // ---- state ---------------------------------------------------------------
-  f32x16 o[QT][4];
+  f32x16 o[QT][G::kDT];
   float m[QT], l[QT];
 #pragma unroll
   for (int t = 0; t < QT; ++t) {
     m[t] = -__builtin_inff();
     l[t] = 0.0f;
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt) o[t][dt] = f32x16{};
+    for (int dt = 0; dt < G::kDT; ++dt) o[t][dt] = f32x16{};
   }
 
   if (nkb > 0) {
@@ -233,24 +282,26 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(
     // (one LDS latency per half, not per MFMA) and the second half's reads
     // issue under the first half's MFMAs.  The first half of the V^T
     // fragments is read before the softmax, whose VALU work hides it.
-    auto read_k = [&](int h0, i32x4 (&kf)[2][4]) {
+    auto read_k = [&](int h0, auto& kf) {
+      constexpr int n = sizeof(kf[0]) / sizeof(kf[0][0]);
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt) {
         const int r = kt * 32 + l32;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          kf[kt][i] = *(const i32x4*)(ks + r * 256 + (((2 * (h0 + i) + half) ^ (r & 15)) << 4));
+        for (int i = 0; i < n; ++i)
+          kf[kt][i] =
+              *(const i32x4*)(ks + r * G::kRB + (((2 * (h0 + i) + half) ^ G::swz_k(r)) << 4));
       }
     };
-    auto read_v = [&](int k0, i32x4 (&vf)[2][4]) {
+    auto read_v = [&](int k0, i32x4 (&vf)[2][G::kDT]) {
       typedef short s16x4 __attribute__((ext_vector_type(4)));
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int dt = 0; dt < 4; ++dt) {
-          const char* p = ks + vt_off[dt] + (k0 + i) * 16 * 256;
+        for (int dt = 0; dt < G::kDT; ++dt) {
+          const char* p = ks + vt_off[dt] + (k0 + i) * 16 * G::kRV;
           const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((s16x4*)p);
-          const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((s16x4*)(p + 8 * 256));
+          const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((s16x4*)(p + 8 * G::kRV));
           typedef int i32x2 __attribute__((ext_vector_type(2)));
           const i32x2 a = __builtin_bit_cast(i32x2, lo), b = __builtin_bit_cast(i32x2, hi);
           vf[i][dt] = i32x4{a[0], a[1], b[0], b[1]};
@@ -259,25 +310,28 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(
     f32x16 s[QT][2];
 #pragma unroll
     for (int t = 0; t < QT; ++t) s[t][0] = s[t][1] = f32x16{};
-    i32x4 kf0[2][4], kf1[2][4];
+    i32x4 kf0[2][G::kH1], kf1[2][G::kH2 > 0 ? G::kH2 : 1];
     read_k(0, kf0);
     __builtin_amdgcn_sched_barrier(0);
-    read_k(4, kf1);
+    if constexpr (G::kH2 > 0) read_k(G::kH1, kf1);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < G::kH1; ++i)
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
         for (int t = 0; t < QT; ++t) s[t][kt] = Mf::run(kf0[kt][i], qf[t][i], s[t][kt]);
     __builtin_amdgcn_sched_barrier(0);
-    i32x4 vf0[2][4], vf1[2][4];
+    i32x4 vf0[2][G::kDT], vf1[2][G::kDT];
     read_v(0, vf0);
+    if constexpr (G::kH2 > 0) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < G::kH2; ++i)
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
+        for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-        for (int t = 0; t < QT; ++t) s[t][kt] = Mf::run(kf1[kt][i], qf[t][4 + i], s[t][kt]);
+          for (int t = 0; t < QT; ++t)
+            s[t][kt] = Mf::run(kf1[kt][i], qf[t][G::kH1 + i], s[t][kt]);
+    }
     __builtin_amdgcn_sched_barrier(0);
     // Online softmax in the exp2 domain: p = exp2(s * scale_log2 - m).
     // The max is taken on raw scores (scale_log2 > 0 commutes with max).
@@ -308,7 +362,7 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(
         m[t] = move ? mb : m[t];
         l[t] *= alpha;
 #pragma unroll
-        for (int dt = 0; dt < 4; ++dt) o[t][dt] *= alpha;
+        for (int dt = 0; dt < G::kDT; ++dt) o[t][dt] *= alpha;
       }
       // A row with every key masked so far keeps m = -inf; subtracting 0
       // instead gives its (all -inf) scores p = 0 rather than NaN.
@@ -335,14 +389,14 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt)
+      for (int dt = 0; dt < G::kDT; ++dt)
 #pragma unroll
         for (int t = 0; t < QT; ++t) o[t][dt] = Mf::run(vf0[i][dt], pf[t][i], o[t][dt]);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt)
+      for (int dt = 0; dt < G::kDT; ++dt)
 #pragma unroll
         for (int t = 0; t < QT; ++t) o[t][dt] = Mf::run(vf1[i][dt], pf[t][2 + i], o[t][dt]);
   };
@@ -358,7 +412,7 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(
     const int buf = j & 1;
     const bool more = j + 1 < nkb;
     if (more) issue_kv(j + 1, buf ^ 1);
-    key_block(smem + buf * kBuf, j * kBN, masked_tag);
+    key_block(smem + buf * G::kBuf, j * kBN, masked_tag);
     if (more) FRISK_WAIT_VMCNT0();
     __syncthreads();
   };
@@ -366,23 +420,30 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(
   for (int j = n_plain; j < nkb; ++j) step(j, std::true_type{});
 
   // ---- epilogue: O = O^T / l, LSE -----------------------------------------
-  char* oh = O + (b * o_sb + h * o_sh) * 2;
+  constexpr int kOB = EltInfo<OUT>::bytes;
+  char* oh = O + (b * o_sb + h * o_sh) * kOB;
 #pragma unroll
   for (int t = 0; t < QT; ++t) {
     const float lt = pair_reduce(l[t], false);  // both lane halves of the row
     const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
     const int qi = wq0 + t * 32 + l32;
     if (qi < seq_q) {
-      char* row = oh + (int64_t)qi * o_ss * 2;
+      char* row = oh + (int64_t)qi * o_ss * kOB;
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt)
+      for (int dt = 0; dt < G::kDT; ++dt)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const int d = dt * 32 + 8 * g + 4 * half;
-          typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-          const u32x2 w = {Mf::pack(o[t][dt][4 * g + 0] * inv, o[t][dt][4 * g + 1] * inv),
-                           Mf::pack(o[t][dt][4 * g + 2] * inv, o[t][dt][4 * g + 3] * inv)};
-          *(u32x2*)(row + d * 2) = w;
+          if (d >= D) continue;  // V padding dims (head_dim < 32)
+          if constexpr (OUT == Elt::F32) {
+            *(f32x4*)(row + d * 4) = f32x4{o[t][dt][4 * g + 0] * inv, o[t][dt][4 * g + 1] * inv,
+                                           o[t][dt][4 * g + 2] * inv, o[t][dt][4 * g + 3] * inv};
+          } else {
+            typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+            const u32x2 w = {Mf::pack(o[t][dt][4 * g + 0] * inv, o[t][dt][4 * g + 1] * inv),
+                             Mf::pack(o[t][dt][4 * g + 2] * inv, o[t][dt][4 * g + 3] * inv)};
+            *(u32x2*)(row + d * 2) = w;
+          }
         }
       if (LSE && half == 0)
         LSE[(int64_t)bh * seq_q + qi] = lt > 0.0f ? (m[t] + __log2f(lt)) * kLn2 : -__builtin_inff();
@@ -399,11 +460,11 @@ template <bool CAUSAL> struct AttnShape;
 template <> struct AttnShape<false> { static constexpr int QT = 1, NW = 8; };
 template <> struct AttnShape<true> { static constexpr int QT = 1, NW = 4; };
 
-template <Elt T, bool CAUSAL>
+template <Elt T, Elt OUT, int D, bool CAUSAL>
 static hipError_t launch_attn(const AttnArgs& a, hipStream_t stream) {
   constexpr int QT = AttnShape<CAUSAL>::QT, NW = AttnShape<CAUSAL>::NW, BM = 32 * QT * NW;
-  auto kern = attn_fwd_kernel<T, QT, NW, CAUSAL>;
-  constexpr int lds = 2 * kBuf;
+  auto kern = attn_fwd_kernel<T, OUT, D, QT, NW, CAUSAL>;
+  constexpr int lds = 2 * AttnGeom<D>::kBuf;
   static const hipError_t attr =
       hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
   if (attr != hipSuccess) return attr;
@@ -417,11 +478,24 @@ static hipError_t launch_attn(const AttnArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-hipError_t attn_fwd_d128(const AttnArgs& a, hipStream_t s) {
-  if (a.dtype == Elt::BF16)
-    return a.causal ? launch_attn<Elt::BF16, true>(a, s) : launch_attn<Elt::BF16, false>(a, s);
-  if (a.dtype == Elt::F16)
-    return a.causal ? launch_attn<Elt::F16, true>(a, s) : launch_attn<Elt::F16, false>(a, s);
+// Every (input dtype, output dtype, mask) variant of one head_dim.
+template <int D>
+hipError_t attn_fwd_dispatch(const AttnArgs& a, hipStream_t s) {
+  const bool f32_out = a.out == Elt::F32;
+  if (a.dtype == Elt::BF16) {
+    if (f32_out)
+      return a.causal ? launch_attn<Elt::BF16, Elt::F32, D, true>(a, s)
+                      : launch_attn<Elt::BF16, Elt::F32, D, false>(a, s);
+    return a.causal ? launch_attn<Elt::BF16, Elt::BF16, D, true>(a, s)
+                    : launch_attn<Elt::BF16, Elt::BF16, D, false>(a, s);
+  }
+  if (a.dtype == Elt::F16) {
+    if (f32_out)
+      return a.causal ? launch_attn<Elt::F16, Elt::F32, D, true>(a, s)
+                      : launch_attn<Elt::F16, Elt::F32, D, false>(a, s);
+    return a.causal ? launch_attn<Elt::F16, Elt::F16, D, true>(a, s)
+                    : launch_attn<Elt::F16, Elt::F16, D, false>(a, s);
+  }
   return hipErrorInvalidValue;
 }
 

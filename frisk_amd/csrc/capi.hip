@@ -142,8 +142,11 @@ int frisk_attn_fwd(const frisk_attn_desc* d, void* stream) {
   if (d->dtype != FRISK_BF16 && d->dtype != FRISK_F16)
     return fail(FRISK_EINVAL, "frisk_attn_fwd: dtype must be bf16 or f16 (got %s)",
                 dtype_name(d->dtype));
-  if (d->head_dim != 128)
-    return fail(FRISK_EUNSUP, "frisk_attn_fwd: head_dim %lld not supported (128 only)",
+  if (d->o_dtype != d->dtype && d->o_dtype != FRISK_F32)
+    return fail(FRISK_EINVAL, "frisk_attn_fwd: o_dtype must be the input dtype or f32 (got %s)",
+                dtype_name(d->o_dtype));
+  if (d->head_dim != 16 && d->head_dim != 32 && d->head_dim != 64 && d->head_dim != 128)
+    return fail(FRISK_EUNSUP, "frisk_attn_fwd: head_dim %lld not supported (16, 32, 64, 128)",
                 (long long)d->head_dim);
   if (!d->q || !d->k || !d->v || !d->o) return fail(FRISK_EINVAL, "frisk_attn_fwd: null tensor");
   if (!aligned16(d->q) || !aligned16(d->k) || !aligned16(d->v) || !aligned16(d->o))
@@ -165,6 +168,7 @@ int frisk_attn_fwd(const frisk_attn_desc* d, void* stream) {
 
   frisk::AttnArgs a;
   a.dtype = (frisk::Elt)d->dtype;
+  a.out = (frisk::Elt)d->o_dtype;
   a.batch = d->batch; a.heads = d->heads; a.seq_q = d->seq_q; a.seq_k = d->seq_k;
   a.head_dim = d->head_dim;
   a.causal = d->causal != 0;
@@ -174,7 +178,7 @@ int frisk_attn_fwd(const frisk_attn_desc* d, void* stream) {
   a.v = d->v; a.v_sb = d->v_stride_b; a.v_sh = d->v_stride_h; a.v_ss = d->v_stride_s;
   a.o = d->o; a.o_sb = d->o_stride_b; a.o_sh = d->o_stride_h; a.o_ss = d->o_stride_s;
   a.lse = d->lse;
-  hipError_t e = frisk::attn_fwd_d128(a, (hipStream_t)stream);
+  hipError_t e = frisk::attn_fwd(a, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "frisk_attn_fwd launch");
   return FRISK_OK;
 }

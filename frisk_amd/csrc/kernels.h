@@ -40,7 +40,8 @@ hipError_t gemm_skinny(const GemmArgs& g, hipStream_t s);
 
 // A validated attention request.
 struct AttnArgs {
-  Elt dtype;
+  Elt dtype;  // Q/K/V
+  Elt out;    // O: dtype or F32
   int64_t batch, heads, seq_q, seq_k, head_dim;
   int causal;
   float sm_scale;
@@ -56,6 +57,18 @@ struct AttnArgs {
 };
 
 hipError_t attn_fwd_d128(const AttnArgs& a, hipStream_t s);
+hipError_t attn_fwd_d64(const AttnArgs& a, hipStream_t s);
+hipError_t attn_fwd_d32(const AttnArgs& a, hipStream_t s);
+hipError_t attn_fwd_d16(const AttnArgs& a, hipStream_t s);
+inline hipError_t attn_fwd(const AttnArgs& a, hipStream_t s) {
+  switch (a.head_dim) {
+    case 128: return attn_fwd_d128(a, s);
+    case 64: return attn_fwd_d64(a, s);
+    case 32: return attn_fwd_d32(a, s);
+    case 16: return attn_fwd_d16(a, s);
+    default: return hipErrorInvalidValue;
+  }
+}
 
 // MFMA fragment-layout probe (probe.hip): atom 0 = bf16 32x32x16,
 // 1 = bf16 16x16x32, 2 = i8 32x32x32; `out` holds mfma_probe_floats(atom)

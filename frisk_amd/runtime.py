@@ -22,7 +22,7 @@ DTYPE_NAMES = {F32: "f32", F16: "f16", BF16: "bf16", E4M3: "e4m3", I8: "i8", I32
 # Exported symbols declared by include/frisk_hip.h.
 EXPORTS = ("frisk_gemm", "frisk_attn_fwd", "frisk_last_error", "frisk_abi_version",
            "frisk_probe_mfma_layout")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 
 class GemmDesc(ctypes.Structure):
@@ -52,6 +52,7 @@ class AttnDesc(ctypes.Structure):
         ("o", ctypes.c_void_p), ("o_stride_b", ctypes.c_int64), ("o_stride_h", ctypes.c_int64),
         ("o_stride_s", ctypes.c_int64),
         ("lse", ctypes.c_void_p),
+        ("o_dtype", ctypes.c_int32),
     ]
 
 
@@ -174,8 +175,11 @@ def attn_desc(q, k, v, o, *, causal=False, sm_scale=None, lse=None) -> AttnDesc:
     if tuple(k.shape) != (b, h, sk, d) or tuple(v.shape) != (b, h, sk, d) \
             or tuple(o.shape) != (b, h, sq, d):
         raise ValueError("attention shapes disagree")
-    if not (q.dtype == k.dtype == v.dtype == o.dtype):
-        raise ValueError("Q/K/V/O must share one dtype")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise ValueError("Q/K/V must share one dtype")
+    import torch
+    if o.dtype not in (q.dtype, torch.float32):
+        raise ValueError("O must have the Q/K/V dtype or float32")
     if lse is not None and (tuple(lse.shape) != (b, h, sq) or not lse.is_contiguous()
                             or lse.dtype.is_floating_point is False or lse.element_size() != 4):
         raise ValueError("lse must be a contiguous f32 [batch, heads, seq_q] tensor")
@@ -187,7 +191,7 @@ def attn_desc(q, k, v, o, *, causal=False, sm_scale=None, lse=None) -> AttnDesc:
                     k.data_ptr(), k.stride(0), k.stride(1), k.stride(2),
                     v.data_ptr(), v.stride(0), v.stride(1), v.stride(2),
                     o.data_ptr(), o.stride(0), o.stride(1), o.stride(2),
-                    lse.data_ptr() if lse is not None else None)
+                    lse.data_ptr() if lse is not None else None, torch_dtype_code(o.dtype))
 
 
 def attn_fwd(q, k, v, o, *, causal=False, sm_scale=None, lse=None, stream=None):

@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define FRISK_ABI_VERSION 1
+#define FRISK_ABI_VERSION 2
 
 /* Element types (the dtype strings of ffi/ir.cpp:399-411 plus bf16/i8/i32). */
 typedef enum frisk_dtype {
@@ -91,11 +91,13 @@ int frisk_gemm(const frisk_gemm_desc* desc, void* stream);
 /*
  * Flash-attention forward over [batch, heads, seq, head_dim] tensors:
  *   O[b,h,i,:] = softmax_j(sm_scale * Q[b,h,i,:].K[b,h,j,:]) . V[b,h,j,:]
- * with j <= i (plus seq_k - seq_q) when causal != 0.  Q/K/V/O are bf16 or
- * f16 (q_type == k_type == v_type == o_type); the softmax statistics are
- * f32.  Strides are in elements; the innermost (head_dim) stride is 1.
- * lse, if non-NULL, receives the f32 natural-log row log-sum-exp of the
- * scaled scores, laid out [batch, heads, seq_q] contiguous.
+ * with j <= i (plus seq_k - seq_q) when causal != 0.  Q/K/V are bf16 or f16
+ * (one dtype); O is that dtype or f32 (o_dtype; the reference's tiled
+ * attention writes f32 O, tiled_attention.py:658-683).  head_dim is 16, 32,
+ * 64 or 128.  The softmax statistics are f32.  Strides are in elements; the
+ * innermost (head_dim) stride is 1.  lse, if non-NULL, receives the f32
+ * natural-log row log-sum-exp of the scaled scores, laid out
+ * [batch, heads, seq_q] contiguous.
  */
 typedef struct frisk_attn_desc {
   int64_t batch, heads, seq_q, seq_k, head_dim;
@@ -111,6 +113,7 @@ typedef struct frisk_attn_desc {
   void* o;
   int64_t o_stride_b, o_stride_h, o_stride_s;
   float* lse;
+  int32_t o_dtype; /* frisk_dtype: equal to dtype, or FRISK_F32 */
 } frisk_attn_desc;
 
 int frisk_attn_fwd(const frisk_attn_desc* desc, void* stream);

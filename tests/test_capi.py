@@ -61,7 +61,8 @@ def attn_call(**over):
                     sm_scale=0.088, q=16, q_stride_b=8192, q_stride_h=8192, q_stride_s=128,
                     k=16, k_stride_b=8192, k_stride_h=8192, k_stride_s=128,
                     v=16, v_stride_b=8192, v_stride_h=8192, v_stride_s=128,
-                    o=16, o_stride_b=8192, o_stride_h=8192, o_stride_s=128, lse=None)
+                    o=16, o_stride_b=8192, o_stride_h=8192, o_stride_s=128, lse=None,
+                    o_dtype=rt.BF16)
     for key, val in over.items():
         setattr(d, key, val)
     lib = rt.load()
@@ -72,8 +73,9 @@ def attn_call(**over):
 @pytest.mark.parametrize("over,code,prefix", [
     (dict(seq_q=0), rt.EINVAL, "frisk_attn_fwd: sizes"),
     (dict(dtype=rt.F32), rt.EINVAL, "frisk_attn_fwd: dtype"),
-    (dict(head_dim=64, q_stride_s=64, k_stride_s=64, v_stride_s=64, o_stride_s=64), rt.EUNSUP,
+    (dict(head_dim=96, q_stride_s=96, k_stride_s=96, v_stride_s=96, o_stride_s=96), rt.EUNSUP,
      "frisk_attn_fwd: head_dim"),
+    (dict(o_dtype=rt.F16), rt.EINVAL, "frisk_attn_fwd: o_dtype"),
     (dict(q=24), rt.EINVAL, "frisk_attn_fwd: Q/K/V/O must be 16-byte"),
     (dict(k_stride_s=100), rt.EINVAL, "frisk_attn_fwd: strides"),
     (dict(v_stride_s=64), rt.EINVAL, "frisk_attn_fwd: sequence stride"),
