@@ -29,6 +29,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 PEAK = {"bf16": 2500.0, "f16": 2500.0, "fp8": 5000.0, "int8": 5000.0}  # dense TFLOP/s (TOP/s)
+REF_FIXED_TILE_US = {"single": 21.584, "graph": 6.5386}  # H100
 HBM_PEAK_GBS = 8000.0
 
 
@@ -90,6 +91,16 @@ def make_workloads(torch, rt):
             return lambda: dst.copy_(src)
         return setup
 
+    def attn_d64():
+        def setup():
+            shape = (2, 32, 1025, 64)
+            q = (torch.rand(shape, generator=gen(8), device=dev) * 2 - 1).half()
+            k = (torch.rand(shape, generator=gen(9), device=dev) * 2 - 1).half()
+            v = (torch.rand(shape, generator=gen(10), device=dev) * 2 - 1).half()
+            o = torch.empty(shape, dtype=torch.float32, device=dev)
+            return lambda: rt.attn_fwd(q, k, v, o, causal=False, sm_scale=0.125)
+        return setup
+
     fa = 4.0 * 4 * 32 * 4096 * 4096 * 128
     return {
         "gemm_bf16_4096": ("bf16", 2.0 * 4096 ** 3, gemm(4096, 4096, 4096, "bf16")),
@@ -99,6 +110,7 @@ def make_workloads(torch, rt):
         "gemm_int8_4096": ("int8", 2.0 * 4096 ** 3, gemm(4096, 4096, 4096, "int8")),
         "fa_fwd_b4h32s4096d128": ("bf16", fa, attn(False)),
         "fa_fwd_b4h32s4096d128_causal": ("bf16", fa / 2, attn(True)),
+        "fa_fwd_d64_b2h32s1025_f16_f32out": ("f16", 4.0 * 2 * 32 * 1025 * 1025 * 64, attn_d64()),
         # Calibration only (--only): a plain 256 MiB device copy, whose
         # FETCH_SIZE / WRITE_SIZE per dispatch scale the HBM counters.
         "copy_256mib": ("bytes", 0.0, copy(256 << 20)),
@@ -117,6 +129,52 @@ def time_launches(torch, fn, steps, warmup):
     end.record()
     torch.cuda.synchronize()
     return start.elapsed_time(end) / steps  # ms per launch
+
+
+def fixed_tile_latency(torch, rt):
+    """The reference's 64x16 attention tile: single-launch and graph-amortized
+    per-launch time in microseconds (see module docstring)."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0)
+    q, k, v = ((torch.rand(1, 1, 64, 16, generator=g, device="cuda") * 2 - 1).half() for _ in range(3))
+    o = torch.empty(1, 1, 64, 16, dtype=torch.float32, device="cuda")
+
+    def launch():
+        rt.attn_fwd(q, k, v, o, sm_scale=0.25)
+
+    for _ in range(20):
+        launch()
+    torch.cuda.synchronize()
+    single = []
+    for _ in range(20):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        launch()
+        b.record()
+        b.synchronize()
+        single.append(a.elapsed_time(b) * 1e3)
+    per_graph = 100
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(per_graph):
+            launch()
+    graph.replay()
+    torch.cuda.synchronize()
+    replays = []
+    for _ in range(20):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        graph.replay()
+        b.record()
+        b.synchronize()
+        replays.append(a.elapsed_time(b) * 1e3 / per_graph)
+    single.sort()
+    replays.sort()
+    return {"single_us_median": round(single[len(single) // 2], 3),
+            "graph_us_median": round(replays[len(replays) // 2], 3),
+            "reference_h100_us": REF_FIXED_TILE_US,
+            "speedup_vs_reference": {"single": round(REF_FIXED_TILE_US["single"] / single[len(single) // 2], 2),
+                                     "graph": round(REF_FIXED_TILE_US["graph"] / replays[len(replays) // 2], 2)}}
 
 
 def cpu_baseline(torch):
@@ -169,6 +227,9 @@ def main():
     rt.load()
     torch.cuda.set_device(0)
     work = make_workloads(torch, rt)
+    if args.only == "fixed_tile_64x16":
+        print(json.dumps({"workload": args.only, **fixed_tile_latency(torch, rt)}), flush=True)
+        return
     if args.only:
         label, flops, setup = work[args.only]
         fn = setup()
@@ -212,6 +273,7 @@ def main():
                      "unit": "TFLOP/s", "frac": round(head["tflops"] / PEAK["bf16"], 4),
                      "traffic": traffic},
         "workloads": results,
+        "fixed_tile_64x16": fixed_tile_latency(torch, rt),
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(torch)
