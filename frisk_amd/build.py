@@ -34,11 +34,14 @@ COMMON = [
     "-fPIC",
     # Packed-fp32 VALU forms are kept out of generated code on this platform.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-    # MFMA accumulators in VGPRs: the softmax rescale and epilogue read them
-    # with VALU ops, which would otherwise copy AGPRs back and forth.
-    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wno-unused-command-line-argument",
 ]
+# MFMA accumulators in VGPRs: the softmax rescale and epilogue read them
+# with VALU ops, which would otherwise copy AGPRs back and forth.
+VGPR_FORM = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
+# Files whose MFMA accumulators live in AGPRs: their kernels hold 256
+# accumulator registers per lane and read them only in the epilogue.
+AGPR_ACC = {"gemm4w.hip"}
 
 
 def sources() -> list[Path]:
@@ -52,7 +55,8 @@ def build(verbose: bool = False, extra: list[str] | None = None) -> Path:
 
     def compile_one(src: Path) -> Path:
         obj = objdir / (src.stem + ".o")
-        cmd = [HIPCC, *flags, "-c", str(src), "-o", str(obj)]
+        form = [] if src.name in AGPR_ACC else VGPR_FORM
+        cmd = [HIPCC, *flags, *form, "-c", str(src), "-o", str(obj)]
         if verbose:
             print(" ".join(shlex.quote(c) for c in cmd), flush=True)
         r = subprocess.run(cmd, capture_output=True, text=True)

@@ -271,6 +271,10 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(
     FRISK_WAIT_VMCNT0();
     __syncthreads();
   }
+  // Drain the scalar loads of kernel arguments used after the loop: with
+  // them pending at loop entry the LGKM counter is unordered and every LDS
+  // read in the loop would be waited for with lgkmcnt(0).
+  __builtin_amdgcn_s_waitcnt(0xC07F);
 
   // One key block: S^T = K.Q^T, online softmax, O^T += V^T.P^T.  Masked
   // blocks (the sequence tail, and blocks crossing this wave's causal

@@ -1,4 +1,6 @@
-// MFMA GEMM kernels for gfx950 (MI355X).
+// MFMA GEMM kernels for gfx950 (MI355X): the 128x128-tile kernel, the
+// generic fallback and the launch policy.  The 256x256-tile kernel lives in
+// gemm4w.hip.
 //
 // Semantics follow frisk.gemm (include/Dialect/Frisk/IR/FriskOps.td:252-292):
 // C = op(A).op(B) when clear_accum, else C += op(A).op(B).  The reference
@@ -6,22 +8,18 @@
 // (benchmark/layout/execution/backend.py:383-431); here the whole problem is
 // tiled for CDNA4:
 //
-//  * 256x256 output tile per 256-thread workgroup (4 waves, 2x2), each wave
-//    owning a 128x128 sub-tile as 4x4 v_mfma 32x32 accumulators in AGPRs.
-//  * K is consumed in stages of 128 bytes per row (64 bf16/f16, 128 fp8/i8):
-//    the A and B stage tiles are 256 rows x 128 B = 32 KiB each, loaded with
-//    one dwordx4 per lane per row chunk (8 lanes cover one 128 B row
-//    segment, fully coalesced) into registers, then written to LDS.
-//  * Two LDS stages (128 KiB of the 160 KiB per CU): the global loads of
-//    stage s+1 are in flight while the MFMAs of stage s run; one barrier per
-//    stage.
-//  * LDS rows are 128 B = 8 chunks of 16 B; chunk c of row r is stored at
-//    chunk c ^ swz(r).  The fragment read of a 32x32 MFMA has 32 lanes read
-//    the same logical chunk of 32 consecutive rows; the XOR spreads those
-//    rows over distinct bank groups.  swz is an F2-linear map of the row
-//    bits (a GF(2) layout in the sense of the reference's bit-linear
-//    shared layouts, SM90GemmConstraints.cpp:106-150).
-//  * The epilogue stages each 32x128 f32 slice of a wave through LDS so the
+//  * 128x128 output tile per 256-thread workgroup (4 waves, 2x2), each wave
+//    owning a 64x64 sub-tile as 2x2 v_mfma 32x32 accumulators; two
+//    workgroups share a CU.
+//  * K is consumed in stages of 64 bytes per row (32 bf16/f16, 64 fp8/i8),
+//    loaded by LDS-DMA (buffer_load_dwordx4 ... lds: no VGPRs stage the
+//    data) into kStages rotating LDS slots, one barrier per stage.
+//  * LDS rows are 4 chunks of 16 B, chunk c of row r stored at chunk
+//    c ^ swz(r); the XOR spreads the 32 rows of a fragment read over distinct
+//    bank groups.  swz is an F2-linear map of the row bits (a GF(2) layout in
+//    the sense of the reference's bit-linear shared layouts,
+//    SM90GemmConstraints.cpp:106-150).
+//  * The epilogue stages each 32-row f32 slice of a wave through LDS so the
 //    global stores are row-contiguous 16 B per lane.
 //
 // Operand contract of the fast kernel: A is [M, K] and B is [N, K] (both
@@ -29,58 +27,14 @@
 // aligned rows; the generic kernel covers every other layout and type.
 
 #include "common.h"
+#include "gemm_common.h"
 #include "kernels.h"
 
 namespace frisk {
 
 // ---------------------------------------------------------------------------
-// MFMA wrappers.  kBytes = bytes of one operand row consumed by one 32x32
-// MFMA; every lane supplies kBytes/2 of them (lanes 0-31 and 32-63 split the
-// row), as i32x4 chunks.  A and B fragments use the same (lane, byte) -> k
-// assignment, so the k order inside an instruction never matters.
-// ---------------------------------------------------------------------------
-template <Elt E> struct Mfma32;
-
-template <> struct Mfma32<Elt::BF16> {
-  static constexpr int kBytes = 32;
-  using Acc = f32x16;
-  __device__ static inline Acc run(const i32x4* a, const i32x4* b, Acc c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a[0]),
-                                                   __builtin_bit_cast(bf16x8, b[0]), c, 0, 0, 0);
-  }
-};
-
-template <> struct Mfma32<Elt::F16> {
-  static constexpr int kBytes = 32;
-  using Acc = f32x16;
-  __device__ static inline Acc run(const i32x4* a, const i32x4* b, Acc c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a[0]),
-                                                  __builtin_bit_cast(f16x8, b[0]), c, 0, 0, 0);
-  }
-};
-
-template <> struct Mfma32<Elt::E4M3> {
-  static constexpr int kBytes = 64;
-  using Acc = f32x16;
-  __device__ static inline Acc run(const i32x4* a, const i32x4* b, Acc c) {
-    const i32x8 av = {a[0][0], a[0][1], a[0][2], a[0][3], a[1][0], a[1][1], a[1][2], a[1][3]};
-    const i32x8 bv = {b[0][0], b[0][1], b[0][2], b[0][3], b[1][0], b[1][1], b[1][2], b[1][3]};
-    // Format 0 = fp8 e4m3 for both operands; E8M0 block scales 127 = 2^0.
-    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, bv, c, 0, 0, 0, 127, 0, 127);
-  }
-};
-
-template <> struct Mfma32<Elt::I8> {
-  static constexpr int kBytes = 32;
-  using Acc = i32x16;
-  __device__ static inline Acc run(const i32x4* a, const i32x4* b, Acc c) {
-    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a[0], b[0], c, 0, 0, 0);
-  }
-};
-
-// ---------------------------------------------------------------------------
 // Tiling.  Each stage holds 64 bytes of K per row (32 bf16/f16, 64 fp8/i8)
-// for the 256 A rows and 256 B rows: 2 x 16 KiB.  kStages stages rotate
+// for the BT A rows and BT B rows (2 x 8 KiB at BT = 128).  kStages rotate
 // through LDS; a stage is filled by LDS-DMA (buffer_load_dwordx4 ... lds),
 // so no VGPRs stage the data and the loads of kStages-2 stages are in
 // flight while one stage is multiplied.
@@ -105,67 +59,7 @@ constexpr int kRow = 64;  // bytes of K per row per stage
 constexpr int kStages = FRISK_GEMM_STAGES;
 // LDS bytes of a BT x BT tile pipeline: kStages stages of (A, B) tiles.
 constexpr int lds_bytes(int bt) { return kStages * 2 * bt * kRow; }
-static_assert(lds_bytes(256) <= 160 * 1024, "LDS budget of one CU");
-
-// s_waitcnt with only the vector-memory counter limited to n (gfx9 encoding:
-// vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]).
-#define FRISK_WAIT_VMCNT(n) \
-  __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
-
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
-
-template <Elt OUT, typename AccS>
-__device__ inline void store8(void* c, int64_t idx, const AccS* v, bool accumulate, float scale) {
-  if constexpr (OUT == Elt::I32) {
-    int32_t* p = (int32_t*)c + idx;
-    i32x4 lo = {(int)v[0], (int)v[1], (int)v[2], (int)v[3]};
-    i32x4 hi = {(int)v[4], (int)v[5], (int)v[6], (int)v[7]};
-    if (accumulate) {
-      lo += *(const i32x4*)p;
-      hi += *(const i32x4*)(p + 4);
-    }
-    *(i32x4*)p = lo;
-    *(i32x4*)(p + 4) = hi;
-  } else if constexpr (OUT == Elt::F32) {
-    float* p = (float*)c + idx;
-    f32x4 lo = {v[0] * scale, v[1] * scale, v[2] * scale, v[3] * scale};
-    f32x4 hi = {v[4] * scale, v[5] * scale, v[6] * scale, v[7] * scale};
-    if (accumulate) {
-      lo += *(const f32x4*)p;
-      hi += *(const f32x4*)(p + 4);
-    }
-    *(f32x4*)p = lo;
-    *(f32x4*)(p + 4) = hi;
-  } else {
-    uint16_t* p = (uint16_t*)c + idx;
-    float f[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) f[i] = v[i] * scale;
-    if (accumulate) {
-      const i32x4 old = *(const i32x4*)p;
-      const uint16_t* o = (const uint16_t*)&old;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        if constexpr (OUT == Elt::BF16) f[i] += bf16_bits_to_f32(o[i]);
-        else f[i] += (float)__builtin_bit_cast(_Float16, o[i]);
-      }
-    }
-    uint16_t r[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      if constexpr (OUT == Elt::BF16) r[i] = f32_to_bf16_bits(f[i]);
-      else r[i] = __builtin_bit_cast(uint16_t, (_Float16)f[i]);
-    }
-    *(i32x4*)p = *(const i32x4*)r;
-  }
-}
-
-// MFMA operand fragments of one k-step: TM A tiles and TN B tiles.
-template <int TM, int TN, int LC>
-struct Frags {
-  i32x4 a[TM][LC];
-  i32x4 b[TN][LC];
-};
+static_assert(2 * lds_bytes(128) <= 160 * 1024, "two 128x128 workgroups per CU");
 
 // One workgroup per BT x BT output tile; WM x WN waves tile it, each wave
 // owning a (BT/WM) x (BT/WN) sub-tile as TM x TN 32x32 accumulators.
@@ -303,6 +197,12 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_tn(const char* __restr
 
   Frag fr[2];
   load_frags(0, 0, fr[0]);
+  // Drain every LGKM operation issued so far (the prologue's fragment reads
+  // and the scalar loads of the epilogue's kernel arguments).  With scalar
+  // loads still pending at the loop entry the LGKM counter is unordered, and
+  // the compiler then waits for lgkmcnt(0) at the top of every iteration,
+  // i.e. for the fragment read it has just issued.
+  __builtin_amdgcn_s_waitcnt(0xC07F);
   int slot = 0;
   for (int kt = 0; kt < nk; ++kt) {
 #pragma unroll
@@ -454,13 +354,6 @@ __global__ __launch_bounds__(256) void gemm_generic(const void* __restrict__ A,
 // ---------------------------------------------------------------------------
 // Launchers.
 // ---------------------------------------------------------------------------
-#ifndef FRISK_GEMM_WM
-#define FRISK_GEMM_WM 2
-#endif
-#ifndef FRISK_GEMM_WN
-#define FRISK_GEMM_WN 4
-#endif
-
 template <Elt IN, Elt OUT, int BT, int WM, int WN>
 static hipError_t launch_tn_cfg(const GemmArgs& g, hipStream_t stream) {
   constexpr int kEsz = EltInfo<IN>::bytes;
@@ -477,16 +370,16 @@ static hipError_t launch_tn_cfg(const GemmArgs& g, hipStream_t stream) {
   return hipGetLastError();
 }
 
-// 256x256 tiles (8 waves, 128x64 each) when there are at least half as
-// many as CUs; otherwise 128x128 tiles (4 waves, 64x64 each, two workgroups
-// per CU), which keep more CUs busy (measured on the projection sweep:
-// M=1024, N=4096 runs 2x faster on 128x128 tiles, N=14336 (224 big tiles)
-// runs faster on 256x256).
+// 256x256 tiles (gemm4w.hip: 4 waves of 128x128, one workgroup per CU)
+// when there are at least half as many as CUs; otherwise 128x128 tiles
+// (4 waves of 64x64, two workgroups per CU), which keep more CUs busy
+// (measured on the projection sweep: M=1024, N=4096 runs 2x faster on
+// 128x128 tiles, N=14336 (224 big tiles) runs faster on 256x256).
 constexpr int kCus = 256;
 template <Elt IN, Elt OUT>
 static hipError_t launch_tn(const GemmArgs& g, hipStream_t stream) {
   const int64_t tiles256 = ((g.m + 255) / 256) * ((g.n + 255) / 256);
-  if (tiles256 >= kCus / 2) return launch_tn_cfg<IN, OUT, 256, FRISK_GEMM_WM, FRISK_GEMM_WN>(g, stream);
+  if (tiles256 >= kCus / 2) return gemm_tn_w4(g, stream);
   return launch_tn_cfg<IN, OUT, 128, 2, 2>(g, stream);
 }
 

@@ -1,0 +1,355 @@
+// Large-tile MFMA GEMM for gfx950: one 256x256 output tile per workgroup of
+// four waves, one wave per SIMD, each wave owning a 128x128 sub-tile as 4x4
+// accumulators of the 32x32 MFMA (256 accumulator registers per lane, held
+// in AGPRs; this file is compiled without the VGPR-form MFMA option).
+//
+// Semantics are those of gemm.hip's fast kernel (frisk.gemm with
+// trans_a == 0, trans_b == 1: C[m, n] = scale * sum_k A[m, k] B[n, k]
+// (+ C when accumulating); include/Dialect/Frisk/IR/FriskOps.td:252-292).
+//
+// Why four waves of 128x128 rather than eight of 128x64: per k-step a wave
+// reads (TM + TN) fragments for TM * TN MFMAs, so the 128x128 sub-tile
+// halves LDS read traffic per flop (8 reads per 16 MFMAs instead of 6 per
+// 8), and with KR = 128 bytes of K per stage (64 bf16) the MFMA time between
+// two workgroup barriers is 64 MFMAs = 2048 cycles.  A 128-byte row segment
+// is one whole cache line: with 64-byte stages every line is fetched from L2
+// twice (rocprofv3: TCP_TCC_READ_REQ halves from 1.34e8 to 6.7e7 at 8192^3).
+// Two 64 KiB stages fill 128 KiB of the 160 KiB LDS.  With a single wave per
+// SIMD nothing else can fill a stall, so every fragment read and DMA issue
+// is placed between MFMAs explicitly (sched_group_barrier).
+
+#include "common.h"
+#include "gemm_common.h"
+#include "kernels.h"
+
+namespace frisk {
+
+// Bytes of K per row per stage (64 or 128), LDS stages, and the number of
+// k-steps that issue DMA (0: the default below).
+#ifndef FRISK_G4_KR
+#define FRISK_G4_KR 128
+#endif
+#ifndef FRISK_G4_STAGES
+#define FRISK_G4_STAGES 2
+#endif
+#ifndef FRISK_G4_PARTS
+#define FRISK_G4_PARTS 0
+#endif
+
+namespace g4 {
+
+constexpr int kBT = 256;
+constexpr int kThreads = 256;
+
+// LDS row swizzles (physical 16 B chunk = logical chunk ^ swz(row)).  A
+// fragment read has 16 lanes per LDS cycle reading one logical chunk of 16
+// consecutive rows; the swizzle sends those rows to 16 distinct 16 B bank
+// groups.  rocprofv3 measured SQ_LDS_BANK_CONFLICT = 0 for both maps on
+// ds_read_b128.
+template <int KR> __device__ __forceinline__ int swz(int r);
+template <> __device__ __forceinline__ int swz<64>(int r) { return (r >> 2) & 3; }
+template <> __device__ __forceinline__ int swz<128>(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+
+constexpr int lds_bytes(int kr, int stages) { return stages * 2 * kBT * kr; }
+
+}  // namespace g4
+
+template <Elt IN, Elt OUT, int KR, int S>
+__global__ __launch_bounds__(g4::kThreads) void gemm_w4_kernel(
+    const char* __restrict__ A, const char* __restrict__ B, void* __restrict__ C, int M, int N,
+    int Kb, int64_t lda_b, int64_t ldb_b, int64_t ldc, float scale, int accumulate) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  using Op = Mfma32<IN>;
+  using Acc = typename Op::Acc;
+  using AccS = typename std::conditional<IN == Elt::I8, int32_t, float>::type;
+  constexpr int BT = g4::kBT;
+  constexpr int TM = 4, TN = 4;                 // 32x32 atoms per wave
+  constexpr int kChunks = KR / 16;              // 16 B chunks per LDS row
+  constexpr int kRowsPerBlock = 1024 / KR;      // rows per 1 KiB DMA block
+  constexpr int kTileBytes = BT * KR;           // one operand, one stage
+  constexpr int kStageBytes = 2 * kTileBytes;
+  constexpr int kStepChunks = Op::kBytes / 16;  // chunks per row per MFMA
+  constexpr int kLaneChunks = kStepChunks / 2;  // chunks per lane per MFMA
+  constexpr int kSteps = KR / Op::kBytes;       // MFMA k-steps per stage
+  constexpr int kBlocks = kTileBytes / 1024 / 4;       // DMA blocks per wave per operand
+  constexpr int kLoads = 2 * kBlocks;                  // DMA loads per lane per stage
+  constexpr int kFragReads = (TM + TN) * kLaneChunks;  // ds_read_b128 per lane per k-step
+  static_assert(S >= 2 && kSteps >= 1, "pipeline shape");
+
+  extern __shared__ __attribute__((aligned(1024))) char smem[];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int l32 = lane & 31, half = lane >> 5;
+
+  const int tiles_m = (M + BT - 1) / BT, tiles_n = (N + BT - 1) / BT;
+  int tm, tn;
+  tile_of_block<4>(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
+  const int row0 = tm * BT, col0 = tn * BT;
+
+  // ---- LDS-DMA mapping ----------------------------------------------------
+  // DMA instruction i of wave w fills 1 KiB block (kBlocks w + i) of a tile:
+  // rows kRowsPerBlock * block + lane / kChunks, physical chunk
+  // lane % kChunks, i.e. logical chunk (lane % kChunks) ^ swz(row).  Raw
+  // buffer loads based at the tile's first row: an offset past num_records
+  // reads zeros, which covers the K tail and the stages past the last one
+  // without branches (and without memory traffic).
+  const char* a_base = A + (int64_t)row0 * lda_b;
+  const char* b_base = B + (int64_t)col0 * ldb_b;
+  const int64_t a_left = (int64_t)(M - 1 - row0) * lda_b + Kb;
+  const int64_t b_left = (int64_t)(N - 1 - col0) * ldb_b + Kb;
+  const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)a_base, (short)0, (int)min(a_left, (int64_t)0x7fffffff), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rsb = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)b_base, (short)0, (int)min(b_left, (int64_t)0x7fffffff), 0x00020000);
+  uint32_t a_off[kBlocks], b_off[kBlocks];
+  int kmax[kBlocks];
+#pragma unroll
+  for (int i = 0; i < kBlocks; ++i) {
+    const int r = (kBlocks * wave + i) * kRowsPerBlock + lane / kChunks;
+    const int c = (lane % kChunks) ^ g4::swz<KR>(r);
+    // Rows past the matrix edge are clamped: they only feed output rows or
+    // columns that are never stored.
+    a_off[i] = (uint32_t)(min(r, M - 1 - row0) * lda_b) + c * 16;
+    b_off[i] = (uint32_t)(min(r, N - 1 - col0) * ldb_b) + c * 16;
+    kmax[i] = Kb - c * 16;  // the chunk is live while kb < kmax
+  }
+  // The DMA of a stage goes out in kParts parts, one in each of the first
+  // kParts k-steps of an iteration; part p covers blocks
+  // [p kBlocks / kParts, (p+1) kBlocks / kParts).  With three or more slots
+  // every k-step issues a part.  With two, the stage being loaded is the
+  // very next one, so only the first half of the k-steps issue DMA and the
+  // loads issued last still have two k-steps of MFMAs to land (spreading
+  // over one, two or three k-steps measured within 4% of each other).
+  constexpr int kParts = FRISK_G4_PARTS > 0 ? (FRISK_G4_PARTS < kSteps ? FRISK_G4_PARTS : kSteps)
+                         : (S >= 3 ? kSteps : (kSteps >= 2 ? kSteps / 2 : 1));
+  static_assert(kBlocks >= kParts, "DMA parts");
+  auto issue_part = [&](int stage, int slot, auto part) {
+    constexpr int p = decltype(part)::value;
+    const int kb = stage * KR;
+    char* dst = smem + slot * kStageBytes + wave * kBlocks * 1024;
+#pragma unroll
+    for (int i = p * kBlocks / kParts; i < (p + 1) * kBlocks / kParts; ++i) {
+      const bool live = kb < kmax[i];
+      uint32_t oa = live ? a_off[i] + kb : 0x80000000u;
+      uint32_t ob = live ? b_off[i] + kb : 0x80000000u;
+      // Keep the selects as selects: otherwise the backend may turn them
+      // into branches around two copies of each load.
+      asm("" : "+v"(oa));
+      asm("" : "+v"(ob));
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (lds_ptr_t)(dst + i * 1024), 16, oa, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsb, (lds_ptr_t)(dst + kTileBytes + i * 1024), 16, ob,
+                                               0, 0, 0);
+    }
+  };
+
+  // ---- fragment reads -----------------------------------------------------
+  int fa_off[TM], fb_off[TN], fa_sw[TM], fb_sw[TN];
+#pragma unroll
+  for (int t = 0; t < TM; ++t) {
+    const int r = wm * (32 * TM) + t * 32 + l32;
+    fa_off[t] = r * KR;
+    fa_sw[t] = g4::swz<KR>(r);
+  }
+#pragma unroll
+  for (int t = 0; t < TN; ++t) {
+    const int r = wn * (32 * TN) + t * 32 + l32;
+    fb_off[t] = kTileBytes + r * KR;
+    fb_sw[t] = g4::swz<KR>(r);
+  }
+  using Frag = Frags<TM, TN, kLaneChunks>;
+  auto load_frags = [&](int slot, int s, Frag& f) {
+    const char* base = smem + slot * kStageBytes;
+#pragma unroll
+    for (int j = 0; j < kLaneChunks; ++j) {
+      const int chunk = s * kStepChunks + half * kLaneChunks + j;
+#pragma unroll
+      for (int t = 0; t < TM; ++t)
+        f.a[t][j] = *(const i32x4*)(base + fa_off[t] + ((chunk ^ fa_sw[t]) << 4));
+#pragma unroll
+      for (int t = 0; t < TN; ++t)
+        f.b[t][j] = *(const i32x4*)(base + fb_off[t] + ((chunk ^ fb_sw[t]) << 4));
+    }
+  };
+
+  Acc acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = Acc{};
+  auto mfma_rows = [&](const Frag& f, int i0, int i1) {
+#pragma unroll
+    for (int i = i0; i < i1; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) acc[i][j] = Op::run(f.a[i], f.b[j], acc[i][j]);
+  };
+
+  // ---- pipeline -----------------------------------------------------------
+  // Stage kt lives in slot kt % S.  In the last k-step of stage kt, after
+  // half of its MFMAs, each wave waits for its own loads of stage kt+1 and
+  // for its LDS reads; a workgroup barrier then publishes stage kt+1 and
+  // proves that every wave is done with slot kt % S.  That slot receives
+  // stage kt+S, whose DMA is spread over the first kParts k-steps of
+  // iteration kt+1.  Stage kt+1 is issued during iteration kt+2-S and S-2
+  // newer stages may be in flight at the wait.  Every iteration issues
+  // exactly kLoads loads (past the last stage they are zero-reads without
+  // memory traffic), so the vmcnt bookkeeping is static.
+  const int nk = (Kb + KR - 1) / KR;
+#pragma unroll
+  for (int st = 0; st < S - 1; ++st)
+    static_for<0, kParts>([&](auto p) { issue_part(st, st, p); });
+  FRISK_WAIT_VMCNT(kLoads * (S - 2));
+  __builtin_amdgcn_s_barrier();
+
+  Frag fr[2];
+  load_frags(0, 0, fr[0]);
+  // Drain every LGKM operation issued so far (these fragment reads and the
+  // scalar loads of the epilogue's kernel arguments): with scalar loads
+  // pending at the loop entry the LGKM counter is unordered, and the
+  // compiler would then wait for lgkmcnt(0) at the top of every iteration.
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  int slot = 0, fslot = S - 1;  // slots of stage kt and of stage kt+S-1
+  constexpr int kMf = TM * TN;
+  constexpr int kHalf = kMf / 2;
+  for (int kt = 0; kt < nk; ++kt) {
+    static_for<0, kSteps>([&](auto step) {
+      constexpr int s = decltype(step)::value;
+      constexpr int cur = s & 1, nxt = cur ^ 1;
+      constexpr bool dma = s < kParts;
+      constexpr int nload = dma ? 2 * ((s + 1) * kBlocks / kParts - s * kBlocks / kParts) : 0;
+      if constexpr (s + 1 < kSteps) {
+        // Program order: fragment reads, then DMA (the compiler keeps LDS
+        // reads and LDS-DMA writes in order, as it cannot tell slots apart).
+        load_frags(slot, s + 1, fr[nxt]);
+        if constexpr (dma) issue_part(kt + S - 1, fslot, step);
+        mfma_rows(fr[cur], 0, TM);
+        if constexpr (dma) {
+          // Fragment reads under the first half of the MFMAs, DMA under the
+          // second half.
+          constexpr int kDsG = kFragReads < kHalf ? kFragReads : kHalf;
+          constexpr int kDsPer = (kFragReads + kDsG - 1) / kDsG;
+          constexpr int kVmPer = (nload + (kMf - kDsG) - 1) / (kMf - kDsG);
+          static_for<0, kDsG>([&](auto) {
+            __builtin_amdgcn_sched_group_barrier(0x100, kDsPer, 0);  // DS read
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);       // MFMA
+          });
+          static_for<0, (nload + kVmPer - 1) / kVmPer>([&](auto) {
+            __builtin_amdgcn_sched_group_barrier(0x010, kVmPer, 0);  // VMEM (LDS-DMA)
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);       // MFMA
+          });
+        } else {
+          static_for<0, kFragReads>([&](auto) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+          });
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      } else {
+        if constexpr (dma) {
+          issue_part(kt + S - 1, fslot, step);
+          mfma_rows(fr[cur], 0, TM / 2);
+          constexpr int kVmPer = (nload + kHalf - 1) / kHalf;
+          static_for<0, (nload + kVmPer - 1) / kVmPer>([&](auto) {
+            __builtin_amdgcn_sched_group_barrier(0x010, kVmPer, 0);  // VMEM (LDS-DMA)
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);       // MFMA
+          });
+        } else {
+          mfma_rows(fr[cur], 0, TM / 2);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // vmcnt <= kLoads (S-2) and lgkmcnt = 0.
+        __builtin_amdgcn_s_waitcnt((((kLoads * (S - 2)) & 15) | (((kLoads * (S - 2)) >> 4) << 14) |
+                                    (7 << 4)));
+        __builtin_amdgcn_s_barrier();
+        const int nslot = slot + 1 == S ? 0 : slot + 1;
+        load_frags(nslot, 0, fr[kSteps & 1 ? nxt : 0]);
+        mfma_rows(fr[cur], TM / 2, TM);
+        constexpr int kDsPer = (kFragReads + kHalf - 1) / kHalf;
+        static_for<0, kHalf>([&](auto) {
+          __builtin_amdgcn_sched_group_barrier(0x100, kDsPer, 0);  // DS read
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);       // MFMA
+        });
+        __builtin_amdgcn_sched_barrier(0);
+        fslot = slot;
+        slot = nslot;
+      }
+    });
+    if constexpr (kSteps == 1) fr[0] = fr[1];
+  }
+  // Drain the trailing DMA loads before the stage buffers are reused.
+  FRISK_WAIT_VMCNT(0);
+  __syncthreads();
+
+  // Epilogue: per wave, stage a 32 x 128 slice (one accumulator row block)
+  // as 32-bit values, then each lane stores 8 consecutive columns.  The
+  // 32x32 accumulator holds D[8*(r/4) + 4*(lane/32) + r%4][lane%32] in
+  // element r.
+  constexpr int kPitch = 32 * TN + 4;
+  static_assert(4 * 32 * kPitch * 4 <= g4::lds_bytes(KR, S), "epilogue staging fits in LDS");
+  AccS* stage = (AccS*)(smem + wave * (32 * kPitch * 4));
+  constexpr int kGroups = 32 * TN / 8;  // 8-column groups per staged row
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int rr = 8 * (r >> 2) + 4 * half + (r & 3);
+        stage[rr * kPitch + j * 32 + l32] = acc[i][j][r];
+      }
+    __syncthreads();
+#pragma unroll
+    for (int it = 0; it < 32 * kGroups / 64; ++it) {
+      const int q = it * 64 + lane;
+      const int rr = q / kGroups, g = q % kGroups;
+      const int gr = row0 + wm * (32 * TM) + i * 32 + rr;
+      const int gc = col0 + wn * (32 * TN) + g * 8;
+      if (gr < M && gc < N) {
+        AccS v[8];
+        *(i32x4*)&v[0] = *(const i32x4*)&stage[rr * kPitch + g * 8];
+        *(i32x4*)&v[4] = *(const i32x4*)&stage[rr * kPitch + g * 8 + 4];
+        store8<OUT>(C, (int64_t)gr * ldc + gc, v, accumulate != 0, scale);
+      }
+    }
+    __syncthreads();
+  }
+#endif  // __HIP_DEVICE_COMPILE__
+}
+
+template <Elt IN, Elt OUT>
+static hipError_t launch_w4(const GemmArgs& g, hipStream_t stream) {
+  constexpr int KR = FRISK_G4_KR, S = FRISK_G4_STAGES;
+  constexpr int kEsz = EltInfo<IN>::bytes;
+  constexpr int kLds = g4::lds_bytes(KR, S);
+  static_assert(kLds <= 160 * 1024, "LDS budget of one CU");
+  auto kern = gemm_w4_kernel<IN, OUT, KR, S>;
+  // Thread-safe one-time opt-in to more than 64 KiB of dynamic LDS.
+  static const hipError_t attr =
+      hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
+  if (attr != hipSuccess) return attr;
+  const int tiles = (int)(((g.m + g4::kBT - 1) / g4::kBT) * ((g.n + g4::kBT - 1) / g4::kBT));
+  hipLaunchKernelGGL(kern, dim3(tiles), dim3(g4::kThreads), kLds, stream, (const char*)g.a,
+                     (const char*)g.b, g.c, (int)g.m, (int)g.n, (int)(g.k * kEsz),
+                     g.lda * kEsz, g.ldb * kEsz, g.ldc, g.scale, g.accumulate);
+  return hipGetLastError();
+}
+
+#define FRISK_PAIR(i, o) (((int)(i) << 8) | (int)(o))
+
+hipError_t gemm_tn_w4(const GemmArgs& g, hipStream_t s) {
+  switch (FRISK_PAIR(g.in, g.out)) {
+    case FRISK_PAIR(Elt::BF16, Elt::BF16): return launch_w4<Elt::BF16, Elt::BF16>(g, s);
+    case FRISK_PAIR(Elt::BF16, Elt::F32): return launch_w4<Elt::BF16, Elt::F32>(g, s);
+    case FRISK_PAIR(Elt::F16, Elt::F16): return launch_w4<Elt::F16, Elt::F16>(g, s);
+    case FRISK_PAIR(Elt::F16, Elt::F32): return launch_w4<Elt::F16, Elt::F32>(g, s);
+    case FRISK_PAIR(Elt::E4M3, Elt::BF16): return launch_w4<Elt::E4M3, Elt::BF16>(g, s);
+    case FRISK_PAIR(Elt::E4M3, Elt::F16): return launch_w4<Elt::E4M3, Elt::F16>(g, s);
+    case FRISK_PAIR(Elt::E4M3, Elt::F32): return launch_w4<Elt::E4M3, Elt::F32>(g, s);
+    case FRISK_PAIR(Elt::I8, Elt::I32): return launch_w4<Elt::I8, Elt::I32>(g, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace frisk

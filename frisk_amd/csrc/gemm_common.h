@@ -1,0 +1,125 @@
+// Pieces shared by the MFMA GEMM kernels (gemm.hip, gemm4w.hip): MFMA
+// wrappers, the vmcnt-only wait, the 8-element epilogue store and the
+// fragment bundle.
+#pragma once
+
+#include "common.h"
+
+namespace frisk {
+
+// ---------------------------------------------------------------------------
+// MFMA wrappers.  kBytes = bytes of one operand row consumed by one 32x32
+// MFMA; every lane supplies kBytes/2 of them (lanes 0-31 and 32-63 split the
+// row), as i32x4 chunks.  A and B fragments use the same (lane, byte) -> k
+// assignment, so the k order inside an instruction never matters.
+// ---------------------------------------------------------------------------
+template <Elt E> struct Mfma32;
+
+template <> struct Mfma32<Elt::BF16> {
+  static constexpr int kBytes = 32;
+  using Acc = f32x16;
+  __device__ static inline Acc run(const i32x4* a, const i32x4* b, Acc c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a[0]),
+                                                   __builtin_bit_cast(bf16x8, b[0]), c, 0, 0, 0);
+  }
+};
+
+template <> struct Mfma32<Elt::F16> {
+  static constexpr int kBytes = 32;
+  using Acc = f32x16;
+  __device__ static inline Acc run(const i32x4* a, const i32x4* b, Acc c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a[0]),
+                                                  __builtin_bit_cast(f16x8, b[0]), c, 0, 0, 0);
+  }
+};
+
+template <> struct Mfma32<Elt::E4M3> {
+  static constexpr int kBytes = 64;
+  using Acc = f32x16;
+  __device__ static inline Acc run(const i32x4* a, const i32x4* b, Acc c) {
+    const i32x8 av = {a[0][0], a[0][1], a[0][2], a[0][3], a[1][0], a[1][1], a[1][2], a[1][3]};
+    const i32x8 bv = {b[0][0], b[0][1], b[0][2], b[0][3], b[1][0], b[1][1], b[1][2], b[1][3]};
+    // Format 0 = fp8 e4m3 for both operands; E8M0 block scales 127 = 2^0.
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, bv, c, 0, 0, 0, 127, 0, 127);
+  }
+};
+
+template <> struct Mfma32<Elt::I8> {
+  static constexpr int kBytes = 32;
+  using Acc = i32x16;
+  __device__ static inline Acc run(const i32x4* a, const i32x4* b, Acc c) {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a[0], b[0], c, 0, 0, 0);
+  }
+};
+
+// s_waitcnt with only the vector-memory counter limited to n (gfx9 encoding:
+// vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]).
+#define FRISK_WAIT_VMCNT(n) \
+  __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// Calls f(std::integral_constant<int, i>) for i = I .. N-1, so that the body
+// can use i in constant expressions (builtin arguments, array bounds).
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
+  }
+}
+
+template <Elt OUT, typename AccS>
+__device__ inline void store8(void* c, int64_t idx, const AccS* v, bool accumulate, float scale) {
+  if constexpr (OUT == Elt::I32) {
+    int32_t* p = (int32_t*)c + idx;
+    i32x4 lo = {(int)v[0], (int)v[1], (int)v[2], (int)v[3]};
+    i32x4 hi = {(int)v[4], (int)v[5], (int)v[6], (int)v[7]};
+    if (accumulate) {
+      lo += *(const i32x4*)p;
+      hi += *(const i32x4*)(p + 4);
+    }
+    *(i32x4*)p = lo;
+    *(i32x4*)(p + 4) = hi;
+  } else if constexpr (OUT == Elt::F32) {
+    float* p = (float*)c + idx;
+    f32x4 lo = {v[0] * scale, v[1] * scale, v[2] * scale, v[3] * scale};
+    f32x4 hi = {v[4] * scale, v[5] * scale, v[6] * scale, v[7] * scale};
+    if (accumulate) {
+      lo += *(const f32x4*)p;
+      hi += *(const f32x4*)(p + 4);
+    }
+    *(f32x4*)p = lo;
+    *(f32x4*)(p + 4) = hi;
+  } else {
+    uint16_t* p = (uint16_t*)c + idx;
+    float f[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[i] = v[i] * scale;
+    if (accumulate) {
+      const i32x4 old = *(const i32x4*)p;
+      const uint16_t* o = (const uint16_t*)&old;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if constexpr (OUT == Elt::BF16) f[i] += bf16_bits_to_f32(o[i]);
+        else f[i] += (float)__builtin_bit_cast(_Float16, o[i]);
+      }
+    }
+    uint16_t r[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if constexpr (OUT == Elt::BF16) r[i] = f32_to_bf16_bits(f[i]);
+      else r[i] = __builtin_bit_cast(uint16_t, (_Float16)f[i]);
+    }
+    *(i32x4*)p = *(const i32x4*)r;
+  }
+}
+
+// MFMA operand fragments of one k-step: TM A tiles and TN B tiles.
+template <int TM, int TN, int LC>
+struct Frags {
+  i32x4 a[TM][LC];
+  i32x4 b[TN][LC];
+};
+
+}  // namespace frisk

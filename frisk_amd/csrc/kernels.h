@@ -27,6 +27,9 @@ struct GemmArgs {
 // 256x256-tile MFMA kernel; requires trans_a == 0, trans_b == 1 and 16 B
 // aligned, K-contiguous rows (checked by the caller).
 hipError_t gemm_tn_mfma(const GemmArgs& g, hipStream_t s);
+// 256x256-tile kernel with four 128x128 waves (gemm4w.hip); same operand
+// contract as gemm_tn_mfma.
+hipError_t gemm_tn_w4(const GemmArgs& g, hipStream_t s);
 // Any layout / shape; LDS-tiled FMA kernel.
 hipError_t gemm_generic_any(const GemmArgs& g, hipStream_t s);
 // Small-M kernel (M <= kSkinnyMaxM, bf16/f16, trans_a == 0, trans_b == 1,

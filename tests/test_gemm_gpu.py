@@ -127,6 +127,38 @@ def test_small_m_kernel(m, n, k, in_dt, out_dt):
     check(decode(c), reference(a, b, False, True, 1.0, 1.0) + decode(c0), in_dt, out_dt)
 
 
+BIG_RAGGED = [(4000, 2056, 1000, torch.bfloat16, torch.bfloat16),
+              (4096, 4104, 776, torch.float16, torch.float32),
+              (3000, 3000, 2000, FP8, torch.float32),
+              (3000, 3000, 2000, FP8, torch.bfloat16),
+              (4000, 2056, 1008, torch.int8, torch.int32)]
+
+
+@pytest.mark.parametrize("m,n,k,in_dt,out_dt", BIG_RAGGED,
+                         ids=lambda x: str(x).replace("torch.", ""))
+def test_large_tiles_ragged(m, n, k, in_dt, out_dt):
+    # At least 128 tiles of 256x256: the four-wave 256x256 kernel, with
+    # partial edge tiles in M and N and a K tail inside the last 128-byte
+    # stage; first overwriting C, then accumulating into it.
+    print(f"case large m={m} n={n} k={k} {in_dt}->{out_dt}", flush=True)
+    a, b, sa, sb = make_operands(m, n, k, in_dt, False, True, seed=m + k)
+    r = sample_rows(m, 40, seed=k)
+    rows = torch.from_numpy(r).cuda()
+    ref = reference(a, b, False, True, sa, sb, rows=r)
+    c = torch.empty(m, n, dtype=out_dt, device="cuda")
+    rt.gemm(a, b, c, trans_b=True, scale_a=sa, scale_b=sb)
+    torch.cuda.synchronize()
+    check(decode(c[rows]), ref, in_dt, out_dt)
+    if out_dt == torch.int32:
+        c0 = torch.randint(-1000, 1000, (m, n), dtype=torch.int32, device="cuda")
+    else:
+        c0 = randn((m, n), 11).to(out_dt)
+    c = c0.clone()
+    rt.gemm(a, b, c, trans_b=True, clear_accum=False, scale_a=sa, scale_b=sb)
+    torch.cuda.synchronize()
+    check(decode(c[rows]), ref + decode(c0[rows]), in_dt, out_dt)
+
+
 @pytest.mark.parametrize("m,n,k", [(1024, 4096, 4096), (512, 640, 1000), (300, 1000, 72)])
 def test_mid_size_tiles(m, n, k):
     # Fewer than 128 tiles of 256x256: the 128x128-tile configuration.
