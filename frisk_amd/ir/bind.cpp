@@ -18,6 +18,7 @@
 #include <numeric>
 
 #include "layout.h"
+#include "infer.h"
 #include "normalize.h"
 #include "ops.h"
 
@@ -125,7 +126,7 @@ py::object attrToPython(const Attribute& a) {
     case AttrKind::Bool: return py::bool_(a->b);
     case AttrKind::Integer: return py::int_(a->i);
     case AttrKind::Float: return py::float_(a->f);
-    case AttrKind::String: return py::str(a->s);
+    case AttrKind::String: case AttrKind::Opaque: return py::str(a->s);
     case AttrKind::TypeA: return wrapType(a->type);
     case AttrKind::DenseI64Array: return py::cast(a->ints);
     case AttrKind::AffineMapA: return py::cast(a->map);
@@ -822,6 +823,27 @@ void bindBuilder(py::module_& m) {
       .def("get_float_attr", [](PyBuilder& b, float v, const std::string& dtype) {
         return PyAttr{Attribute::floating(floatAttrType(b.b.context(), dtype), v)};
       })
+      // Extensions for building tensor-form IR directly (the form
+      // frisk.normalize_layout_ir produces and layout inference consumes).
+      .def("get_i64_array_attr", [](PyBuilder&, std::vector<int64_t> v) {
+        return PyAttr{Attribute::denseI64(std::move(v))};
+      })
+      .def("get_dense_splat_attr", [](PyBuilder&, const PyType& tensor, double v) {
+        if (!tensor.t.isTensor()) throw InvalidArgument("dense splat needs a tensor type");
+        if (tensor.t.elementType().isFloat()) return PyAttr{Attribute::denseFloat(tensor.t, {v})};
+        return PyAttr{Attribute::denseInt(tensor.t, {(int64_t)v})};
+      })
+      .def("create_op", [](PyBuilder& b, const std::string& name, std::vector<PyValue> operands,
+                           std::vector<PyType> resultTypes, std::map<std::string, PyAttr> attrs) {
+        std::vector<Value> ops;
+        for (auto& v : operands) ops.push_back(v.v);
+        std::vector<Type> tys;
+        for (auto& t : resultTypes) tys.push_back(t.t);
+        std::vector<NamedAttr> na;
+        for (auto& kv : attrs) na.push_back({kv.first, kv.second.a});
+        return PyOpState{b.b.create(name, ops, tys, na)};
+      }, py::arg("name"), py::arg("operands"), py::arg("result_types"),
+         py::arg("attrs") = std::map<std::string, PyAttr>{})
       // Constants.
       .def("get_int64", [](PyBuilder& b, int64_t v) {
         Type t = b.b.context()->integer(64);
@@ -1199,6 +1221,71 @@ void bindFrisk(py::module_& m) {
     std::string err = normalizeLegacyFragments(requireOp(mod));
     if (!err.empty()) throw InvalidArgument(err);
   }, py::arg("module"), py::arg("target") = py::none());
+
+  // Pass: frisk-infer-layouts for gfx950 (layout inference, cost model,
+  // materialization).  Returns the solver report as a dict.
+  m.def("infer_layouts", [](PyModule& mod, std::optional<std::string> target, int64_t exactLimit,
+                            int64_t beamWidth, int64_t maxExpanded, bool analysisOnly,
+                            std::optional<std::string> costProfile) {
+    Operation* op = requireOp(mod);
+    if (target) op->setAttr("frisk.target", Attribute::string(*target));
+    InferOptions o;
+    o.exactCombinationLimit = exactLimit;
+    o.beamWidth = beamWidth;
+    o.maxExpandedStates = maxExpanded;
+    o.analysisOnly = analysisOnly;
+    if (costProfile) o.profile = CostProfile::fromJson(*costProfile);
+    InferReport r = inferLayouts(op, o);
+    if (r.status == "failed") throw InvalidArgument(r.failure.empty() ? "layout-inference failed" : r.failure);
+    py::dict d;
+    d["status"] = r.status;
+    d["method"] = r.method;
+    d["cost_model"] = r.costModelId;
+    d["cost"] = r.cost;
+    d["variables"] = r.variables;
+    d["combinations"] = r.combinations;
+    d["expanded"] = r.expanded;
+    d["conversions_inserted"] = r.conversionsInserted;
+    d["features"] = r.features;
+    d["assignments"] = r.assignments;
+    d["conversions"] = r.conversions;
+    d["graph"] = r.graph;
+    return d;
+  }, py::arg("module"), py::arg("target") = py::none(), py::arg("exact_combination_limit") = 256,
+     py::arg("beam_width") = 32, py::arg("max_expanded_states") = 65536,
+     py::arg("analysis_only") = false, py::arg("cost_profile") = py::none());
+  // Pass: frisk-export-execution -> the execution packet as JSON text.
+  m.def("export_execution", [](PyModule& mod) {
+    std::string err;
+    std::string out = exportExecution(requireOp(mod), &err);
+    if (out.empty()) throw InvalidArgument(err);
+    return out;
+  }, py::arg("module"));
+  m.def("cost_profile_defaults", []() {
+    CostProfile p = CostProfile::defaults();
+    py::dict d;
+    d["id"] = p.id;
+    d["weights"] = p.weights;
+    return d;
+  });
+  m.def("mma_bindings", [](int64_t mm, int64_t n, int64_t k, const PyType& in, const PyType& acc,
+                           int64_t threads) {
+    py::list out;
+    for (const MmaBinding& b : cdna4MmaBindings(mm, n, k, in.t, acc.t, threads)) {
+      py::dict d;
+      d["atom"] = std::string(b.hw.atom.name);
+      d["wave_grid"] = std::vector<int64_t>{b.hw.gM, b.hw.gN};
+      d["swapped"] = b.swapped;
+      d["contract"] = b.str();
+      d["a"] = b.operand('A').str();
+      d["b"] = b.operand('B').str();
+      d["c"] = b.operand('C').str();
+      d["mfma_per_wave"] = b.mfmaPerWave();
+      out.append(d);
+    }
+    return out;
+  }, py::arg("m"), py::arg("n"), py::arg("k"), py::arg("in_type"), py::arg("acc_type"),
+     py::arg("threads") = 256);
 
   bindLayout(m);
 }

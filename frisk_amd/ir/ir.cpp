@@ -700,6 +700,11 @@ Attribute Attribute::string(std::string s) {
   p->s = std::move(s);
   return Attribute(p);
 }
+Attribute Attribute::opaque(std::string text) {
+  auto p = newAttr(AttrKind::Opaque);
+  p->s = std::move(text);
+  return Attribute(p);
+}
 Attribute Attribute::typeAttr(Type t) {
   auto p = newAttr(AttrKind::TypeA);
   p->type = t;
@@ -758,7 +763,7 @@ bool Attribute::operator==(const Attribute& o) const {
     case AttrKind::Float:
       return a.type == b.type && floatBits(a.type.impl()->fkind, a.f) ==
                                      floatBits(b.type.impl()->fkind, b.f);
-    case AttrKind::String: return a.s == b.s;
+    case AttrKind::String: case AttrKind::Opaque: return a.s == b.s;
     case AttrKind::TypeA: return a.type == b.type;
     case AttrKind::DenseI64Array: return a.ints == b.ints;
     case AttrKind::AffineMapA: return a.map == b.map;
@@ -784,6 +789,7 @@ std::string Attribute::str() const {
       os << formatFloat(a.type.impl()->fkind, a.f) << " : " << a.type.str();
       break;
     case AttrKind::String: os << escapeString(a.s); break;
+    case AttrKind::Opaque: os << a.s; break;
     case AttrKind::TypeA: os << a.type.str(); break;
     case AttrKind::DenseI64Array:
       os << "array<i64";

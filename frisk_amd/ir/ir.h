@@ -240,7 +240,8 @@ class Type {
 // ----------------------------------------------------------------------------
 enum class AttrKind : uint8_t {
   Unit, Bool, Integer, Float, String, TypeA, DenseI64Array, AffineMapA, MemorySpaceA,
-  GemmPolicyA, DenseFloat, DenseInt
+  GemmPolicyA, DenseFloat, DenseInt,
+  Opaque  // a dialect attribute kept as its textual form, printed verbatim
 };
 
 struct AttrStorage {
@@ -273,6 +274,7 @@ class Attribute {
   // nearest even, saturating fp8 kinds like their finite-only encodings).
   static Attribute floating(Type t, double v);
   static Attribute string(std::string s);
+  static Attribute opaque(std::string text);
   static Attribute typeAttr(Type t);
   static Attribute denseI64(std::vector<int64_t> v);
   static Attribute affineMap(AffineMap m);

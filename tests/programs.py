@@ -122,3 +122,62 @@ def attention(Bt, H, S, D, BM=64, BN=64, dtype="bf16", k_transposed=False, threa
     else:
         b.create_copy_op(acc_o, O, [], [bz, by, bx], empty, omap, [BM, D], [1, 1, BM, D])
     return s, kernel
+
+
+def attention_tensor_form(M=64, N=64, D=16, dtype="fp16", threads=128, scale=0.25,
+                          name="attention"):
+    """The tensor-form (normalized) attention tile program that layout
+    inference consumes: the structure of the reference's
+    test/Transforms/attention-layout.mlir (Q.K^T, scale, row max, exp, row
+    sum, divide, truncate, P.V, store), built with the generic op builder."""
+    s = F.create_session()
+    b = s.builder
+    G, SH = F.MemorySpace.GLOBAL, F.MemorySpace.SHARED
+    in_ty = {"fp16": b.get_f16_ty(), "bf16": b.get_bf16_ty()}[dtype]
+    f32 = b.get_f32_ty()
+    mq = s.memref_type([M, D], dtype, space=G)
+    mk = s.memref_type([N, D], dtype, space=G)
+    mo = s.memref_type([M, D], "fp32", space=G)
+    kernel, entry = s.new_kernel(name, [mq, mk, mk, mo])
+    q, k, v, o = (entry.get_argument(i) for i in range(4))
+    i64 = lambda x: b.get_int64_attr(x)
+    sq = s.memref_type([M, D], dtype, space=SH)
+    sk = s.memref_type([N, D], dtype, space=SH)
+    par = b.create_parallel_op([1], threads)
+    pb = par.add_entry_block()
+    b.set_insertion_point_to_start(pb)
+    qs = b.create_op("memref.alloc", [], [sq], {"alignment": i64(1024)}).get_result(0)
+    ks = b.create_op("memref.alloc", [], [sk], {"alignment": i64(1024)}).get_result(0)
+    vs = b.create_op("memref.alloc", [], [sk], {"alignment": i64(1024)}).get_result(0)
+    view = lambda x, t: b.create_op("frisk.layout_view", [x], [t]).get_result(0)
+    qg, kg, vg = view(q, mq), view(k, mk), view(v, mk)
+    qv, kv, vv = view(qs, sq), view(ks, sk), view(vs, sk)
+    empty = b.get_empty_affine_map()
+    for src, dst, rows in ((qg, qv, M), (kg, kv, N), (vg, vv, N)):
+        b.create_copy_op(src, dst, [], [], empty, empty, [rows, D], [rows, D])
+    t2 = lambda r, c, e: b.get_ranked_tensor_ty(e, [r, c])
+    t1 = lambda r, e: b.get_ranked_tensor_ty(e, [r])
+    const = lambda ty, x: b.create_op("arith.constant", [], [ty],
+                                      {"value": b.get_dense_splat_attr(ty, x)}).get_result(0)
+    op = lambda n, ins, ty, attrs=None: b.create_op(n, ins, [ty], attrs or {}).get_result(0)
+    zero = const(t2(M, N, f32), 0.0)
+    scores = op("frisk.mma", [qv, kv, zero], t2(M, N, f32),
+                {"m": i64(M), "n": i64(N), "k": i64(D), "trans_a": b.get_bool_attr(False),
+                 "trans_b": b.get_bool_attr(True)})
+    scaled = op("arith.mulf", [scores, const(t2(M, N, f32), scale)], t2(M, N, f32))
+    mx = op("frisk.reduce_tensor", [scaled], t1(M, f32), {"kind": b.get_str_attr("max"), "dim": i64(1)})
+    e0 = op("tensor.empty", [], t2(M, N, f32))
+    bm = op("linalg.broadcast", [mx, e0], t2(M, N, f32), {"dimensions": b.get_i64_array_attr([1])})
+    centered = op("arith.subf", [scaled, bm], t2(M, N, f32))
+    ex = op("math.exp", [centered], t2(M, N, f32))
+    sm = op("frisk.reduce_tensor", [ex], t1(M, f32), {"kind": b.get_str_attr("sum"), "dim": i64(1)})
+    e1 = op("tensor.empty", [], t2(M, N, f32))
+    bs = op("linalg.broadcast", [sm, e1], t2(M, N, f32), {"dimensions": b.get_i64_array_attr([1])})
+    normalized = op("arith.divf", [ex, bs], t2(M, N, f32))
+    p = op("arith.truncf", [normalized], t2(M, N, in_ty))
+    ozero = const(t2(M, D, f32), 0.0)
+    result = op("frisk.mma", [p, vv, ozero], t2(M, D, f32),
+                {"m": i64(M), "n": i64(D), "k": i64(N), "trans_a": b.get_bool_attr(False),
+                 "trans_b": b.get_bool_attr(False)})
+    b.create_op("frisk.tile_store", [result, view(o, mo)], [])
+    return s, kernel
