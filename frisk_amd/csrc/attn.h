@@ -215,10 +215,8 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(
     v_row[i] = ((wave * kVI + i) < kVIns && c * 8 < D) ? r : 1 << 30;
     v_off[i] = (uint32_t)(r * v_ss * 2) + (c << 4);
   }
-  auto issue_kv = [&](int kb, int buf) {
-    char* dst = smem + buf * G::kBuf;
+  auto issue_k = [&](int kb, char* dst) {
     const uint32_t kbase = (uint32_t)((int64_t)kb * kBN * k_ss * 2);
-    const uint32_t vbase = (uint32_t)((int64_t)kb * kBN * v_ss * 2);
 #pragma unroll
     for (int i = 0; i < kKI; ++i) {
       if ((wave * kKI + i) >= kKIns) continue;  // wave-uniform
@@ -227,6 +225,9 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(
                                                r < seq_k ? kbase + k_off[i] : 0x80000000u, 0,
                                                0, 0);
     }
+  };
+  auto issue_v = [&](int kb, char* dst) {
+    const uint32_t vbase = (uint32_t)((int64_t)kb * kBN * v_ss * 2);
 #pragma unroll
     for (int i = 0; i < kVI; ++i) {
       if ((wave * kVI + i) >= kVIns) continue;  // wave-uniform
@@ -235,6 +236,11 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(
           rsv, (lds_ptr_t)(dst + G::kKTile + (wave * kVI + i) * 1024), 16,
           r < seq_k ? vbase + v_off[i] : 0x80000000u, 0, 0, 0);
     }
+  };
+  auto issue_kv = [&](int kb, int buf) {
+    char* dst = smem + buf * G::kBuf;
+    issue_k(kb, dst);
+    issue_v(kb, dst);
   };
 
   // ---- V^T fragments by transposing LDS reads ------------------------------
@@ -266,80 +272,40 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(
     for (int dt = 0; dt < G::kDT; ++dt) o[t][dt] = f32x16{};
   }
 
-  if (nkb > 0) {
-    issue_kv(0, 0);
-    FRISK_WAIT_VMCNT0();
-    __syncthreads();
-  }
-  // Drain the scalar loads of kernel arguments used after the loop: with
-  // them pending at loop entry the LGKM counter is unordered and every LDS
-  // read in the loop would be waited for with lgkmcnt(0).
-  __builtin_amdgcn_s_waitcnt(0xC07F);
-
-  // One key block: S^T = K.Q^T, online softmax, O^T += V^T.P^T.  Masked
-  // blocks (the sequence tail, and blocks crossing this wave's causal
-  // diagonal) apply the key mask; every other block runs without it.
-  auto key_block = [&](const char* ks, int kbase, auto masked_tag) {
-    constexpr bool kMasked = decltype(masked_tag)::value;
-    // S^T: two 32-key tiles x QT query tiles, 8 head-dim steps, in two
-    // halves of 4 steps: the 8 K fragments of a half are read together
-    // (one LDS latency per half, not per MFMA) and the second half's reads
-    // issue under the first half's MFMAs.  The first half of the V^T
-    // fragments is read before the softmax, whose VALU work hides it.
-    auto read_k = [&](int h0, auto& kf) {
-      constexpr int n = sizeof(kf[0]) / sizeof(kf[0][0]);
+  // ---- building blocks ----------------------------------------------------
+  // K fragments of head-dim steps h0 .. h0+n-1 for both 32-key tiles.
+  auto read_k = [&](const char* ks, int h0, auto& kf) {
+    constexpr int n = sizeof(kf[0]) / sizeof(kf[0][0]);
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-        const int r = kt * 32 + l32;
+    for (int kt = 0; kt < 2; ++kt) {
+      const int r = kt * 32 + l32;
 #pragma unroll
-        for (int i = 0; i < n; ++i)
-          kf[kt][i] =
-              *(const i32x4*)(ks + r * G::kRB + (((2 * (h0 + i) + half) ^ G::swz_k(r)) << 4));
-      }
-    };
-    auto read_v = [&](int k0, i32x4 (&vf)[2][G::kDT]) {
-      typedef short s16x4 __attribute__((ext_vector_type(4)));
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int dt = 0; dt < G::kDT; ++dt) {
-          const char* p = ks + vt_off[dt] + (k0 + i) * 16 * G::kRV;
-          const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((s16x4*)p);
-          const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((s16x4*)(p + 8 * G::kRV));
-          typedef int i32x2 __attribute__((ext_vector_type(2)));
-          const i32x2 a = __builtin_bit_cast(i32x2, lo), b = __builtin_bit_cast(i32x2, hi);
-          vf[i][dt] = i32x4{a[0], a[1], b[0], b[1]};
-        }
-    };
-    f32x16 s[QT][2];
-#pragma unroll
-    for (int t = 0; t < QT; ++t) s[t][0] = s[t][1] = f32x16{};
-    i32x4 kf0[2][G::kH1], kf1[2][G::kH2 > 0 ? G::kH2 : 1];
-    read_k(0, kf0);
-    __builtin_amdgcn_sched_barrier(0);
-    if constexpr (G::kH2 > 0) read_k(G::kH1, kf1);
-#pragma unroll
-    for (int i = 0; i < G::kH1; ++i)
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int t = 0; t < QT; ++t) s[t][kt] = Mf::run(kf0[kt][i], qf[t][i], s[t][kt]);
-    __builtin_amdgcn_sched_barrier(0);
-    i32x4 vf0[2][G::kDT], vf1[2][G::kDT];
-    read_v(0, vf0);
-    if constexpr (G::kH2 > 0) {
-#pragma unroll
-      for (int i = 0; i < G::kH2; ++i)
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-          for (int t = 0; t < QT; ++t)
-            s[t][kt] = Mf::run(kf1[kt][i], qf[t][G::kH1 + i], s[t][kt]);
+      for (int i = 0; i < n; ++i)
+        kf[kt][i] =
+            *(const i32x4*)(ks + r * G::kRB + (((2 * (h0 + i) + half) ^ G::swz_k(r)) << 4));
     }
-    __builtin_amdgcn_sched_barrier(0);
-    // Online softmax in the exp2 domain: p = exp2(s * scale_log2 - m).
-    // The max is taken on raw scores (scale_log2 > 0 commutes with max).
-    i32x4 pf[QT][4];
+  };
+  // V^T fragments of key steps k0, k0+1 (16 keys each).
+  auto read_v = [&](const char* ks, int k0, i32x4 (&vf)[2][G::kDT]) {
+    typedef short s16x4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int dt = 0; dt < G::kDT; ++dt) {
+        const char* p = ks + vt_off[dt] + (k0 + i) * 16 * G::kRV;
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((s16x4*)p);
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((s16x4*)(p + 8 * G::kRV));
+        typedef int i32x2 __attribute__((ext_vector_type(2)));
+        const i32x2 a = __builtin_bit_cast(i32x2, lo), b = __builtin_bit_cast(i32x2, hi);
+        vf[i][dt] = i32x4{a[0], a[1], b[0], b[1]};
+      }
+  };
+  // Online softmax of one key block in the exp2 domain:
+  // p = exp2(s * scale_log2 - m).  The max is taken on raw scores
+  // (scale_log2 > 0 commutes with max).  Masked blocks (the sequence tail,
+  // and blocks crossing this wave's causal diagonal) apply the key mask.
+  auto softmax = [&](f32x16 (&s)[QT][2], i32x4 (&pf)[QT][4], int kbase, auto masked_tag) {
+    constexpr bool kMasked = decltype(masked_tag)::value;
 #pragma unroll
     for (int t = 0; t < QT; ++t) {
       if constexpr (kMasked) {
@@ -387,9 +353,63 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(
       }
       l[t] = rs;
     }
+  };
+
+  // Key blocks [0, n_plain) need no mask for any wave of this workgroup
+  // (they end at or before wave 0's causal diagonal and the sequence end);
+  // the remaining few run the masked variant.
+  int n_plain = seq_k / kBN;
+  if (CAUSAL) n_plain = min(n_plain, max(0, (q0 + diag + 1) / kBN));
+  n_plain = min(n_plain, nkb);
+
+  if (nkb > 0) {
+    issue_kv(0, 0);
+    FRISK_WAIT_VMCNT0();
+    __syncthreads();
+  }
+  // Drain the scalar loads of kernel arguments used after the loop: with
+  // them pending at loop entry the LGKM counter is unordered and every LDS
+  // read in the loop would be waited for with lgkmcnt(0).
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+
+  // One key block: S^T = K.Q^T, online softmax, O^T += V^T.P^T.  S^T runs
+  // in two halves of the head-dim steps: the K fragments of a half are
+  // read together (one LDS latency per half, not per MFMA) and the second
+  // half's reads issue under the first half's MFMAs.  The first half of
+  // the V^T fragments is read before the softmax, whose VALU work hides
+  // it.
+  auto key_block = [&](const char* ks, int kbase, auto masked_tag) {
+    f32x16 s[QT][2];
+#pragma unroll
+    for (int t = 0; t < QT; ++t) s[t][0] = s[t][1] = f32x16{};
+    i32x4 kf0[2][G::kH1], kf1[2][G::kH2 > 0 ? G::kH2 : 1];
+    read_k(ks, 0, kf0);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (G::kH2 > 0) read_k(ks, G::kH1, kf1);
+#pragma unroll
+    for (int i = 0; i < G::kH1; ++i)
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int t = 0; t < QT; ++t) s[t][kt] = Mf::run(kf0[kt][i], qf[t][i], s[t][kt]);
+    __builtin_amdgcn_sched_barrier(0);
+    i32x4 vf0[2][G::kDT], vf1[2][G::kDT];
+    read_v(ks, 0, vf0);
+    if constexpr (G::kH2 > 0) {
+#pragma unroll
+      for (int i = 0; i < G::kH2; ++i)
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int t = 0; t < QT; ++t)
+            s[t][kt] = Mf::run(kf1[kt][i], qf[t][G::kH1 + i], s[t][kt]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    i32x4 pf[QT][4];
+    softmax(s, pf, kbase, masked_tag);
     // O^T += V^T . P^T over 4 key steps of 16; the second half of the V^T
     // fragments is read under the first half's MFMAs.
-    read_v(2, vf1);
+    read_v(ks, 2, vf1);
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -405,13 +425,6 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(
         for (int t = 0; t < QT; ++t) o[t][dt] = Mf::run(vf1[i][dt], pf[t][2 + i], o[t][dt]);
   };
 
-  // Key blocks [0, n_plain) need no mask for any wave of this workgroup
-  // (they end at or before wave 0's causal diagonal and the sequence end);
-  // the remaining few run the masked variant.  Two loops keep the mask code
-  // out of the main loop.
-  int n_plain = seq_k / kBN;
-  if (CAUSAL) n_plain = min(n_plain, max(0, (q0 + diag + 1) / kBN));
-  n_plain = min(n_plain, nkb);
   auto step = [&](int j, auto masked_tag) {
     const int buf = j & 1;
     const bool more = j + 1 < nkb;
