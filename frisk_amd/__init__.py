@@ -7,6 +7,8 @@ submodule with its op classes, ...) plus FriskHelper, create_context and
 create_session.  On top of that:
 
 execute  -- run a GEMM / attention tile program on the GPU (C-ABI)
+execute_packet / plan_packet -- run an execution packet written by
+            frisk.export_execution (after frisk.infer_layouts)
 runtime  -- ctypes binding of libfrisk_hip.so (include/frisk_hip.h)
 build    -- ahead-of-time build of libfrisk_hip.so (hipcc, gfx950) and of
             the frisk_ffi extension (g++, pybind11)
@@ -48,6 +50,9 @@ def __getattr__(name: str):
     if name == "execute":
         from .executor import execute
         return execute
+    if name in ("execute_packet", "plan_packet"):
+        from . import packet
+        return getattr(packet, name)
     if name.startswith("__") or name == "frisk_ffi":
         raise AttributeError(name)
     ir = _ir()
@@ -57,7 +62,7 @@ def __getattr__(name: str):
 
 
 def __dir__():
-    names = set(globals()) | set(_HELPERS) | {"execute"}
+    names = set(globals()) | set(_HELPERS) | {"execute", "execute_packet", "plan_packet"}
     try:
         names |= {n for n in dir(_ir()) if not n.startswith("_")}
     except ImportError:

@@ -1428,7 +1428,20 @@ std::string exportExecution(Operation* module, std::string* error) {
         err = "export: " + op->name + " result has no materialized layout";
     }
     ops << (firstOp ? "" : ",") << "\n  {\"name\": \"" << op->name << "\", \"operands\": " << ints(in)
-        << ", \"results\": " << ints(out) << ", \"attrs\": {";
+        << ", \"results\": " << ints(out);
+    if (op->numRegions()) {
+      ops << ", \"region_args\": [";
+      bool fb = true;
+      for (auto& r : op->regions)
+        for (auto& blk : r->blocks) {
+          std::vector<int64_t> args;
+          for (unsigned i = 0; i < blk->numArguments(); ++i) args.push_back(id(blk->argument(i)));
+          ops << (fb ? "" : ",") << ints(args);
+          fb = false;
+        }
+      ops << "]";
+    }
+    ops << ", \"attrs\": {";
     firstOp = false;
     bool fa = true;
     for (auto& na : op->attrs) {

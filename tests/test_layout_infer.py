@@ -284,3 +284,35 @@ def test_export_requires_materialized_layouts():
     s = _gemm_module()
     with pytest.raises(ValueError, match="not materialized"):
         F.frisk.export_execution(s.module)
+
+
+# ---- packet consumer (plan on CPU) ------------------------------------------
+
+def _packet(s):
+    F.frisk.infer_layouts(s.module)
+    return F.frisk.export_execution(s.module)
+
+
+def test_plan_packet_attention_and_gemm():
+    p = F.plan_packet(_packet(_attention(64, 64, 16, 128, dtype="fp16")))
+    assert p["kind"] == "attention" and p["scale"] == 0.25 and p["head_dim"] == 16
+    assert (p["q"], p["k"], p["v"], p["o"]) == (0, 1, 2, 3)
+    assert p["layouts_match"] is False  # head_dim 16: the packet converts P, the kernel pads V
+    p = F.plan_packet(_packet(_attention(256, 64, 128, 512)))
+    assert p["kind"] == "attention" and p["layouts_match"] is True
+    g = F.plan_packet(_packet(_gemm_module()))
+    assert g["kind"] == "gemm" and (g["a"], g["b"], g["c"]) == (0, 1, 2)
+    assert (g["m"], g["n"], g["k"]) == (64, 64, 16) and not g["trans_a"] and not g["trans_b"]
+
+
+def test_plan_packet_rejects_other_programs():
+    pk = json.loads(_packet(_attention(64, 64, 16, 128, dtype="fp16")))
+    ops = pk["operations"]
+    ex = next(i for i, o in enumerate(ops) if o["name"] == "math.exp")
+    ops[ex]["name"] = "math.exp2"
+    with pytest.raises(ValueError, match="not a GEMM or attention"):
+        F.plan_packet(pk)
+    pk = json.loads(_packet(_attention(64, 64, 16, 128, dtype="fp16")))
+    pk["target"] = "sm_90a"
+    with pytest.raises(ValueError, match="schema_version 1 for target gfx950"):
+        F.plan_packet(pk)

@@ -1,0 +1,75 @@
+"""Execution packets (frisk.export_execution after frisk.infer_layouts) run on
+the MI355X through F.execute_packet, checked against the fp64 oracle.
+
+The 64x16 attention case is the reference's fixed-ABI fixture shape
+(test/Transforms/attention-layout-fixed-abi.mlir:45-94, Q/K/V 64x16 f16,
+scale 0.25, O f32) with the tolerance of run_execution.py:85
+(|err| <= 0.002 + 0.002 |ref|)."""
+import numpy as np
+import pytest
+import torch
+
+import frisk_amd as F
+from oracle import attention as A
+from oracle import gemm as G
+from tests import programs as P
+from tests.gpu_util import decode, randn
+
+pytestmark = pytest.mark.gpu
+
+
+def _packet(M, N, D, dtype, threads):
+    s, _ = P.attention_tensor_form(M=M, N=N, D=D, dtype=dtype, threads=threads)
+    s.module.set_attr("frisk.target", s.builder.get_str_attr("gfx950"))
+    F.frisk.infer_layouts(s.module)
+    return F.frisk.export_execution(s.module)
+
+
+@pytest.mark.parametrize("M,N,D,dtype,threads", [(64, 64, 16, "fp16", 128), (128, 64, 64, "bf16", 256),
+                                                  (256, 128, 128, "bf16", 512)])
+def test_attention_packet(M, N, D, dtype, threads):
+    print(f"case packet attention M={M} N={N} D={D} {dtype}", flush=True)
+    tdt = torch.float16 if dtype == "fp16" else torch.bfloat16
+    g = torch.Generator(device="cuda")
+    g.manual_seed(M + N + D)
+    q, k, v = ((torch.rand(n, D, generator=g, device="cuda") * 2 - 1).to(tdt) for n in (M, N, N))
+    o = torch.full((M, D), float("nan"), dtype=torch.float32, device="cuda")
+    plan = F.execute_packet(_packet(M, N, D, dtype, threads), [q, k, v, o])
+    torch.cuda.synchronize()
+    assert plan["kind"] == "attention" and plan["scale"] == 0.25
+    qd, kd, vd = decode(q), decode(k), decode(v)
+    ref = A.attention_fp64(qd[None, None], kd[None, None], vd[None, None], scale=0.25)[0][0, 0]
+    err = np.abs(decode(o) - ref)
+    if dtype == "fp16":
+        # The reference fixture's tolerance (run_execution.py:85).
+        assert np.all(err <= 0.002 + 0.002 * np.abs(ref)), err.max()
+    else:
+        # P enters the PV product in bf16 (unit roundoff u = 2^-8) and the
+        # row sum uses the same rounded P, so each normalized weight moves by
+        # at most 2u w_j: |err| <= 2^-7 sum_j w_j |v_j| plus f32 noise.
+        s = 0.25 * qd @ kd.T
+        w = np.exp(s - s.max(axis=1, keepdims=True))
+        w /= w.sum(axis=1, keepdims=True)
+        assert np.all(err <= 2.0 ** -7 * (w @ np.abs(vd)) + 1e-6), err.max()
+
+
+def test_gemm_packet():
+    s = F.create_session()
+    S = F.MemorySpace.SHARED
+    _, entry = s.new_kernel("gemm", [s.memref_type([64, 32], "bf16", space=S),
+                                     s.memref_type([32, 64], "bf16", space=S),
+                                     s.memref_type([64, 64], "fp32")])
+    c = s.alloc_buffer([64, 64], "fp32")
+    s.create_gemm(entry.get_argument(0), entry.get_argument(1), c, clear_accum=True,
+                  legacy_semantics="tensor_v1")
+    s.builder.create_copy_op(c, entry.get_argument(2), [], [])
+    F.frisk.normalize_layout_ir(s.module, "gfx950")
+    F.frisk.infer_layouts(s.module)
+    a = randn((64, 32), 1).to(torch.bfloat16)
+    b = randn((32, 64), 2).to(torch.bfloat16)
+    out = torch.full((64, 64), float("nan"), dtype=torch.float32, device="cuda")
+    plan = F.execute_packet(F.frisk.export_execution(s.module), [a, b, out])
+    torch.cuda.synchronize()
+    assert plan["kind"] == "gemm"
+    ref = decode(a) @ decode(b)
+    assert G.row_scaled_error(decode(out), ref) <= 1e-5
