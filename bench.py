@@ -10,7 +10,11 @@ metric names, each timed the same way (W warm-up launches, then K timed
 launches between device synchronisations): fp16 4096^3 NT,
 fp8-e4m3 4096x8192x8192 with per-tensor scales, int8 4096^3,
 and the flash-attention forward at b4 h32 s4096 d128 bf16, non-causal and
-causal (configs[4]; causal FLOPs counted as half).
+causal (configs[4]; causal FLOPs counted as half).  The HBM-bound tile ops
+on either side of them (frisk_reduce, frisk_copy with an f32 -> bf16
+conversion, frisk_fill) are reported in GB/s of algorithmic traffic (each
+input byte read once, each output byte written once) against the 8 TB/s
+HBM peak.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
        python bench.py --only NAME --steps K   (one workload, for rocprofv3)
@@ -101,6 +105,26 @@ def make_workloads(torch, rt):
             return lambda: rt.attn_fwd(q, k, v, o, causal=False, sm_scale=0.125)
         return setup
 
+    def reduce(rows, cols, axis, kind):
+        def setup():
+            x = torch.randn(rows, cols, generator=gen(11), device=dev)
+            out = torch.empty(rows if axis == 1 else cols, device=dev)
+            return lambda: rt.reduce(x, out, kind, axis=axis)
+        return setup
+
+    def cast(rows, cols):
+        def setup():
+            x = torch.randn(rows, cols, generator=gen(12), device=dev)
+            y = torch.empty(rows, cols, dtype=torch.bfloat16, device=dev)
+            return lambda: rt.copy(x, y)
+        return setup
+
+    def fill(rows, cols):
+        def setup():
+            y = torch.empty(rows, cols, dtype=torch.bfloat16, device=dev)
+            return lambda: rt.fill(y, 0.5)
+        return setup
+
     fa = 4.0 * 4 * 32 * 4096 * 4096 * 128
     return {
         "gemm_bf16_4096": ("bf16", 2.0 * 4096 ** 3, gemm(4096, 4096, 4096, "bf16")),
@@ -111,6 +135,13 @@ def make_workloads(torch, rt):
         "fa_fwd_b4h32s4096d128": ("bf16", fa, attn(False)),
         "fa_fwd_b4h32s4096d128_causal": ("bf16", fa / 2, attn(True)),
         "fa_fwd_d64_b2h32s1025_f16_f32out": ("f16", 4.0 * 2 * 32 * 1025 * 1025 * 64, attn_d64()),
+        # HBM-bound tile ops: second entry = algorithmic bytes per launch.
+        "reduce_sum_f32_32768x4096_rows": ("hbm", 32768 * 4096 * 4 + 32768 * 4,
+                                           reduce(32768, 4096, 1, "sum")),
+        "reduce_max_f32_8192x16384_cols": ("hbm", 8192 * 16384 * 4 + 16384 * 4,
+                                           reduce(8192, 16384, 0, "max")),
+        "copy_f32_to_bf16_16384x8192": ("hbm", 16384 * 8192 * (4 + 2), cast(16384, 8192)),
+        "fill_bf16_16384x16384": ("hbm", 16384 * 16384 * 2, fill(16384, 16384)),
         # Calibration only (--only): a plain 256 MiB device copy, whose
         # FETCH_SIZE / WRITE_SIZE per dispatch scale the HBM counters.
         "copy_256mib": ("bytes", 0.0, copy(256 << 20)),
@@ -234,7 +265,8 @@ def main():
         label, flops, setup = work[args.only]
         fn = setup()
         ms = time_launches(torch, fn, args.steps, args.warmup)
-        print(json.dumps({"workload": args.only, "ms": ms, "tflops": flops / ms / 1e9}), flush=True)
+        rate = {"gbs": flops / ms / 1e6} if label == "hbm" else {"tflops": flops / ms / 1e9}
+        print(json.dumps({"workload": args.only, "ms": ms, **rate}), flush=True)
         return
 
     results = {}
@@ -244,9 +276,14 @@ def main():
         fn = setup()
         steps = args.steps
         ms = time_launches(torch, fn, steps, args.warmup)
-        tf = flops / ms / 1e9
-        results[name] = {"dtype": label, "ms": round(ms, 6), "tflops": round(tf, 2),
-                         "frac_peak": round(tf / PEAK[label], 4)}
+        if label == "hbm":
+            gbs = flops / ms / 1e6
+            results[name] = {"bytes": flops, "ms": round(ms, 6), "gbs": round(gbs, 1),
+                             "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+        else:
+            tf = flops / ms / 1e9
+            results[name] = {"dtype": label, "ms": round(ms, 6), "tflops": round(tf, 2),
+                             "frac_peak": round(tf / PEAK[label], 4)}
         del fn
         torch.cuda.empty_cache()
 

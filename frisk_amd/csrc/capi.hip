@@ -11,6 +11,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
+#include <cmath>
 #include <string>
 
 #include "../../include/frisk_hip.h"
@@ -70,6 +72,53 @@ bool gemm_pair_ok(int in, int out) {
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Bit pattern of `v` rounded to nearest even in a float format with `mant`
+// explicit mantissa bits, `ebits` exponent bits (bias 2^(ebits-1) - 1) and
+// `max_finite`; without infinities (e4m3fn) overflow and NaN give the
+// all-ones NaN.  Mirrors how a fill value becomes a FloatAttr of the tile's
+// element type (ffi/ir.cpp:439-454).
+uint64_t float_bits(double v, int mant, int ebits, double max_finite, bool has_inf) {
+  const int bias = (1 << (ebits - 1)) - 1, emin = 1 - bias;
+  const uint64_t sign = std::signbit(v) ? 1ull << (mant + ebits) : 0;
+  const uint64_t emask = (1ull << ebits) - 1;
+  const uint64_t nan = has_inf ? (emask << mant) | (1ull << (mant - 1)) : (emask << mant) | ((1ull << mant) - 1);
+  if (std::isnan(v)) return nan;
+  double a = std::fabs(v);
+  if (std::isinf(a)) return has_inf ? sign | (emask << mant) : sign | nan;
+  if (a == 0.0) return sign;
+  int e2;
+  std::frexp(a, &e2);
+  const int e = std::max(e2 - 1, emin);
+  const double q = std::ldexp(1.0, e - mant);
+  const double r = std::nearbyint(a / q) * q;  // ties to even
+  if (r > max_finite) return has_inf ? sign | (emask << mant) : sign | nan;
+  int re;
+  std::frexp(r, &re);
+  if (re - 1 < emin) return sign | (uint64_t)(r / std::ldexp(1.0, emin - mant));  // subnormal
+  const uint64_t field = (uint64_t)(re - 1 + bias);
+  const uint64_t frac = (uint64_t)((r / std::ldexp(1.0, re - 1) - 1.0) * std::ldexp(1.0, mant));
+  return sign | (field << mant) | frac;
+}
+
+bool fill_bits(int dtype, double v, uint64_t* out) {
+  switch (dtype) {
+    case FRISK_F64: { uint64_t b; memcpy(&b, &v, 8); *out = b; return true; }
+    case FRISK_F32: *out = float_bits(v, 23, 8, 3.4028234663852886e38, true); return true;
+    case FRISK_F16: *out = float_bits(v, 10, 5, 65504.0, true); return true;
+    case FRISK_BF16: *out = float_bits(v, 7, 8, 3.3895313892515355e38, true); return true;
+    case FRISK_E4M3: *out = float_bits(v, 3, 4, 448.0, false); return true;
+    case FRISK_I8:
+      if (!(v == std::floor(v) && v >= -128.0 && v <= 127.0)) return false;
+      *out = (uint8_t)(int8_t)v;
+      return true;
+    case FRISK_I32:
+      if (!(v == std::floor(v) && v >= -2147483648.0 && v <= 2147483647.0)) return false;
+      *out = (uint32_t)(int32_t)v;
+      return true;
+    default: return false;
+  }
+}
 
 }  // namespace
 
@@ -180,6 +229,134 @@ int frisk_attn_fwd(const frisk_attn_desc* d, void* stream) {
   a.lse = d->lse;
   hipError_t e = frisk::attn_fwd(a, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "frisk_attn_fwd launch");
+  return FRISK_OK;
+}
+
+int frisk_reduce(const frisk_reduce_desc* d, void* stream) {
+  g_last_error.clear();
+  if (!d) return fail(FRISK_EINVAL, "frisk_reduce: null descriptor");
+  if (d->rows <= 0 || d->cols <= 0)
+    return fail(FRISK_EINVAL, "frisk_reduce: rows and cols must be positive (got %lld, %lld)",
+                (long long)d->rows, (long long)d->cols);
+  if (d->dtype != FRISK_F32 && d->dtype != FRISK_F16 && d->dtype != FRISK_BF16)
+    return fail(FRISK_EINVAL, "frisk_reduce: dtype must be f32, f16 or bf16 (got %s)",
+                dtype_name(d->dtype));
+  if (d->kind != FRISK_REDUCE_SUM && d->kind != FRISK_REDUCE_MAX && d->kind != FRISK_REDUCE_MIN)
+    return fail(FRISK_EINVAL, "frisk_reduce: unknown reduction kind %d", d->kind);
+  if (d->axis != 0 && d->axis != 1)
+    return fail(FRISK_EINVAL, "frisk_reduce: axis must be 0 or 1 (got %d)", d->axis);
+  if (!d->src || !d->dst) return fail(FRISK_EINVAL, "frisk_reduce: null tensor");
+  const int es = esize(d->dtype);
+  if ((uintptr_t)d->src % es || (uintptr_t)d->dst % es)
+    return fail(FRISK_EINVAL, "frisk_reduce: pointers must be element-aligned");
+  if (d->ld_src < d->cols || d->dst_stride < 1)
+    return fail(FRISK_EINVAL, "frisk_reduce: ld_src %lld < cols %lld or dst_stride %lld < 1",
+                (long long)d->ld_src, (long long)d->cols, (long long)d->dst_stride);
+  if (d->rows >= ((int64_t)1 << 31) || d->cols >= ((int64_t)1 << 31) ||
+      (d->axis == 0 && d->rows >= ((int64_t)1 << 23)))
+    return fail(FRISK_EUNSUP, "frisk_reduce: size beyond the kernels' limits (rows, cols < 2^31; "
+                              "axis 0 rows < 2^23)");
+  const int64_t extent = d->axis == 1 ? d->cols : d->rows;
+  if (d->leaf_order_bits < 0 || d->leaf_order_bits > 30)
+    return fail(FRISK_EINVAL, "frisk_reduce: leaf_order_bits %d outside 0..30", d->leaf_order_bits);
+  if (d->leaf_order_bits > 0) {
+    if (extent != ((int64_t)1 << d->leaf_order_bits))
+      return fail(FRISK_EINVAL, "frisk_reduce: a leaf order of %d bits needs a reduced extent of "
+                                "%lld (got %lld)",
+                  d->leaf_order_bits, (long long)1 << d->leaf_order_bits, (long long)extent);
+    uint32_t seen = 0;
+    for (int j = 0; j < d->leaf_order_bits; ++j) {
+      const int b = d->leaf_order[j];
+      if (b >= d->leaf_order_bits || (seen >> b) & 1u)
+        return fail(FRISK_EINVAL, "frisk_reduce: leaf_order is not a permutation of 0..%d",
+                    d->leaf_order_bits - 1);
+      seen |= 1u << b;
+    }
+  }
+  frisk::ReduceArgs a;
+  a.order_bits = d->leaf_order_bits;
+  for (int j = 0; j < 32; ++j) a.order[j] = j < d->leaf_order_bits ? d->leaf_order[j] : 0;
+  a.dtype = (frisk::Elt)d->dtype;
+  a.kind = d->kind;
+  a.axis = d->axis;
+  a.clear = d->clear != 0;
+  a.rows = d->rows; a.cols = d->cols;
+  a.src = d->src; a.ld = d->ld_src;
+  a.dst = d->dst; a.dst_stride = d->dst_stride;
+  hipError_t e = frisk::tile_reduce(a, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "frisk_reduce launch");
+  return FRISK_OK;
+}
+
+int frisk_copy(const frisk_copy_desc* d, void* stream) {
+  g_last_error.clear();
+  if (!d) return fail(FRISK_EINVAL, "frisk_copy: null descriptor");
+  if (d->rows <= 0 || d->cols <= 0)
+    return fail(FRISK_EINVAL, "frisk_copy: rows and cols must be positive (got %lld, %lld)",
+                (long long)d->rows, (long long)d->cols);
+  const int ses = esize(d->src_type), des = esize(d->dst_type);
+  if (!ses || !des)
+    return fail(FRISK_EINVAL, "frisk_copy: unknown element type %d -> %d", d->src_type,
+                d->dst_type);
+  auto convertible = [](int t) {
+    return t == FRISK_F32 || t == FRISK_F16 || t == FRISK_BF16 || t == FRISK_E4M3;
+  };
+  if (d->src_type != d->dst_type && !(convertible(d->src_type) && convertible(d->dst_type)))
+    return fail(FRISK_EINVAL, "frisk_copy: no conversion %s -> %s (f32, f16, bf16, e4m3)",
+                dtype_name(d->src_type), dtype_name(d->dst_type));
+  if (!d->src || !d->dst) return fail(FRISK_EINVAL, "frisk_copy: null tensor");
+  if ((uintptr_t)d->src % ses || (uintptr_t)d->dst % des)
+    return fail(FRISK_EINVAL, "frisk_copy: pointers must be element-aligned");
+  if (d->ld_src < d->cols || d->ld_dst < d->cols)
+    return fail(FRISK_EINVAL, "frisk_copy: row stride smaller than cols");
+  if (d->rows >= ((int64_t)1 << 40) || d->cols >= ((int64_t)1 << 40))
+    return fail(FRISK_EUNSUP, "frisk_copy: size beyond the kernels' limits");
+  frisk::CopyArgs a;
+  a.src_t = (frisk::Elt)d->src_type;
+  a.dst_t = (frisk::Elt)d->dst_type;
+  a.esize = ses;
+  a.rows = d->rows; a.cols = d->cols;
+  a.src = d->src; a.ld_src = d->ld_src;
+  a.dst = d->dst; a.ld_dst = d->ld_dst;
+  if (a.rows > 1 && a.ld_src == a.cols && a.ld_dst == a.cols) {  // contiguous: one long row
+    a.cols *= a.rows;
+    a.ld_src = a.ld_dst = a.cols;
+    a.rows = 1;
+  }
+  hipError_t e = frisk::tile_copy(a, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "frisk_copy launch");
+  return FRISK_OK;
+}
+
+int frisk_fill(const frisk_fill_desc* d, void* stream) {
+  g_last_error.clear();
+  if (!d) return fail(FRISK_EINVAL, "frisk_fill: null descriptor");
+  if (d->rows <= 0 || d->cols <= 0)
+    return fail(FRISK_EINVAL, "frisk_fill: rows and cols must be positive (got %lld, %lld)",
+                (long long)d->rows, (long long)d->cols);
+  const int es = esize(d->dtype);
+  if (!es) return fail(FRISK_EINVAL, "frisk_fill: unknown element type %d", d->dtype);
+  if (!d->dst) return fail(FRISK_EINVAL, "frisk_fill: null tensor");
+  if ((uintptr_t)d->dst % es) return fail(FRISK_EINVAL, "frisk_fill: pointer must be element-aligned");
+  if (d->ld < d->cols) return fail(FRISK_EINVAL, "frisk_fill: row stride smaller than cols");
+  if (d->rows >= ((int64_t)1 << 40) || d->cols >= ((int64_t)1 << 40))
+    return fail(FRISK_EUNSUP, "frisk_fill: size beyond the kernels' limits");
+  uint64_t bits = 0;
+  if (!fill_bits(d->dtype, d->value, &bits))
+    return fail(FRISK_EINVAL, "frisk_fill: value %g is not representable as %s", d->value,
+                dtype_name(d->dtype));
+  frisk::FillArgs a;
+  a.esize = es;
+  a.bits = bits;
+  a.rows = d->rows; a.cols = d->cols;
+  a.dst = d->dst; a.ld = d->ld;
+  if (a.rows > 1 && a.ld == a.cols) {
+    a.cols *= a.rows;
+    a.ld = a.cols;
+    a.rows = 1;
+  }
+  hipError_t e = frisk::tile_fill(a, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "frisk_fill launch");
   return FRISK_OK;
 }
 

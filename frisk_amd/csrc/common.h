@@ -16,7 +16,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 // Element kinds the kernels are templated on (mirrors frisk_dtype).
-enum class Elt : int { F32 = 0, F16 = 1, BF16 = 2, E4M3 = 3, I8 = 4, I32 = 5 };
+enum class Elt : int { F32 = 0, F16 = 1, BF16 = 2, E4M3 = 3, I8 = 4, I32 = 5, F64 = 6 };
 
 template <Elt E> struct EltInfo;
 template <> struct EltInfo<Elt::F32> { using T = float; static constexpr int bytes = 4; };

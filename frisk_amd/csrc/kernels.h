@@ -73,6 +73,49 @@ inline hipError_t attn_fwd(const AttnArgs& a, hipStream_t s) {
   }
 }
 
+// Tile ops (tileops.hip).  Reduction kinds of frisk.reduce_tensor.
+constexpr int kReduceSum = 0, kReduceMax = 1, kReduceMin = 2;
+
+// A validated reduction of a [rows, cols] tensor (element strides) along
+// `axis`; dtype F32, F16 or BF16 for source and destination.
+struct ReduceArgs {
+  Elt dtype;
+  int kind, axis, clear;
+  int64_t rows, cols;
+  const void* src;
+  int64_t ld;
+  void* dst;
+  int64_t dst_stride;
+  // Leaf order: 0 = ascending index; else the reduced extent is
+  // 2^order_bits and tree level j combines along index bit order[j].
+  int order_bits;
+  uint8_t order[32];
+};
+hipError_t tile_reduce(const ReduceArgs& a, hipStream_t s);
+
+// A validated copy of a [rows, cols] tensor; src_t == dst_t copies raw
+// elements of `esize` bytes, otherwise both are F32, F16, BF16 or E4M3.
+struct CopyArgs {
+  Elt src_t, dst_t;
+  int esize;
+  int64_t rows, cols;
+  const void* src;
+  int64_t ld_src;
+  void* dst;
+  int64_t ld_dst;
+};
+hipError_t tile_copy(const CopyArgs& a, hipStream_t s);
+
+// Fill a [rows, cols] tensor of `esize`-byte elements with a bit pattern.
+struct FillArgs {
+  int esize;
+  uint64_t bits;
+  int64_t rows, cols;
+  void* dst;
+  int64_t ld;
+};
+hipError_t tile_fill(const FillArgs& a, hipStream_t s);
+
 // MFMA fragment-layout probe (probe.hip): atom 0 = bf16 32x32x16,
 // 1 = bf16 16x16x32, 2 = i8 32x32x32; `out` holds mfma_probe_floats(atom)
 // floats.

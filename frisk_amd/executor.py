@@ -39,7 +39,7 @@ import math
 from dataclasses import dataclass
 from typing import Optional, Sequence
 
-from . import _ir
+from . import _ir, tileprog
 
 ir = _ir()
 fr = ir.frisk
@@ -417,7 +417,8 @@ def _attention(ops, entry) -> AttnPlan:
 
 # ---------------------------------------------------------------------------
 def plan(module, kernel: str):
-    """Recognise kernel `kernel` of `module`: a GemmPlan or an AttnPlan."""
+    """Recognise kernel `kernel` of `module`: a GemmPlan, an AttnPlan or a
+    tileprog.OpsPlan (fill / copy / reduce programs)."""
     k = module.get_kernel(kernel)
     if k is None:
         raise ValueError(f"execute: module has no kernel @{kernel}")
@@ -426,17 +427,19 @@ def plan(module, kernel: str):
     entry = k.get_region(0).front()
     ops = _body_ops(entry)
     reasons = []
-    for recognise in (_gemm_whole, _gemm_tiled, _attention):
+    for recognise in (_gemm_whole, _gemm_tiled, _attention, tileprog.plan_whole,
+                      tileprog.plan_tiled):
         try:
             return recognise(ops, entry)
-        except _Reject as e:
+        except (_Reject, tileprog.Reject) as e:
             reasons.append(f"{recognise.__name__.lstrip('_')}: {e}")
-    raise ValueError(f"execute: kernel @{kernel} is not a recognised GEMM or attention tile program ("
+    raise ValueError(f"execute: kernel @{kernel} is not a recognised GEMM, attention or tile-op "
+                     "program ("
                      + "; ".join(reasons) + ")")
 
 
 _TORCH_DTYPES = {"f16": "float16", "bf16": "bfloat16", "f32": "float32", "f8E4M3FN": "float8_e4m3fn",
-                 "i8": "int8", "i32": "int32"}
+                 "i8": "int8", "i32": "int32", "f64": "float64"}
 
 
 def _check_tensor(t, value, name):
@@ -462,6 +465,8 @@ def execute(module, kernel: str, tensors: Sequence, *, stream=None, causal: bool
         raise ValueError(f"execute: @{kernel} takes {len(args)} tensors, got {len(tensors)}")
     for i, (t, a) in enumerate(zip(tensors, args)):
         _check_tensor(t, a, f"argument {i}")
+    if isinstance(p, tileprog.OpsPlan):
+        return tileprog.run(p, tensors, stream=stream)
     if isinstance(p, GemmPlan):
         return rt.gemm(tensors[p.a], tensors[p.b], tensors[p.c], trans_a=p.trans_a, trans_b=p.trans_b,
                        clear_accum=p.clear_accum, scale_a=scale_a, scale_b=scale_b, stream=stream)

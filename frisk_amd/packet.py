@@ -11,7 +11,17 @@ library implements and dispatched through the C-ABI:
   arguments, then frisk.tile_store of the result -> frisk_gemm;
 * attention: Q.K^T, scale, row max, exp, row sum, divide, truncate, P.V,
   store (the program of test/Transforms/attention-layout.mlir) ->
-  frisk_attn_fwd with the packet's scale.
+  frisk_attn_fwd with the packet's scale;
+* reduction: frisk.tile_load, frisk.reduce_tensor (sum/max/min along one
+  dim), optionally merged with a constant by arith.addf / maximumf /
+  minimumf, frisk.tile_store -> frisk_fill of the constant and frisk_reduce.
+  The packet's fibers fix the order of each sum
+  (ReductionLayoutProof.cpp:108-140: an output's distinct inputs sorted by
+  carrier, paired level by level); that order is read back from the fibers
+  and the source layout's carrier enumeration and passed to frisk_reduce as
+  its leaf order, so the sums are bit-exact with the packet's contract;
+* fill: a splat constant stored by frisk.tile_store -> frisk_fill;
+* copy: frisk.tile_load then frisk.tile_store -> frisk_copy.
 
 The packet's distributed layouts describe how the solver would place the
 tile; the kernels use their own fixed layouts, and `plan_packet` reports
@@ -42,15 +52,31 @@ def _load(packet) -> dict:
 
 
 def _splat(text: str) -> float:
+    """Value of a splat constant: `dense<1.5> : ...`, or a hex bit pattern of
+    the element type (`dense<0xFF800000> : tensor<64xf32>`), the form used for
+    values without an exact decimal spelling such as infinities."""
     m = re.match(r"dense<([-+0-9.eEinfa]+)>", text or "")
-    if not m:
-        raise ValueError(f"execution packet: expected a splat constant, got {text!r}")
-    return float(m.group(1))
+    if m:
+        return float(m.group(1))
+    m = re.match(r"dense<0x([0-9A-Fa-f]+)>\s*:\s*\w+<(?:\d+x)*(\w+)>", text or "")
+    if m:
+        import struct
+        bits, elem = int(m.group(1), 16), m.group(2)
+        if elem == "f32":
+            return struct.unpack("<f", struct.pack("<I", bits))[0]
+        if elem == "f64":
+            return struct.unpack("<d", struct.pack("<Q", bits))[0]
+        if elem == "f16":
+            return struct.unpack("<e", struct.pack("<H", bits))[0]
+        if elem == "bf16":
+            return struct.unpack("<f", struct.pack("<I", bits << 16))[0]
+    raise ValueError(f"execution packet: expected a splat constant, got {text!r}")
 
 
 def plan_packet(packet) -> dict:
     """Recognise the packet's tile program.  Returns a dict with `kind`
-    ("gemm" or "attention"), the kernel-argument positions of each operand,
+    ("gemm", "attention", "reduce", "fill" or "copy"), the kernel-argument
+    positions of each operand,
     the program parameters and `layouts_match` (whether the packet's MMA
     contracts are the ones the library kernel implements)."""
     pk = _load(packet)
@@ -127,7 +153,96 @@ def plan_packet(packet) -> dict:
                 "seq_k": qk["attrs"]["n"], "head_dim": head_dim,
                 "contract": contract(qk), "layouts_match": bool(kernel_layout and head_dim >= 32),
                 "arg_types": [types[a] for a in args]}
-    raise ValueError("execution packet: not a GEMM or attention tile program: " + ", ".join(names))
+    values = {v["id"]: v for v in pk["values"]}
+    if names in (["frisk.tile_load", "frisk.reduce_tensor", "frisk.tile_store"],
+                 ["frisk.tile_load", "frisk.reduce_tensor", "arith.addf", "frisk.tile_store"],
+                 ["frisk.tile_load", "frisk.reduce_tensor", "arith.maximumf", "frisk.tile_store"],
+                 ["frisk.tile_load", "frisk.reduce_tensor", "arith.minimumf", "frisk.tile_store"]):
+        return _plan_reduce(body, producer, values, source_arg, types, args, root)
+    if names == ["frisk.tile_store"]:
+        store = body[0]
+        cst = producer.get(store["operands"][0])
+        if not cst or cst["name"] != "arith.constant":
+            raise ValueError("execution packet: a lone tile_store must store a constant")
+        return {"kind": "fill", "dst": source_arg(store["operands"][1]),
+                "value": _splat(cst["attrs"].get("value")), "arg_types": [types[a] for a in args]}
+    if names == ["frisk.tile_load", "frisk.tile_store"]:
+        load, store = body
+        if store["operands"][0] != load["results"][0]:
+            raise ValueError("execution packet: the stored tile is not the loaded one")
+        return {"kind": "copy", "src": source_arg(load["operands"][0]),
+                "dst": source_arg(store["operands"][1]), "arg_types": [types[a] for a in args]}
+    raise ValueError("execution packet: not a GEMM, attention, reduction, fill or copy tile "
+                     "program: " + ", ".join(names))
+
+
+_MERGE = {"arith.addf": "sum", "arith.maximumf": "max", "arith.minimumf": "min"}
+
+
+def leaf_order_of(fibers, logical, shape, dim):
+    """Leaf order of a reduction packet: for every output, the reduced index
+    of each fiber leaf (carrier -> logical element -> index along `dim`), in
+    fiber order.  Returns None for ascending order, else the bit permutation
+    (tree level j combines along index bit order[j]) shared by all fibers."""
+    cols = shape[1] if len(shape) == 2 else 1
+    extent = shape[dim]
+    order = None
+    for fiber in fibers:
+        idx = [(logical[c] // cols) if dim == 0 else (logical[c] % cols) for c in fiber]
+        if len(idx) != extent or extent & (extent - 1):
+            raise ValueError("execution packet: a reduction fiber does not hold every index of a "
+                             "power-of-two extent once")
+        nb = extent.bit_length() - 1
+        bits = []
+        for j in range(nb):
+            v = idx[1 << j] ^ idx[0]
+            if v & (v - 1) or v == 0:
+                raise ValueError("execution packet: reduction leaf order is not a permutation of "
+                                 "index bits")
+            bits.append(v.bit_length() - 1)
+        if idx[0] != 0 or any(idx[p] != sum(((p >> j) & 1) << bits[j] for j in range(nb))
+                              for p in range(extent)):
+            raise ValueError("execution packet: reduction leaf order is not a permutation of "
+                             "index bits")
+        if order is not None and bits != order:
+            raise ValueError("execution packet: reduction fibers use different leaf orders")
+        order = bits
+    return None if order == sorted(order or []) else order
+
+
+def _plan_reduce(body, producer, values, source_arg, types, args, root):
+    load, red = body[0], body[1]
+    store = body[-1]
+    if root(red["operands"][0]) != load["results"][0]:
+        raise ValueError("execution packet: the reduction does not read the loaded tile")
+    kind, dim = red["attrs"].get("kind"), red["attrs"].get("dim")
+    if kind not in ("sum", "max", "min") or dim not in (0, 1):
+        raise ValueError(f"execution packet: reduction kind {kind!r} along {dim!r}")
+    init = None
+    result = red["results"][0]
+    if len(body) == 4:
+        merge = body[2]
+        if _MERGE[merge["name"]] != kind:
+            raise ValueError(f"execution packet: {merge['name']} cannot merge a {kind} reduction")
+        if root(merge["operands"][1]) != result:
+            raise ValueError("execution packet: the merge must combine (old value, reduction)")
+        cst = producer.get(root(merge["operands"][0]))
+        if not cst or cst["name"] != "arith.constant":
+            raise ValueError("execution packet: the merged old value must be a constant")
+        init = _splat(cst["attrs"].get("value"))
+        result = merge["results"][0]
+    if root(store["operands"][0]) != result:
+        raise ValueError("execution packet: the stored value is not the reduction")
+    src_val = values[load["results"][0]]
+    dist = src_val.get("distributed")
+    fibers = red.get("attrs", {}).get("fibers", red.get("fibers"))
+    if not dist or fibers is None:
+        raise ValueError("execution packet: the reduction has no fibers or source layout")
+    shape = [int(x) for x in re.findall(r"(\d+)x", src_val["type"].split("<", 1)[1])]
+    order = leaf_order_of(fibers, dist["logical"], shape, dim)
+    return {"kind": "reduce", "src": source_arg(load["operands"][0]),
+            "dst": source_arg(store["operands"][1]), "reduce": kind, "dim": dim, "init": init,
+            "leaf_order": order, "arg_types": [types[a] for a in args]}
 
 
 def execute_packet(packet, tensors, *, stream=None) -> dict:
@@ -147,6 +262,16 @@ def execute_packet(packet, tensors, *, stream=None) -> dict:
     if plan["kind"] == "gemm":
         rt.gemm(tensors[plan["a"]], tensors[plan["b"]], tensors[plan["c"]], trans_a=plan["trans_a"],
                 trans_b=plan["trans_b"], stream=stream)
+    elif plan["kind"] == "reduce":
+        dst = tensors[plan["dst"]]
+        if plan["init"] is not None:
+            rt.fill(dst, plan["init"], stream=stream)
+        rt.reduce(tensors[plan["src"]], dst, plan["reduce"], axis=plan["dim"],
+                  clear=plan["init"] is None, leaf_order=plan["leaf_order"], stream=stream)
+    elif plan["kind"] == "fill":
+        rt.fill(tensors[plan["dst"]], plan["value"], stream=stream)
+    elif plan["kind"] == "copy":
+        rt.copy(tensors[plan["src"]], tensors[plan["dst"]], stream=stream)
     else:
         q, k, v, o = (tensors[plan[n]] for n in ("q", "k", "v", "o"))
         view = lambda t: t.view(1, 1, *t.shape)

@@ -1,8 +1,8 @@
 """ctypes binding of libfrisk_hip.so (include/frisk_hip.h).
 
 This is the Python side of the C-ABI: it fills the descriptors from torch
-device tensors and calls frisk_gemm / frisk_attn_fwd on the current HIP
-stream.  There is no fallback: if the library is missing or a call fails,
+device tensors and calls frisk_gemm / frisk_attn_fwd / frisk_reduce /
+frisk_copy / frisk_fill on the current HIP stream.  There is no fallback: if the library is missing or a call fails,
 a RuntimeError (or ValueError for rejected requests, matching the
 reference's ValueError on contract violations, ffi/ir.cpp:333-341) is raised.
 """
@@ -20,9 +20,12 @@ OK, EINVAL, EUNSUP, EHIP = 0, -1, -2, -3
 DTYPE_NAMES = {F32: "f32", F16: "f16", BF16: "bf16", E4M3: "e4m3", I8: "i8", I32: "i32", F64: "f64"}
 
 # Exported symbols declared by include/frisk_hip.h.
-EXPORTS = ("frisk_gemm", "frisk_attn_fwd", "frisk_last_error", "frisk_abi_version",
-           "frisk_probe_mfma_layout")
-ABI_VERSION = 2
+EXPORTS = ("frisk_gemm", "frisk_attn_fwd", "frisk_reduce", "frisk_copy", "frisk_fill",
+           "frisk_last_error", "frisk_abi_version", "frisk_probe_mfma_layout")
+ABI_VERSION = 3
+
+REDUCE_SUM, REDUCE_MAX, REDUCE_MIN = 0, 1, 2
+REDUCE_KINDS = {"sum": REDUCE_SUM, "add": REDUCE_SUM, "max": REDUCE_MAX, "min": REDUCE_MIN}
 
 
 class GemmDesc(ctypes.Structure):
@@ -56,6 +59,34 @@ class AttnDesc(ctypes.Structure):
     ]
 
 
+class ReduceDesc(ctypes.Structure):
+    _fields_ = [
+        ("rows", ctypes.c_int64), ("cols", ctypes.c_int64),
+        ("dtype", ctypes.c_int32), ("kind", ctypes.c_int32), ("axis", ctypes.c_int32),
+        ("clear", ctypes.c_int32),
+        ("src", ctypes.c_void_p), ("ld_src", ctypes.c_int64),
+        ("dst", ctypes.c_void_p), ("dst_stride", ctypes.c_int64),
+        ("leaf_order_bits", ctypes.c_int32), ("leaf_order", ctypes.c_uint8 * 32),
+    ]
+
+
+class CopyDesc(ctypes.Structure):
+    _fields_ = [
+        ("rows", ctypes.c_int64), ("cols", ctypes.c_int64),
+        ("src_type", ctypes.c_int32), ("dst_type", ctypes.c_int32),
+        ("src", ctypes.c_void_p), ("ld_src", ctypes.c_int64),
+        ("dst", ctypes.c_void_p), ("ld_dst", ctypes.c_int64),
+    ]
+
+
+class FillDesc(ctypes.Structure):
+    _fields_ = [
+        ("rows", ctypes.c_int64), ("cols", ctypes.c_int64),
+        ("dtype", ctypes.c_int32), ("value", ctypes.c_double),
+        ("dst", ctypes.c_void_p), ("ld", ctypes.c_int64),
+    ]
+
+
 _lib = None
 
 
@@ -73,6 +104,12 @@ def load() -> ctypes.CDLL:
     lib.frisk_gemm.restype = ctypes.c_int
     lib.frisk_attn_fwd.argtypes = [ctypes.POINTER(AttnDesc), ctypes.c_void_p]
     lib.frisk_attn_fwd.restype = ctypes.c_int
+    lib.frisk_reduce.argtypes = [ctypes.POINTER(ReduceDesc), ctypes.c_void_p]
+    lib.frisk_reduce.restype = ctypes.c_int
+    lib.frisk_copy.argtypes = [ctypes.POINTER(CopyDesc), ctypes.c_void_p]
+    lib.frisk_copy.restype = ctypes.c_int
+    lib.frisk_fill.argtypes = [ctypes.POINTER(FillDesc), ctypes.c_void_p]
+    lib.frisk_fill.restype = ctypes.c_int
     lib.frisk_last_error.argtypes = []
     lib.frisk_last_error.restype = ctypes.c_char_p
     lib.frisk_abi_version.argtypes = []
@@ -200,3 +237,68 @@ def attn_fwd(q, k, v, o, *, causal=False, sm_scale=None, lse=None, stream=None):
     _check(load().frisk_attn_fwd(ctypes.byref(d), ctypes.c_void_p(_stream_handle(stream))),
            "frisk_attn_fwd")
     return o
+
+
+def _matrix(t, name: str):
+    """(rows, cols, row stride) of a rank-1 or rank-2 device tensor with unit
+    innermost stride; a rank-1 tensor is one row."""
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a device tensor")
+    if t.dim() == 1:
+        if t.stride(0) != 1 and t.numel() > 1:
+            raise ValueError(f"{name} must have unit stride")
+        return 1, t.shape[0], max(t.shape[0], 1)
+    if t.dim() != 2 or (t.stride(1) != 1 and t.shape[1] > 1):
+        raise ValueError(f"{name} must be a rank-1 or rank-2 tensor with unit column stride")
+    return t.shape[0], t.shape[1], max(t.stride(0), t.shape[1])
+
+
+def reduce(src, dst, kind="sum", *, axis=1, clear=True, leaf_order=None, stream=None):
+    """frisk.reduce: dst = reduce(src) along `axis` of the [rows, cols] tensor
+    src (or dst = combine(dst, reduce(src)) with clear=False).  dst is a
+    rank-1 tensor of the kept extent, any stride, same dtype.  `leaf_order`
+    (a permutation of the reduced index bits, tree level j along bit
+    leaf_order[j]) replaces the ascending leaf order."""
+    rows, cols, ld = _matrix(src, "src")
+    if src.dim() != 2:
+        raise ValueError("src must be rank 2")
+    if kind not in REDUCE_KINDS:
+        raise ValueError(f"unknown reduction kind {kind!r} (sum/add, max, min)")
+    if axis not in (0, 1):
+        raise ValueError("axis must be 0 or 1")
+    n = rows if axis == 1 else cols
+    if dst.dim() != 1 or dst.shape[0] != n or not dst.is_cuda:
+        raise ValueError(f"dst must be a rank-1 device tensor of {n} elements")
+    if dst.dtype != src.dtype:
+        raise ValueError("src and dst must share one dtype")
+    order = list(leaf_order or [])
+    if len(order) > 32:
+        raise ValueError("leaf_order has more than 32 bits")
+    d = ReduceDesc(rows, cols, torch_dtype_code(src.dtype), REDUCE_KINDS[kind], axis,
+                   int(bool(clear)), src.data_ptr(), ld, dst.data_ptr(), max(dst.stride(0), 1),
+                   len(order), (ctypes.c_uint8 * 32)(*order))
+    _check(load().frisk_reduce(ctypes.byref(d), ctypes.c_void_p(_stream_handle(stream))),
+           "frisk_reduce")
+    return dst
+
+
+def copy(src, dst, *, stream=None):
+    """frisk.copy of a whole tile: dst = src converted to dst's dtype."""
+    rows, cols, lds = _matrix(src, "src")
+    drows, dcols, ldd = _matrix(dst, "dst")
+    if (rows, cols) != (drows, dcols):
+        raise ValueError(f"copy shapes differ: {tuple(src.shape)} -> {tuple(dst.shape)}")
+    d = CopyDesc(rows, cols, torch_dtype_code(src.dtype), torch_dtype_code(dst.dtype),
+                 src.data_ptr(), lds, dst.data_ptr(), ldd)
+    _check(load().frisk_copy(ctypes.byref(d), ctypes.c_void_p(_stream_handle(stream))),
+           "frisk_copy")
+    return dst
+
+
+def fill(dst, value, *, stream=None):
+    """frisk.fill: every element of dst = value rounded to dst's dtype."""
+    rows, cols, ld = _matrix(dst, "dst")
+    d = FillDesc(rows, cols, torch_dtype_code(dst.dtype), float(value), dst.data_ptr(), ld)
+    _check(load().frisk_fill(ctypes.byref(d), ctypes.c_void_p(_stream_handle(stream))),
+           "frisk_fill")
+    return dst

@@ -1,12 +1,13 @@
 /*
- * frisk_hip.h — C-ABI of the MI355X (gfx950) GEMM and attention kernels.
+ * frisk_hip.h — C-ABI of the MI355X (gfx950) GEMM, attention and tile-op
+ * kernels.
  *
  * The reference (guoqiao7/frisk) has no execute entry in its FFI: the
  * pass/execute bindings are commented out at ffi/ffi.h:14 and ffi/ffi.cpp:6,
  * and the only GPU path is the out-of-process harness
  * benchmark/layout/execution/run_execution.py:23-95 (frisk-opt -> JSON ->
  * Triton).  These entry points are what that FFI would bind for the GEMM and
- * attention tile programs:
+ * attention tile programs and the tile ops around them:
  *
  *   frisk_gemm      <- the semantics of frisk.gemm
  *                      (include/Dialect/Frisk/IR/FriskOps.td:252-292;
@@ -18,6 +19,17 @@
  *   frisk_attn_fwd  <- the attention tile program (tmp/ir.mlir:89-157,
  *                      benchmark/layout/execution/tiled_attention.py:210-728),
  *                      with online softmax instead of three passes.
+ *   frisk_reduce    <- frisk.reduce (include/Dialect/Frisk/IR/FriskOps.td:
+ *                      425-453; clear/merge lowering LegacyFragmentNormalization
+ *                      .cpp:522-555) and frisk.reduce_tensor (FriskLayoutOps.td:
+ *                      17-30) in the canonical_fiber_tree_v1 order
+ *                      (lib/Dialect/Frisk/Analysis/ReductionLayoutProof.cpp:
+ *                      108-140).
+ *   frisk_copy      <- frisk.copy (FriskOps.td:351-397) of a whole tile,
+ *                      including the element-type change of a fragment stored
+ *                      to global memory (tmp/ir.mlir:154).
+ *   frisk_fill      <- frisk.fill (FriskOps.td:400-422; builder ffi/ir.cpp:
+ *                      439-454).
  *
  * Conventions: plain pointers and sizes only; every pointer is a device
  * pointer owned by the caller; `stream` is a hipStream_t (NULL = the null
@@ -34,7 +46,7 @@
 extern "C" {
 #endif
 
-#define FRISK_ABI_VERSION 2
+#define FRISK_ABI_VERSION 3
 
 /* Element types (the dtype strings of ffi/ir.cpp:399-411 plus bf16/i8/i32). */
 typedef enum frisk_dtype {
@@ -117,6 +129,85 @@ typedef struct frisk_attn_desc {
 } frisk_attn_desc;
 
 int frisk_attn_fwd(const frisk_attn_desc* desc, void* stream);
+
+/* Reduction kinds (frisk.reduce "add"/"max"/"min", reduce_tensor "sum"/...). */
+typedef enum frisk_reduce_kind {
+  FRISK_REDUCE_SUM = 0,
+  FRISK_REDUCE_MAX = 1,
+  FRISK_REDUCE_MIN = 2
+} frisk_reduce_kind;
+
+/*
+ * Reduction of src[rows, cols] (row stride ld_src) along `axis`:
+ *   axis 1:  dst[r * dst_stride] = reduce over c of src[r, c]   (rows outputs)
+ *   axis 0:  dst[c * dst_stride] = reduce over r of src[r, c]   (cols outputs)
+ * clear == 0 merges with the destination's old value:
+ *   dst = combine(dst, reduction)   (frisk.reduce with clear = false).
+ * dtype is f32, f16 or bf16 for both src and dst, and every combine is done
+ * in it: a sum is rounded to dtype after each addition.  Sums associate as
+ * the canonical pairwise tree over the reduced index in ascending order
+ * (adjacent pairs first, an odd last node carried up), so results are
+ * deterministic and independent of the launch shape.  max / min propagate
+ * NaN and order -0.0 below +0.0.  src and dst must not overlap; pointers are
+ * element-aligned.  Limits: rows, cols < 2^31; axis 0 needs rows < 2^23.
+ *
+ * leaf_order_bits > 0 selects another leaf order, that of a distributed
+ * layout whose reduced-axis bits sit on single carrier bits (the fibers of
+ * canonical_fiber_tree_v1, ReductionLayoutProof.cpp:119-124): the reduced
+ * extent must be 2^leaf_order_bits, leaf_order[0..bits) is a permutation of
+ * 0..bits-1, and leaf position p holds reduced index
+ * sum_j ((p >> j) & 1) << leaf_order[j].  This path runs one thread per
+ * output and is meant for tile-sized reductions.
+ */
+typedef struct frisk_reduce_desc {
+  int64_t rows, cols;
+  int32_t dtype; /* frisk_dtype: FRISK_F32, FRISK_F16 or FRISK_BF16 */
+  int32_t kind;  /* frisk_reduce_kind */
+  int32_t axis;  /* 0 or 1 */
+  int32_t clear;
+  const void* src;
+  int64_t ld_src;
+  void* dst;
+  int64_t dst_stride;
+  int32_t leaf_order_bits; /* 0: ascending index order */
+  uint8_t leaf_order[32];
+} frisk_reduce_desc;
+
+int frisk_reduce(const frisk_reduce_desc* desc, void* stream);
+
+/*
+ * dst[r, c] = convert(src[r, c]) for a [rows, cols] tile (row strides
+ * ld_src, ld_dst in elements).  Equal types copy the elements unchanged (any
+ * frisk_dtype).  Otherwise src_type and dst_type are f32, f16, bf16 or e4m3:
+ * widening is exact and narrowing rounds to nearest even (arith.truncf);
+ * f16 and bf16 overflow to infinity, e4m3 (no infinity) to NaN.  src and dst
+ * must not overlap.
+ */
+typedef struct frisk_copy_desc {
+  int64_t rows, cols;
+  int32_t src_type, dst_type; /* frisk_dtype */
+  const void* src;
+  int64_t ld_src;
+  void* dst;
+  int64_t ld_dst;
+} frisk_copy_desc;
+
+int frisk_copy(const frisk_copy_desc* desc, void* stream);
+
+/*
+ * dst[r, c] = value for a [rows, cols] tile (row stride ld).  For float
+ * dtypes `value` is rounded to nearest even in dtype (e4m3: values past 464
+ * in magnitude become NaN); for i8 / i32 it must be an integer in range.
+ */
+typedef struct frisk_fill_desc {
+  int64_t rows, cols;
+  int32_t dtype; /* frisk_dtype */
+  double value;
+  void* dst;
+  int64_t ld;
+} frisk_fill_desc;
+
+int frisk_fill(const frisk_fill_desc* desc, void* stream);
 
 /* Description of the last failure on the calling thread ("" if none). */
 const char* frisk_last_error(void);

@@ -181,3 +181,181 @@ def attention_tensor_form(M=64, N=64, D=16, dtype="fp16", threads=128, scale=0.2
                  "trans_b": b.get_bool_attr(False)})
     b.create_op("frisk.tile_store", [result, view(o, mo)], [])
     return s, kernel
+
+
+def row_reduce(R, C, BR=64, kind="max", dtype="fp32", init=None, threads=128, name="row_reduce"):
+    """Y[r] = reduce_c X[r, c] as a grid of R/BR row tiles: each tile is
+    copied into a Local buffer, reduced along dim 1 into a Local vector
+    (clear, or merged into a vector filled with `init`) and stored."""
+    s = F.create_session()
+    b = s.builder
+    G = F.MemorySpace.GLOBAL
+    kernel, entry = s.new_kernel(name, [s.memref_type([R, C], dtype, space=G),
+                                        s.memref_type([R], dtype, space=G)])
+    X, Y = entry.get_argument(0), entry.get_argument(1)
+    par = b.create_parallel_op([R // BR], threads)
+    b.set_insertion_point_to_start(par.add_entry_block())
+    (i,) = par.get_ivs()
+    t = s.alloc_buffer([BR, C], dtype)
+    r = s.alloc_buffer([BR], dtype)
+    ctx = s.context
+    d0, zero = b.get_affine_dim_expr(0), b.get_affine_constant_expr(0)
+    empty = b.get_empty_affine_map()
+    b.create_copy_op(X, t, [i], [], F.AffineMap.get(1, 0, [d0 * BR, zero], ctx), empty)
+    if init is None:
+        b.create_reduce_op(t, r, kind, 1, True)
+    else:
+        b.create_fill_op(r, init, "fp32" if dtype != "fp16" else "fp16")
+        b.create_reduce_op(t, r, kind, 1, False)
+    b.create_copy_op(r, Y, [], [i], empty, F.AffineMap.get(1, 0, [d0 * BR], ctx), [BR], [BR])
+    return s, kernel
+
+
+def col_reduce_tiles(R, C, BC=64, kind="add", dtype="fp32", threads=128, name="col_reduce"):
+    """Y[c] = reduce_r X[r, c] over a grid of C/BC column strips (each tile
+    spans every row)."""
+    s = F.create_session()
+    b = s.builder
+    G = F.MemorySpace.GLOBAL
+    kernel, entry = s.new_kernel(name, [s.memref_type([R, C], dtype, space=G),
+                                        s.memref_type([C], dtype, space=G)])
+    X, Y = entry.get_argument(0), entry.get_argument(1)
+    par = b.create_parallel_op([C // BC], threads)
+    b.set_insertion_point_to_start(par.add_entry_block())
+    (j,) = par.get_ivs()
+    t = s.alloc_buffer([R, BC], dtype, space=F.MemorySpace.SHARED)
+    r = s.alloc_buffer([BC], dtype)
+    ctx = s.context
+    d0, zero = b.get_affine_dim_expr(0), b.get_affine_constant_expr(0)
+    empty = b.get_empty_affine_map()
+    b.create_copy_op(X, t, [j], [], F.AffineMap.get(1, 0, [zero, d0 * BC], ctx), empty)
+    b.create_reduce_op(t, r, kind, 0, True)
+    b.create_copy_op(r, Y, [], [j], empty, F.AffineMap.get(1, 0, [d0 * BC], ctx), [BC], [BC])
+    return s, kernel
+
+
+def tiled_cast(R, C, BR=64, BC=128, src="fp32", dst="bf16", staged=False, threads=256,
+               name="cast"):
+    """Y = X converted to Y's element type, tile by tile: the conversion is the
+    store copy of a Local tile into the narrower global tensor (the epilogue
+    of tmp/ir.mlir:154), or a Local-to-Local copy first when `staged`."""
+    s = F.create_session()
+    b = s.builder
+    G = F.MemorySpace.GLOBAL
+    kernel, entry = s.new_kernel(name, [s.memref_type([R, C], src, space=G),
+                                        s.memref_type([R, C], dst, space=G)])
+    X, Y = entry.get_argument(0), entry.get_argument(1)
+    par = b.create_parallel_op([R // BR, C // BC], threads)
+    b.set_insertion_point_to_start(par.add_entry_block())
+    i, j = par.get_ivs()
+    t = s.alloc_buffer([BR, BC], src)
+    ctx = s.context
+    d0, d1 = b.get_affine_dim_expr(0), b.get_affine_dim_expr(1)
+    empty = b.get_empty_affine_map()
+    tile = F.AffineMap.get(2, 0, [d0 * BR, d1 * BC], ctx)
+    b.create_copy_op(X, t, [i, j], [], tile, empty)
+    out = t
+    if staged:
+        out = s.alloc_buffer([BR, BC], dst)
+        b.create_copy_op(t, out, [], [])
+    b.create_copy_op(out, Y, [], [i, j], empty, tile, [BR, BC], [BR, BC])
+    return s, kernel
+
+
+def tiled_fill(R, C, value, BR=32, BC=64, dtype="fp32", threads=128, name="fill"):
+    s = F.create_session()
+    b = s.builder
+    G = F.MemorySpace.GLOBAL
+    kernel, entry = s.new_kernel(name, [s.memref_type([R, C], dtype, space=G)])
+    Y = entry.get_argument(0)
+    par = b.create_parallel_op([R // BR, C // BC], threads)
+    b.set_insertion_point_to_start(par.add_entry_block())
+    i, j = par.get_ivs()
+    t = s.alloc_buffer([BR, BC], dtype)
+    b.create_fill_op(t, value, dtype)
+    ctx = s.context
+    d0, d1 = b.get_affine_dim_expr(0), b.get_affine_dim_expr(1)
+    b.create_copy_op(t, Y, [], [i, j], b.get_empty_affine_map(),
+                     F.AffineMap.get(2, 0, [d0 * BR, d1 * BC], ctx), [BR, BC], [BR, BC])
+    return s, kernel
+
+
+def gemm_then_cast(M, N, K, dtype="bf16", name="gemm_cast"):
+    """Whole-tensor sequence: C (Global f32 buffer) = 0; C += A . B^T; D = C
+    converted to `dtype`."""
+    s = F.create_session()
+    b = s.builder
+    G = F.MemorySpace.GLOBAL
+    kernel, entry = s.new_kernel(name, [s.memref_type([M, K], dtype, space=G),
+                                        s.memref_type([N, K], dtype, space=G),
+                                        s.memref_type([M, N], dtype, space=G)])
+    A, B, D = (entry.get_argument(i) for i in range(3))
+    c = s.alloc_buffer([M, N], "fp32", space=G)
+    b.create_fill_op(c, 0.0, "fp32")
+    b.create_gemm_op(A, B, c, False, True, False, None)
+    b.create_copy_op(c, D, [], [])
+    return s, kernel
+
+
+def single_tile_reduce(R=64, C=64, kind="add", dtype="fp32", init=None, dim=1, threads=128,
+                       name="tile_reduce"):
+    """One tile in the reference's normalizable form (whole-tile copies, a
+    tensor_v1 frisk.reduce): Y = reduce(X) along `dim`, merged into a vector
+    filled with `init` when given (LegacyNormalizationNumericTest.cpp:74-118
+    builds the same shape of program)."""
+    s = F.create_session()
+    b = s.builder
+    G = F.MemorySpace.GLOBAL
+    out = C if dim == 0 else R
+    kernel, entry = s.new_kernel(name, [s.memref_type([R, C], dtype, space=G),
+                                        s.memref_type([out], dtype, space=G)])
+    X, Y = entry.get_argument(0), entry.get_argument(1)
+    par = b.create_parallel_op([1], threads)
+    b.set_insertion_point_to_start(par.add_entry_block())
+    t = s.alloc_buffer([R, C], dtype)
+    r = s.alloc_buffer([out], dtype)
+    b.create_copy_op(X, t, [], [])
+    if init is None:
+        b.create_reduce_op(t, r, kind, dim, True, "tensor_v1")
+    else:
+        b.create_fill_op(r, init, dtype)
+        b.create_reduce_op(t, r, kind, dim, False, "tensor_v1")
+    b.create_copy_op(r, Y, [], [])
+    return s, kernel
+
+
+def single_tile_fill(R=64, C=64, value=1.5, dtype="fp32", threads=128, name="tile_fill"):
+    s = F.create_session()
+    b = s.builder
+    kernel, entry = s.new_kernel(name, [s.memref_type([R, C], dtype, space=F.MemorySpace.GLOBAL)])
+    par = b.create_parallel_op([1], threads)
+    b.set_insertion_point_to_start(par.add_entry_block())
+    t = s.alloc_buffer([R, C], dtype)
+    b.create_fill_op(t, value, dtype)
+    b.create_copy_op(t, entry.get_argument(0), [], [])
+    return s, kernel
+
+
+def single_tile_copy(R=64, C=64, dtype="fp32", threads=128, name="tile_copy"):
+    s = F.create_session()
+    b = s.builder
+    G = F.MemorySpace.GLOBAL
+    kernel, entry = s.new_kernel(name, [s.memref_type([R, C], dtype, space=G),
+                                        s.memref_type([R, C], dtype, space=G)])
+    par = b.create_parallel_op([1], threads)
+    b.set_insertion_point_to_start(par.add_entry_block())
+    t = s.alloc_buffer([R, C], dtype)
+    b.create_copy_op(entry.get_argument(0), t, [], [])
+    b.create_copy_op(t, entry.get_argument(1), [], [])
+    return s, kernel
+
+
+def exported_packet(built):
+    """Normalize (tensor_v1, gfx950), infer layouts and export the packet."""
+    import json
+    s, _ = built
+    s.module.set_attr("frisk.legacy_semantics", s.builder.get_str_attr("tensor_v1"))
+    F.frisk.normalize_layout_ir(s.module, "gfx950")
+    report = F.frisk.infer_layouts(s.module)
+    assert report["status"] == "materialized", report
+    return json.loads(F.frisk.export_execution(s.module))

@@ -100,3 +100,112 @@ def test_python_binding_rejects_host_tensors_and_bad_shapes():
         rt.gemm(a, a, torch.zeros(4, 4, dtype=torch.bfloat16), trans_b=True)
     with pytest.raises(ValueError, match="rank-2"):
         rt.gemm_desc(torch.zeros(4, dtype=torch.bfloat16), a, a)
+
+
+def reduce_call(**over):
+    d = rt.ReduceDesc(rows=64, cols=64, dtype=rt.F32, kind=rt.REDUCE_SUM, axis=1, clear=1,
+                      src=16, ld_src=64, dst=16, dst_stride=1)
+    for key, val in over.items():
+        setattr(d, key, val)
+    lib = rt.load()
+    return lib.frisk_reduce(ctypes.byref(d), None), lib.frisk_last_error().decode()
+
+
+@pytest.mark.parametrize("over,code,prefix", [
+    (dict(rows=0), rt.EINVAL, "frisk_reduce: rows and cols"),
+    (dict(dtype=rt.I32), rt.EINVAL, "frisk_reduce: dtype"),
+    (dict(dtype=rt.E4M3), rt.EINVAL, "frisk_reduce: dtype"),
+    (dict(kind=3), rt.EINVAL, "frisk_reduce: unknown reduction kind"),
+    (dict(axis=2), rt.EINVAL, "frisk_reduce: axis"),
+    (dict(src=0), rt.EINVAL, "frisk_reduce: null"),
+    (dict(src=18), rt.EINVAL, "frisk_reduce: pointers must be element-aligned"),
+    (dict(ld_src=32), rt.EINVAL, "frisk_reduce: ld_src"),
+    (dict(dst_stride=0), rt.EINVAL, "frisk_reduce: ld_src"),
+    (dict(axis=0, rows=1 << 23, ld_src=64), rt.EUNSUP, "frisk_reduce: size"),
+    (dict(leaf_order_bits=5), rt.EINVAL, "frisk_reduce: a leaf order of 5 bits"),
+    (dict(leaf_order_bits=31), rt.EINVAL, "frisk_reduce: leaf_order_bits"),
+    (dict(leaf_order_bits=6, leaf_order=(ctypes.c_uint8 * 32)(0, 1, 2, 3, 4, 4)), rt.EINVAL,
+     "frisk_reduce: leaf_order is not a permutation"),
+    (dict(leaf_order_bits=6, leaf_order=(ctypes.c_uint8 * 32)(0, 1, 2, 3, 4, 6)), rt.EINVAL,
+     "frisk_reduce: leaf_order is not a permutation"),
+])
+def test_reduce_rejects_invalid_requests(over, code, prefix):
+    rc, msg = reduce_call(**over)
+    assert rc == code and msg.startswith(prefix), (rc, msg)
+
+
+def copy_call(**over):
+    d = rt.CopyDesc(rows=8, cols=8, src_type=rt.F32, dst_type=rt.BF16, src=16, ld_src=8, dst=16,
+                    ld_dst=8)
+    for key, val in over.items():
+        setattr(d, key, val)
+    lib = rt.load()
+    return lib.frisk_copy(ctypes.byref(d), None), lib.frisk_last_error().decode()
+
+
+@pytest.mark.parametrize("over,code,prefix", [
+    (dict(cols=0), rt.EINVAL, "frisk_copy: rows and cols"),
+    (dict(src_type=9), rt.EINVAL, "frisk_copy: unknown element type"),
+    (dict(src_type=rt.I8), rt.EINVAL, "frisk_copy: no conversion i8 -> bf16"),
+    (dict(dst_type=rt.I32), rt.EINVAL, "frisk_copy: no conversion f32 -> i32"),
+    (dict(dst=0), rt.EINVAL, "frisk_copy: null"),
+    (dict(src=18), rt.EINVAL, "frisk_copy: pointers"),
+    (dict(ld_dst=4), rt.EINVAL, "frisk_copy: row stride"),
+])
+def test_copy_rejects_invalid_requests(over, code, prefix):
+    rc, msg = copy_call(**over)
+    assert rc == code and msg.startswith(prefix), (rc, msg)
+
+
+def fill_call(**over):
+    d = rt.FillDesc(rows=8, cols=8, dtype=rt.F32, value=1.0, dst=16, ld=8)
+    for key, val in over.items():
+        setattr(d, key, val)
+    lib = rt.load()
+    return lib.frisk_fill(ctypes.byref(d), None), lib.frisk_last_error().decode()
+
+
+@pytest.mark.parametrize("over,code,prefix", [
+    (dict(rows=-1), rt.EINVAL, "frisk_fill: rows and cols"),
+    (dict(dtype=11), rt.EINVAL, "frisk_fill: unknown element type"),
+    (dict(dst=0), rt.EINVAL, "frisk_fill: null"),
+    (dict(dtype=rt.I32, dst=18), rt.EINVAL, "frisk_fill: pointer"),
+    (dict(ld=7), rt.EINVAL, "frisk_fill: row stride"),
+    (dict(dtype=rt.I8, value=128.0), rt.EINVAL, "frisk_fill: value"),
+    (dict(dtype=rt.I32, value=0.5), rt.EINVAL, "frisk_fill: value"),
+])
+def test_fill_rejects_invalid_requests(over, code, prefix):
+    rc, msg = fill_call(**over)
+    assert rc == code and msg.startswith(prefix), (rc, msg)
+
+
+def test_tileop_null_descriptors():
+    lib = rt.load()
+    assert lib.frisk_reduce(None, None) == rt.EINVAL
+    assert lib.frisk_copy(None, None) == rt.EINVAL
+    assert lib.frisk_fill(None, None) == rt.EINVAL
+
+
+def test_descriptor_layouts_match_the_header(tmp_path):
+    """sizeof / offsetof of every descriptor as a C compiler lays out
+    include/frisk_hip.h, against the ctypes mirrors."""
+    import subprocess
+    structs = {"frisk_gemm_desc": rt.GemmDesc, "frisk_attn_desc": rt.AttnDesc,
+               "frisk_reduce_desc": rt.ReduceDesc, "frisk_copy_desc": rt.CopyDesc,
+               "frisk_fill_desc": rt.FillDesc}
+    lines = ['#include <stddef.h>', '#include <stdio.h>', f'#include "{HEADER}"', "int main(void) {"]
+    for cname, py in structs.items():
+        lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
+        for field, _ in py._fields_:
+            lines.append(f'printf("{cname} {field} %zu\\n", offsetof({cname}, {field}));')
+    lines.append("return 0; }")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
+    got = dict((" ".join(l.split()[:2]), int(l.split()[2])) for l in out if l)
+    for cname, py in structs.items():
+        assert got[f"{cname} size"] == ctypes.sizeof(py), cname
+        for field, _ in py._fields_:
+            assert got[f"{cname} {field}"] == getattr(py, field).offset, (cname, field)

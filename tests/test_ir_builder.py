@@ -669,5 +669,5 @@ def _mutated_gemm(mutation):
 def test_plan_rejects_wrong_programs(mutation):
     from frisk_amd.executor import plan
     assert plan(_mutated_gemm("none").module, "matmul").m == 256
-    with pytest.raises(ValueError, match="not a recognised GEMM or attention tile program"):
+    with pytest.raises(ValueError, match="not a recognised GEMM, attention or tile-op program"):
         plan(_mutated_gemm(mutation).module, "matmul")

@@ -310,7 +310,7 @@ def test_plan_packet_rejects_other_programs():
     ops = pk["operations"]
     ex = next(i for i, o in enumerate(ops) if o["name"] == "math.exp")
     ops[ex]["name"] = "math.exp2"
-    with pytest.raises(ValueError, match="not a GEMM or attention"):
+    with pytest.raises(ValueError, match="not a GEMM, attention, reduction, fill or copy"):
         F.plan_packet(pk)
     pk = json.loads(_packet(_attention(64, 64, 16, 128, dtype="fp16")))
     pk["target"] = "sm_90a"

@@ -73,3 +73,58 @@ def test_gemm_packet():
     assert plan["kind"] == "gemm"
     ref = decode(a) @ decode(b)
     assert G.row_scaled_error(decode(out), ref) <= 1e-5
+
+
+# ---- reduction, fill and copy packets ------------------------------------------------
+def _reduce_case(R, C, kind, dtype, dim, threads, init=None):
+    from oracle import tileops as T
+    from tests.test_packet_tileops import fiber_tree_reference
+    dt = {"fp32": "f32", "fp16": "f16"}[dtype]
+    tdt = {"f32": torch.float32, "f16": torch.float16}[dt]
+    pk = P.exported_packet(P.single_tile_reduce(R, C, kind=kind, dtype=dtype, dim=dim,
+                                                threads=threads, init=init))
+    rng = np.random.default_rng(R + C + dim + len(kind))
+    span = 10 if dt == "f16" else 20
+    x = T.round_to(dt, (rng.standard_normal((R, C)) * np.exp2(rng.integers(-span, span + 1, (R, C))))
+                   .astype(np.float32))
+    n = R if dim == 1 else C
+    y = torch.full((n,), 9.0, dtype=tdt, device="cuda")
+    plan = F.execute_packet(pk, [torch.from_numpy(x).to(tdt).cuda(), y])
+    torch.cuda.synchronize()
+    want = fiber_tree_reference(pk, x, kind, dt)
+    if init is not None:
+        want = T.combine(T.KINDS[kind], dt, np.full(n, init, dtype=np.float32), want)
+    got = y.float().cpu().numpy()
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    ok = ~np.isnan(want)
+    assert np.array_equal(got[ok].view(np.uint32), want[ok].astype(np.float32).view(np.uint32))
+    return plan
+
+
+@pytest.mark.parametrize("dim", [1, 0])
+@pytest.mark.parametrize("kind", ["add", "max"])
+@pytest.mark.parametrize("dtype", ["fp32", "fp16"])
+@pytest.mark.parametrize("shape,threads", [((64, 64), 128), ((32, 16), 64), ((128, 32), 256)])
+def test_reduce_packet_matches_its_fibers(shape, threads, dtype, kind, dim):
+    """The packet's sums follow its fibers' tree, including the permuted row
+    order of the column sums, bit for bit."""
+    print(f"case reduce packet {shape} threads={threads} {dtype} {kind} dim={dim}", flush=True)
+    _reduce_case(*shape, kind, dtype, dim, threads)
+
+
+@pytest.mark.parametrize("kind,init", [("max", float("-inf")), ("add", 0.5), ("min", 3.0)])
+def test_merge_reduce_packet(kind, init):
+    print(f"case merge packet {kind} {init}", flush=True)
+    plan = _reduce_case(64, 64, kind, "fp32", 1, 128, init=init)
+    assert plan["init"] == init
+
+
+def test_fill_and_copy_packets_run():
+    print("case fill/copy packets", flush=True)
+    y = torch.zeros(64, 64, device="cuda")
+    F.execute_packet(P.exported_packet(P.single_tile_fill(64, 64, value=-2.25)), [y])
+    x = torch.randn(64, 64, device="cuda")
+    z = torch.zeros(64, 64, device="cuda")
+    F.execute_packet(P.exported_packet(P.single_tile_copy(64, 64)), [x, z])
+    torch.cuda.synchronize()
+    assert torch.equal(y, torch.full_like(y, -2.25)) and torch.equal(x, z)
