@@ -109,7 +109,9 @@ def make_workloads(torch, rt):
         def setup():
             x = torch.randn(rows, cols, generator=gen(11), device=dev)
             out = torch.empty(rows if axis == 1 else cols, device=dev)
-            return lambda: rt.reduce(x, out, kind, axis=axis)
+            ws = torch.empty(max(rt.reduce_workspace_bytes(x, out, kind, axis=axis), 16),
+                             dtype=torch.uint8, device=dev)
+            return lambda: rt.reduce(x, out, kind, axis=axis, workspace=ws)
         return setup
 
     def cast(rows, cols):
@@ -279,7 +281,8 @@ def main():
         if label == "hbm":
             gbs = flops / ms / 1e6
             results[name] = {"bytes": flops, "ms": round(ms, 6), "gbs": round(gbs, 1),
-                             "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+                             "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+                             "traffic": traffic_from_profile(name)}
         else:
             tf = flops / ms / 1e9
             results[name] = {"dtype": label, "ms": round(ms, 6), "tflops": round(tf, 2),

@@ -232,50 +232,90 @@ int frisk_attn_fwd(const frisk_attn_desc* d, void* stream) {
   return FRISK_OK;
 }
 
-int frisk_reduce(const frisk_reduce_desc* d, void* stream) {
-  g_last_error.clear();
-  if (!d) return fail(FRISK_EINVAL, "frisk_reduce: null descriptor");
+}  // extern "C"
+
+namespace {
+
+// Checks of frisk_reduce / frisk_reduce_workspace_size; 0 or an error code.
+int check_reduce(const frisk_reduce_desc* d, const char* fn) {
+  if (!d) return fail(FRISK_EINVAL, "%s: null descriptor", fn);
   if (d->rows <= 0 || d->cols <= 0)
-    return fail(FRISK_EINVAL, "frisk_reduce: rows and cols must be positive (got %lld, %lld)",
+    return fail(FRISK_EINVAL, "%s: rows and cols must be positive (got %lld, %lld)", fn,
                 (long long)d->rows, (long long)d->cols);
   if (d->dtype != FRISK_F32 && d->dtype != FRISK_F16 && d->dtype != FRISK_BF16)
-    return fail(FRISK_EINVAL, "frisk_reduce: dtype must be f32, f16 or bf16 (got %s)",
+    return fail(FRISK_EINVAL, "%s: dtype must be f32, f16 or bf16 (got %s)", fn,
                 dtype_name(d->dtype));
   if (d->kind != FRISK_REDUCE_SUM && d->kind != FRISK_REDUCE_MAX && d->kind != FRISK_REDUCE_MIN)
-    return fail(FRISK_EINVAL, "frisk_reduce: unknown reduction kind %d", d->kind);
+    return fail(FRISK_EINVAL, "%s: unknown reduction kind %d", fn, d->kind);
   if (d->axis != 0 && d->axis != 1)
-    return fail(FRISK_EINVAL, "frisk_reduce: axis must be 0 or 1 (got %d)", d->axis);
-  if (!d->src || !d->dst) return fail(FRISK_EINVAL, "frisk_reduce: null tensor");
-  const int es = esize(d->dtype);
-  if ((uintptr_t)d->src % es || (uintptr_t)d->dst % es)
-    return fail(FRISK_EINVAL, "frisk_reduce: pointers must be element-aligned");
+    return fail(FRISK_EINVAL, "%s: axis must be 0 or 1 (got %d)", fn, d->axis);
   if (d->ld_src < d->cols || d->dst_stride < 1)
-    return fail(FRISK_EINVAL, "frisk_reduce: ld_src %lld < cols %lld or dst_stride %lld < 1",
+    return fail(FRISK_EINVAL, "%s: ld_src %lld < cols %lld or dst_stride %lld < 1", fn,
                 (long long)d->ld_src, (long long)d->cols, (long long)d->dst_stride);
   if (d->rows >= ((int64_t)1 << 31) || d->cols >= ((int64_t)1 << 31) ||
       (d->axis == 0 && d->rows >= ((int64_t)1 << 23)))
-    return fail(FRISK_EUNSUP, "frisk_reduce: size beyond the kernels' limits (rows, cols < 2^31; "
-                              "axis 0 rows < 2^23)");
+    return fail(FRISK_EUNSUP, "%s: size beyond the kernels' limits (rows, cols < 2^31; "
+                              "axis 0 rows < 2^23)", fn);
   const int64_t extent = d->axis == 1 ? d->cols : d->rows;
   if (d->leaf_order_bits < 0 || d->leaf_order_bits > 30)
-    return fail(FRISK_EINVAL, "frisk_reduce: leaf_order_bits %d outside 0..30", d->leaf_order_bits);
+    return fail(FRISK_EINVAL, "%s: leaf_order_bits %d outside 0..30", fn, d->leaf_order_bits);
   if (d->leaf_order_bits > 0) {
     if (extent != ((int64_t)1 << d->leaf_order_bits))
-      return fail(FRISK_EINVAL, "frisk_reduce: a leaf order of %d bits needs a reduced extent of "
-                                "%lld (got %lld)",
-                  d->leaf_order_bits, (long long)1 << d->leaf_order_bits, (long long)extent);
+      return fail(FRISK_EINVAL, "%s: a leaf order of %d bits needs a reduced extent of %lld "
+                                "(got %lld)",
+                  fn, d->leaf_order_bits, (long long)1 << d->leaf_order_bits, (long long)extent);
     uint32_t seen = 0;
     for (int j = 0; j < d->leaf_order_bits; ++j) {
       const int b = d->leaf_order[j];
       if (b >= d->leaf_order_bits || (seen >> b) & 1u)
-        return fail(FRISK_EINVAL, "frisk_reduce: leaf_order is not a permutation of 0..%d",
+        return fail(FRISK_EINVAL, "%s: leaf_order is not a permutation of 0..%d", fn,
                     d->leaf_order_bits - 1);
       seen |= 1u << b;
     }
   }
+  if (d->workspace_bytes < 0) return fail(FRISK_EINVAL, "%s: negative workspace_bytes", fn);
+  return FRISK_OK;
+}
+
+// Bytes of workspace the two-pass axis-0 kernels take (0: single pass).
+int64_t reduce_workspace(const frisk_reduce_desc* d) {
+  if (d->axis != 0 || d->leaf_order_bits > 0 || d->rows < 256) return 0;
+  const frisk::ColsSplit sp = frisk::cols_split(d->rows, d->cols);
+  return sp.blocks * d->cols * (int64_t)sizeof(float);
+}
+
+}  // namespace
+
+extern "C" {
+
+int64_t frisk_reduce_workspace_size(const frisk_reduce_desc* d) {
+  g_last_error.clear();
+  const int rc = check_reduce(d, "frisk_reduce_workspace_size");
+  return rc ? rc : reduce_workspace(d);
+}
+
+int frisk_reduce(const frisk_reduce_desc* d, void* stream) {
+  g_last_error.clear();
+  const int rc = check_reduce(d, "frisk_reduce");
+  if (rc) return rc;
+  if (!d->src || !d->dst) return fail(FRISK_EINVAL, "frisk_reduce: null tensor");
+  const int es = esize(d->dtype);
+  if ((uintptr_t)d->src % es || (uintptr_t)d->dst % es)
+    return fail(FRISK_EINVAL, "frisk_reduce: pointers must be element-aligned");
+  const int64_t need = reduce_workspace(d);
+  void* ws = nullptr;
+  if (d->workspace && need > 0) {
+    if (d->workspace_bytes < need)
+      return fail(FRISK_EINVAL, "frisk_reduce: workspace of %lld bytes, this reduction takes %lld",
+                  (long long)d->workspace_bytes, (long long)need);
+    if ((uintptr_t)d->workspace % 16)
+      return fail(FRISK_EINVAL, "frisk_reduce: workspace must be 16-byte aligned");
+    ws = d->workspace;
+  }
   frisk::ReduceArgs a;
   a.order_bits = d->leaf_order_bits;
   for (int j = 0; j < 32; ++j) a.order[j] = j < d->leaf_order_bits ? d->leaf_order[j] : 0;
+  a.workspace = ws;
   a.dtype = (frisk::Elt)d->dtype;
   a.kind = d->kind;
   a.axis = d->axis;

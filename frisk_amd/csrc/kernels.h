@@ -90,8 +90,19 @@ struct ReduceArgs {
   // 2^order_bits and tree level j combines along index bit order[j].
   int order_bits;
   uint8_t order[32];
+  // Axis 0 only: f32 scratch of cols_split(rows, cols).blocks * cols
+  // elements for the two-pass kernels, or null for the single pass.
+  void* workspace;
 };
 hipError_t tile_reduce(const ReduceArgs& a, hipStream_t s);
+
+// Two-pass axis-0 geometry: strips of 4 * 2^sps_log2 columns x row blocks
+// of 2^b_log2 rows.
+struct ColsSplit {
+  int64_t strips, blocks;
+  int sps_log2, b_log2;
+};
+ColsSplit cols_split(int64_t rows, int64_t cols);
 
 // A validated copy of a [rows, cols] tensor; src_t == dst_t copies raw
 // elements of `esize` bytes, otherwise both are F32, F16, BF16 or E4M3.

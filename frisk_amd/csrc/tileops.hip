@@ -278,6 +278,107 @@ __global__ __launch_bounds__(kColThreads) void reduce_cols_kernel(
   }
 }
 
+// ---- axis 0 in two passes ----------------------------------------------------------
+// Pass 1: workgroup (strip, block) reduces rows [block B, (block + 1) B) of a
+// strip of 4 * SPS columns (SPS = 2^sps_log2 <= 256 four-column slots, one
+// per lane along the columns, so a row segment of up to 4 KiB is read
+// contiguously by the whole workgroup); the 256 / SPS row groups each take
+// B / groups consecutive rows.  Group roots are combined by the pairwise
+// tree over the groups in LDS, and the block root (a complete subtree of B
+// rows; the last block padded) goes to the workspace as
+// partial[block][column].  Pass 2 combines the partials of each column in
+// block order through a binary counter.
+template <Elt E, int KIND>
+__global__ __launch_bounds__(tile::kThreads) void reduce_cols_blocks_kernel(
+    const void* __restrict__ src, int64_t ld, int64_t rows, int64_t cols, int sps_log2,
+    int b_log2, float* __restrict__ partial) {
+  using namespace tile;
+  constexpr int kEsz = EltInfo<E>::bytes;
+  __shared__ float part[kThreads * 4];
+  const int tid = threadIdx.x;
+  const int sps = 1 << sps_log2;
+  const int cs = tid & (sps - 1), g = tid >> sps_log2;
+  const int groups = kThreads >> sps_log2;
+  const int64_t c0 = ((int64_t)blockIdx.x * sps + cs) * 4;
+  const int64_t gb = ((int64_t)1 << b_log2) / groups;  // rows per group, >= 8
+  const int64_t r0 = ((int64_t)blockIdx.y << b_log2) + g * gb;
+  const int64_t r1 = min(rows, r0 + gb);
+  const bool full = c0 + 4 <= cols;
+
+  // gb <= 2^12 (cols_split), so a group pushes at most 2^9 eight-row subtrees.
+  Counter<E, KIND, 10> ctr[4];
+  uint32_t n8 = 0;
+  for (int64_t i0 = r0; i0 < r1; i0 += 8, ++n8) {
+    float x[8][4];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int64_t r = i0 + i;
+      const char* rp = (const char*)src + r * ld * kEsz;
+      if (r < r1 && full) {
+        if constexpr (E == Elt::F32) {
+          const f32x4 v = *(const f32x4*)((const float*)rp + c0);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) x[i][j] = v[j];
+        } else {
+          const uint2 v = *(const uint2*)((const uint16_t*)rp + c0);
+          const uint32_t w[2] = {v.x, v.y};
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const uint16_t h = (uint16_t)(w[j >> 1] >> (16 * (j & 1)));
+            x[i][j] = E == Elt::BF16 ? bf16_bits_to_f32(h) : (float)__builtin_bit_cast(_Float16, h);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          x[i][j] = r < r1 && c0 + j < cols ? load_as_f32<E>(rp, c0 + j) : identity<KIND>();
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+      for (int w = 1; w < 8; w <<= 1)
+#pragma unroll
+        for (int i = 0; i < 8; i += 2 * w) x[i][j] = combine<E, KIND>(x[i][j], x[i + w][j]);
+      ctr[j].push(n8, x[0][j]);
+    }
+  }
+  if (groups == 1) {  // no exchange needed
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (c0 + j < cols)
+        partial[(int64_t)blockIdx.y * cols + c0 + j] = n8 ? ctr[j].finish(n8) : identity<KIND>();
+    return;
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) part[(g * sps + cs) * 4 + j] = n8 ? ctr[j].finish(n8) : identity<KIND>();
+  __syncthreads();
+  if (g == 0) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      for (int w = 1; w < groups; w <<= 1)
+        for (int i = 0; i < groups; i += 2 * w)
+          part[(i * sps + cs) * 4 + j] =
+              combine<E, KIND>(part[(i * sps + cs) * 4 + j], part[((i + w) * sps + cs) * 4 + j]);
+      if (c0 + j < cols) partial[(int64_t)blockIdx.y * cols + c0 + j] = part[cs * 4 + j];
+    }
+  }
+}
+
+template <Elt E, int KIND>
+__global__ __launch_bounds__(tile::kThreads) void reduce_cols_final_kernel(
+    const float* __restrict__ partial, int64_t cols, uint32_t blocks, void* __restrict__ dst,
+    int64_t dst_stride, int clear) {
+  using namespace tile;
+  const int64_t c = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (c >= cols) return;
+  Counter<E, KIND, 24> ctr;
+  for (uint32_t b = 0; b < blocks; ++b) ctr.push(b, partial[(int64_t)b * cols + c]);
+  float res = ctr.finish(blocks);
+  if (!clear) res = combine<E, KIND>(load_as_f32<E>(dst, c * dst_stride), res);
+  store_from_f32<E>(dst, c * dst_stride, res);
+}
+
 // ---- any axis, permuted leaf order ------------------------------------------------
 // The tree over 2^nb leaves in which leaf position p holds reduced index
 // sum_j bit_j(p) << order[j] (the fiber order of a distributed layout whose
@@ -483,6 +584,30 @@ bool aligned(const void* p, int64_t ld_bytes, int a) {
   return ((uintptr_t)p % a) == 0 && ld_bytes % a == 0;
 }
 
+}  // namespace
+
+ColsSplit cols_split(int64_t rows, int64_t cols) {
+  // One round of workgroups: pass 1 holds about 104 VGPRs, so 4 workgroups
+  // of 256 threads are resident per CU and 1024 fill the 256 CUs.  A sweep
+  // on 8192 x 16384 f32 (strips of 64 .. 1024 columns, row blocks of 8 ..
+  // 2^16 rows) peaked at exactly 1024 workgroups (4.0 TB/s; 2048 gave 3.7,
+  // 512 gave 2.6) with strips of 64 or 128 columns, whose 16 or 8 row groups
+  // keep each thread on a long run of rows.
+  ColsSplit sp;
+  const int64_t slots = (cols + 3) / 4;
+  sp.sps_log2 = ilog2(slots) < 5 ? ilog2(slots) : 5;
+  const int g_log2 = 8 - sp.sps_log2;  // log2 of the row groups
+  sp.strips = (slots + ((int64_t)1 << sp.sps_log2) - 1) >> sp.sps_log2;
+  const int64_t want_blocks = sp.strips >= 1024 ? 1 : 1024 / sp.strips;
+  sp.b_log2 = ilog2((rows + want_blocks - 1) / want_blocks);
+  if (sp.b_log2 < 3 + g_log2) sp.b_log2 = 3 + g_log2;
+  if (sp.b_log2 > 12 + g_log2) sp.b_log2 = 12 + g_log2;
+  sp.blocks = (rows + ((int64_t)1 << sp.b_log2) - 1) >> sp.b_log2;
+  return sp;
+}
+
+namespace {
+
 template <Elt E, int KIND>
 hipError_t reduce_typed(const ReduceArgs& a, hipStream_t s) {
   constexpr int kEsz = EltInfo<E>::bytes;
@@ -516,6 +641,17 @@ hipError_t reduce_typed(const ReduceArgs& a, hipStream_t s) {
       default: FRISK_ROWS(8); break;
     }
 #undef FRISK_ROWS
+  } else if (a.workspace) {
+    const ColsSplit sp = cols_split(a.rows, a.cols);
+    hipLaunchKernelGGL((reduce_cols_blocks_kernel<E, KIND>), dim3(sp.strips, sp.blocks),
+                       dim3(tile::kThreads), 0, s, a.src, a.ld, a.rows, a.cols, sp.sps_log2,
+                       sp.b_log2, (float*)a.workspace);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((reduce_cols_final_kernel<E, KIND>),
+                       dim3((unsigned)((a.cols + tile::kThreads - 1) / tile::kThreads)),
+                       dim3(tile::kThreads), 0, s, (const float*)a.workspace, a.cols,
+                       (uint32_t)sp.blocks, a.dst, a.dst_stride, a.clear);
   } else {
     const int64_t slots = (a.cols + 3) / 4;
     // Widest column strip (best coalescing) that still yields >= 1024

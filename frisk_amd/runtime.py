@@ -20,7 +20,8 @@ OK, EINVAL, EUNSUP, EHIP = 0, -1, -2, -3
 DTYPE_NAMES = {F32: "f32", F16: "f16", BF16: "bf16", E4M3: "e4m3", I8: "i8", I32: "i32", F64: "f64"}
 
 # Exported symbols declared by include/frisk_hip.h.
-EXPORTS = ("frisk_gemm", "frisk_attn_fwd", "frisk_reduce", "frisk_copy", "frisk_fill",
+EXPORTS = ("frisk_gemm", "frisk_attn_fwd", "frisk_reduce", "frisk_reduce_workspace_size",
+           "frisk_copy", "frisk_fill",
            "frisk_last_error", "frisk_abi_version", "frisk_probe_mfma_layout")
 ABI_VERSION = 3
 
@@ -67,6 +68,7 @@ class ReduceDesc(ctypes.Structure):
         ("src", ctypes.c_void_p), ("ld_src", ctypes.c_int64),
         ("dst", ctypes.c_void_p), ("dst_stride", ctypes.c_int64),
         ("leaf_order_bits", ctypes.c_int32), ("leaf_order", ctypes.c_uint8 * 32),
+        ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_int64),
     ]
 
 
@@ -106,6 +108,8 @@ def load() -> ctypes.CDLL:
     lib.frisk_attn_fwd.restype = ctypes.c_int
     lib.frisk_reduce.argtypes = [ctypes.POINTER(ReduceDesc), ctypes.c_void_p]
     lib.frisk_reduce.restype = ctypes.c_int
+    lib.frisk_reduce_workspace_size.argtypes = [ctypes.POINTER(ReduceDesc)]
+    lib.frisk_reduce_workspace_size.restype = ctypes.c_int64
     lib.frisk_copy.argtypes = [ctypes.POINTER(CopyDesc), ctypes.c_void_p]
     lib.frisk_copy.restype = ctypes.c_int
     lib.frisk_fill.argtypes = [ctypes.POINTER(FillDesc), ctypes.c_void_p]
@@ -253,12 +257,26 @@ def _matrix(t, name: str):
     return t.shape[0], t.shape[1], max(t.stride(0), t.shape[1])
 
 
-def reduce(src, dst, kind="sum", *, axis=1, clear=True, leaf_order=None, stream=None):
+def reduce_workspace_bytes(src, dst, kind="sum", *, axis=1) -> int:
+    """frisk_reduce_workspace_size for reduce(src, dst, kind, axis=axis)."""
+    rows, cols, ld = _matrix(src, "src")
+    d = ReduceDesc(rows, cols, torch_dtype_code(src.dtype), REDUCE_KINDS[kind], axis, 1,
+                   src.data_ptr(), ld, dst.data_ptr(), max(dst.stride(0), 1))
+    need = int(load().frisk_reduce_workspace_size(ctypes.byref(d)))
+    _check(need if need < 0 else OK, "frisk_reduce_workspace_size")
+    return need
+
+
+def reduce(src, dst, kind="sum", *, axis=1, clear=True, leaf_order=None, workspace=True,
+           stream=None):
     """frisk.reduce: dst = reduce(src) along `axis` of the [rows, cols] tensor
     src (or dst = combine(dst, reduce(src)) with clear=False).  dst is a
     rank-1 tensor of the kept extent, any stride, same dtype.  `leaf_order`
     (a permutation of the reduced index bits, tree level j along bit
-    leaf_order[j]) replaces the ascending leaf order."""
+    leaf_order[j]) replaces the ascending leaf order.  `workspace`: True
+    allocates the scratch frisk_reduce_workspace_size asks for (torch's
+    caching allocator), a uint8 device tensor supplies it, False runs the
+    single-pass kernels."""
     rows, cols, ld = _matrix(src, "src")
     if src.dim() != 2:
         raise ValueError("src must be rank 2")
@@ -276,7 +294,16 @@ def reduce(src, dst, kind="sum", *, axis=1, clear=True, leaf_order=None, stream=
         raise ValueError("leaf_order has more than 32 bits")
     d = ReduceDesc(rows, cols, torch_dtype_code(src.dtype), REDUCE_KINDS[kind], axis,
                    int(bool(clear)), src.data_ptr(), ld, dst.data_ptr(), max(dst.stride(0), 1),
-                   len(order), (ctypes.c_uint8 * 32)(*order))
+                   len(order), (ctypes.c_uint8 * 32)(*order), None, 0)
+    ws = None
+    if workspace is not False:
+        need = load().frisk_reduce_workspace_size(ctypes.byref(d))
+        _check(int(need) if need < 0 else OK, "frisk_reduce_workspace_size")
+        if need > 0:
+            import torch
+            ws = workspace if workspace is not True else \
+                torch.empty(need, dtype=torch.uint8, device=src.device)
+            d.workspace, d.workspace_bytes = ws.data_ptr(), ws.numel() * ws.element_size()
     _check(load().frisk_reduce(ctypes.byref(d), ctypes.c_void_p(_stream_handle(stream))),
            "frisk_reduce")
     return dst

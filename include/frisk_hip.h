@@ -158,6 +158,12 @@ typedef enum frisk_reduce_kind {
  * 0..bits-1, and leaf position p holds reduced index
  * sum_j ((p >> j) & 1) << leaf_order[j].  This path runs one thread per
  * output and is meant for tile-sized reductions.
+ *
+ * workspace / workspace_bytes: optional device scratch (16-byte aligned)
+ * owned by the caller.  An axis-0 reduction of many rows with at least
+ * frisk_reduce_workspace_size() bytes splits the rows over the whole GPU
+ * in two passes (same tree, same result); without it, or when the size is
+ * 0, one pass runs.  Calls that share a workspace must not overlap.
  */
 typedef struct frisk_reduce_desc {
   int64_t rows, cols;
@@ -171,9 +177,16 @@ typedef struct frisk_reduce_desc {
   int64_t dst_stride;
   int32_t leaf_order_bits; /* 0: ascending index order */
   uint8_t leaf_order[32];
+  void* workspace;         /* optional, may be NULL */
+  int64_t workspace_bytes;
 } frisk_reduce_desc;
 
 int frisk_reduce(const frisk_reduce_desc* desc, void* stream);
+
+/* Workspace bytes that make frisk_reduce(desc) take its two-pass path (0:
+ * none is used), or a negative FRISK_E* code for an invalid descriptor.
+ * Pointers in desc are not read. */
+int64_t frisk_reduce_workspace_size(const frisk_reduce_desc* desc);
 
 /*
  * dst[r, c] = convert(src[r, c]) for a [rows, cols] tile (row strides

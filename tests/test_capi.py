@@ -209,3 +209,36 @@ def test_descriptor_layouts_match_the_header(tmp_path):
         assert got[f"{cname} size"] == ctypes.sizeof(py), cname
         for field, _ in py._fields_:
             assert got[f"{cname} {field}"] == getattr(py, field).offset, (cname, field)
+
+
+def test_reduce_workspace_size_query():
+    lib = rt.load()
+
+    def size(**over):
+        d = rt.ReduceDesc(rows=64, cols=64, dtype=rt.F32, kind=rt.REDUCE_SUM, axis=1, clear=1,
+                          src=16, ld_src=64, dst=16, dst_stride=1)
+        for key, val in over.items():
+            setattr(d, key, val)
+        return lib.frisk_reduce_workspace_size(ctypes.byref(d))
+
+    assert size() == 0                                           # axis 1: one pass
+    assert size(axis=0, rows=255) == 0                           # few rows: one pass
+    # 16384 columns = 128 strips of 128; 1024 workgroups -> 8 row blocks of 1024
+    assert size(axis=0, rows=8192, cols=16384, ld_src=16384) == 8 * 16384 * 4
+    # 32 strips: 32 blocks wanted; blocks are capped at 2^15 rows (8 groups x 2^12)
+    assert size(axis=0, rows=1 << 22, cols=4096, ld_src=4096) == 128 * 4096 * 4
+    # 64 columns = 16 slots: one strip, 16 row groups, 1024 blocks of at least 128 rows
+    assert size(axis=0, rows=4096, cols=64, ld_src=64) == 32 * 64 * 4
+    assert size(axis=0, rows=8192, cols=16384, ld_src=16384, leaf_order_bits=13,
+                leaf_order=(ctypes.c_uint8 * 32)(*range(13))) == 0
+    assert size(rows=0) == rt.EINVAL
+    assert lib.frisk_reduce_workspace_size(None) == rt.EINVAL
+
+
+def test_reduce_rejects_a_short_workspace():
+    rc, msg = reduce_call(axis=0, rows=8192, cols=16384, ld_src=16384, workspace=16,
+                          workspace_bytes=1000)
+    assert rc == rt.EINVAL and msg.startswith("frisk_reduce: workspace of 1000 bytes"), msg
+    rc, msg = reduce_call(axis=0, rows=8192, cols=16384, ld_src=16384, workspace=24,
+                          workspace_bytes=8 * 16384 * 4)
+    assert rc == rt.EINVAL and "16-byte aligned" in msg, msg

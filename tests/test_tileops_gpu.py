@@ -290,3 +290,27 @@ def test_execute_gemm_then_cast_sequence():
     rt.gemm(a, b, ref, trans_b=True)
     torch.cuda.synchronize()
     assert torch.equal(d.view(torch.int16), ref.view(torch.int16))
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("kind", ["sum", "max"])
+@pytest.mark.parametrize("shape", [(256, 3), (300, 256), (4097, 1031), (20000, 64)],
+                         ids=lambda s: f"{s[0]}x{s[1]}")
+def test_reduce_axis0_two_pass_matches_single_pass_and_oracle(dtype, kind, shape):
+    """The workspace path (row blocks over the whole GPU, then the block
+    roots) is the same tree as the single pass and the oracle."""
+    src = values(dtype, shape, seed=seed_of("twopass", dtype, kind, shape))
+    x = device_from_bits(dtype, T.to_bits(dtype, src))
+    rows, cols = shape
+    desc = rt.ReduceDesc(rows, cols, rt.torch_dtype_code(TORCH[dtype]), rt.REDUCE_KINDS[kind], 0,
+                         1, 16, cols, 16, 1)
+    assert rt.load().frisk_reduce_workspace_size(desc) > 0
+    two = Guarded((cols,), TORCH[dtype])
+    one = torch.empty(cols, dtype=TORCH[dtype], device="cuda")
+    rt.reduce(x, two.t, kind, axis=0)
+    rt.reduce(x, one, kind, axis=0, workspace=False)
+    torch.cuda.synchronize()
+    want = T.to_bits(dtype, T.reduce(src, kind, 0, dtype))
+    assert_same_bits(dtype, bits_of(dtype, two.t), want, "two-pass")
+    assert_same_bits(dtype, bits_of(dtype, one), want, "single pass")
+    assert two.guards_intact()
