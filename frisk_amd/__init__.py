@@ -9,6 +9,9 @@ create_session.  On top of that:
 execute  -- run a GEMM / attention tile program on the GPU (C-ABI)
 execute_packet / plan_packet -- run an execution packet written by
             frisk.export_execution (after frisk.infer_layouts)
+parse_module -- read textual tile IR (the printed form, or MLIR's generic
+            operation form) back into a module; `python -m frisk_amd.opt`
+            is the frisk-opt-like driver over it
 runtime  -- ctypes binding of libfrisk_hip.so (include/frisk_hip.h)
 build    -- ahead-of-time build of libfrisk_hip.so (hipcc, gfx950) and of
             the frisk_ffi extension (g++, pybind11)
@@ -43,6 +46,16 @@ def _ir():
 _HELPERS = ("FriskHelper", "create_context", "create_session")
 
 
+def parse_module(text: str, context=None):
+    """Parse textual tile IR into a module (in `context`, or a new one that
+    the module keeps alive as `module.context`)."""
+    from .common import utils
+    ctx = context if context is not None else utils.create_context()
+    module = _ir().frisk.parse_module(text, ctx)
+    module.context = ctx
+    return module
+
+
 def __getattr__(name: str):
     if name in _HELPERS:
         from .common import utils
@@ -53,6 +66,8 @@ def __getattr__(name: str):
     if name in ("execute_packet", "plan_packet"):
         from . import packet
         return getattr(packet, name)
+    if name == "parse_module":
+        return parse_module
     if name.startswith("__") or name == "frisk_ffi":
         raise AttributeError(name)
     ir = _ir()

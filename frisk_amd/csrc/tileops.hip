@@ -373,7 +373,15 @@ __global__ __launch_bounds__(tile::kThreads) void reduce_cols_final_kernel(
   const int64_t c = (int64_t)blockIdx.x * kThreads + threadIdx.x;
   if (c >= cols) return;
   Counter<E, KIND, 24> ctr;
-  for (uint32_t b = 0; b < blocks; ++b) ctr.push(b, partial[(int64_t)b * cols + c]);
+  uint32_t b = 0;
+  for (; b + 8 <= blocks; b += 8) {  // eight loads in flight, then their pushes
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = partial[(int64_t)(b + i) * cols + c];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ctr.push(b + i, v[i]);
+  }
+  for (; b < blocks; ++b) ctr.push(b, partial[(int64_t)b * cols + c]);
   float res = ctr.finish(blocks);
   if (!clear) res = combine<E, KIND>(load_as_f32<E>(dst, c * dst_stride), res);
   store_from_f32<E>(dst, c * dst_stride, res);

@@ -19,6 +19,7 @@
 
 #include "layout.h"
 #include "infer.h"
+#include "parse.h"
 #include "normalize.h"
 #include "ops.h"
 
@@ -1255,6 +1256,14 @@ void bindFrisk(py::module_& m) {
      py::arg("beam_width") = 32, py::arg("max_expanded_states") = 65536,
      py::arg("analysis_only") = false, py::arg("cost_profile") = py::none());
   // Pass: frisk-export-execution -> the execution packet as JSON text.
+  m.def("print_module", [](PyModule& mod, bool debugInfo) {
+    PrintOptions o;
+    o.debugInfo = debugInfo;
+    return printOp(requireOp(mod), o);
+  }, py::arg("module"), py::arg("debug_info") = false);
+  m.def("parse_module", [](const std::string& text, Context& ctx) {
+    return PyModule{{parseModule(&ctx, text)}};
+  }, py::arg("text"), py::arg("context"));
   m.def("export_execution", [](PyModule& mod) {
     std::string err;
     std::string out = exportExecution(requireOp(mod), &err);

@@ -1186,6 +1186,9 @@ class Inference {
       rep_.failure = "verification: an operation's layout is undetermined";
       return;
     }
+    // Classes no cost term consulted (a value nothing reads, such as an
+    // unused MMA result) are resolved from the chosen assignment here.
+    for (size_t c = 0; c < classes_.size(); ++c) classLayout((int)c, best_);
     rep_.features = f;
     rep_.conversions = conv;
     for (size_t i = 0; i < nv; ++i) {
