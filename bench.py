@@ -6,7 +6,8 @@ HBM-resident input: the bf16 GEMM C[4096, 4096] = A[4096, 4096] . B^T with
 B stored [N, K] (A and B ~ N(0, 1), f32 accumulation, bf16 output), the
 "bf16 4096^3" of BASELINE.json's metric.  `value` is its TFLOP/s
 (2*M*N*K per launch).  The same JSON line carries the other workloads the
-metric names, each timed the same way (W warm-up launches, then K timed
+metric names, each timed the same way (--settle seconds of untimed launches
+to bring the GPU to its steady clock, W warm-up launches, then K timed
 launches between device synchronisations): fp16 4096^3 NT,
 fp8-e4m3 4096x8192x8192 with per-tensor scales, int8 4096^3,
 and the flash-attention forward at b4 h32 s4096 d128 bf16, non-causal and
@@ -35,6 +36,7 @@ sys.path.insert(0, str(ROOT))
 PEAK = {"bf16": 2500.0, "f16": 2500.0, "fp8": 5000.0, "int8": 5000.0}  # dense TFLOP/s (TOP/s)
 REF_FIXED_TILE_US = {"single": 21.584, "graph": 6.5386}  # H100
 HBM_PEAK_GBS = 8000.0
+SETTLE_S = 0.25  # untimed load before each workload's warm-up, see time_launches
 
 
 def parse():
@@ -44,6 +46,8 @@ def parse():
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--only", default=None, help="run a single workload (for profilers)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--settle", type=float, default=SETTLE_S,
+                   help="seconds of untimed load before each workload's warm-up")
     return p.parse_args()
 
 
@@ -150,7 +154,17 @@ def make_workloads(torch, rt):
     }
 
 
-def time_launches(torch, fn, steps, warmup):
+def time_launches(torch, fn, steps, warmup, settle_s=SETTLE_S):
+    # An idle MI355X takes about 50 ms of load to reach its steady clock
+    # (measured: the first 25 ms of 4096^3 GEMMs run at 1090 TFLOP/s, every
+    # later window at 1230 for seconds).  The untimed settle runs the workload
+    # for settle_s before the W warm-up launches, so that the K timed launches
+    # see the clock a sustained workload sees.
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < settle_s:
+        for _ in range(8):
+            fn()
+        torch.cuda.synchronize()
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -274,7 +288,7 @@ def main():
     if args.only:
         label, flops, setup = work[args.only]
         fn = setup()
-        ms = time_launches(torch, fn, args.steps, args.warmup)
+        ms = time_launches(torch, fn, args.steps, args.warmup, args.settle)
         rate = {"gbs": flops / ms / 1e6} if label == "hbm" else {"tflops": flops / ms / 1e9}
         print(json.dumps({"workload": args.only, "ms": ms, **rate}), flush=True)
         return
@@ -285,7 +299,7 @@ def main():
             continue
         fn = setup()
         steps = args.steps
-        ms = time_launches(torch, fn, steps, args.warmup)
+        ms = time_launches(torch, fn, steps, args.warmup, args.settle)
         if label == "hbm":
             gbs = flops / ms / 1e6
             results[name] = {"bytes": flops, "ms": round(ms, 6), "gbs": round(gbs, 1),
@@ -308,6 +322,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle_s": args.settle,
         "ms_per_step": head["ms"],
         "higher_is_better": True,
         "scaling": "weak",
