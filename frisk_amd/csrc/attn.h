@@ -37,6 +37,8 @@
 
 #pragma once
 
+#include <atomic>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -469,17 +471,24 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(
 #endif  // __HIP_DEVICE_COMPILE__
 }
 
-// Workgroup shape per mask mode (measured on MI355X at b4 h32 s4096 d128):
-// non-causal runs 8 waves x 32 queries (one K/V tile feeds 256 queries);
-// causal runs 4 waves x 32 queries, whose smaller query blocks balance the
-// triangular work better.
-template <bool CAUSAL> struct AttnShape;
-template <> struct AttnShape<false> { static constexpr int QT = 1, NW = 8; };
-template <> struct AttnShape<true> { static constexpr int QT = 1, NW = 4; };
+// Compute units of the current device (cached per device).
+inline int attn_device_cus() {
+  static std::atomic<int> cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cached[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
 
-template <Elt T, Elt OUT, int D, bool CAUSAL>
-static hipError_t launch_attn(const AttnArgs& a, hipStream_t stream) {
-  constexpr int QT = AttnShape<CAUSAL>::QT, NW = AttnShape<CAUSAL>::NW, BM = 32 * QT * NW;
+// One workgroup shape: NW waves x 32 queries.
+template <Elt T, Elt OUT, int D, int NW, bool CAUSAL>
+static hipError_t launch_attn_nw(const AttnArgs& a, hipStream_t stream) {
+  constexpr int QT = 1, BM = 32 * QT * NW;
   auto kern = attn_fwd_kernel<T, OUT, D, QT, NW, CAUSAL>;
   constexpr int lds = 2 * AttnGeom<D>::kBuf;
   static const hipError_t attr =
@@ -493,6 +502,36 @@ static hipError_t launch_attn(const AttnArgs& a, hipStream_t stream) {
                      (int)a.seq_q, (int)a.seq_k, a.q_sb, a.q_sh, a.q_ss, a.k_sb, a.k_sh, a.k_ss,
                      a.v_sb, a.v_sh, a.v_ss, a.o_sb, a.o_sh, a.o_ss, scale_log2, q_blocks);
   return hipGetLastError();
+}
+
+// Workgroup shape per launch (measured on MI355X).  Every query's arithmetic
+// is the same in both shapes (same key blocks in the same order), so the
+// choice never changes a result bit.
+//  * Causal: 4 waves x 32 queries; the smaller query blocks balance the
+//    triangular work better.
+//  * Non-causal: 8 waves x 32 queries (one K/V tile feeds 256 queries)
+//    unless 4 waves finish sooner.  A CU runs one 8-wave workgroup or two
+//    4-wave ones at a time (two waves per SIMD), so in units of one 8-wave
+//    workgroup's run: 8 waves take ceil(w8 / CUs); 4 waves take one unit
+//    per 2 CUs workgroups, and a last round of at most one workgroup per CU
+//    about 0.6 (one wave per SIMD runs each wave faster).  Measured
+//    non-causal: b4 h32 s4096 d128 1030 vs 1012 TFLOP/s (8 kept);
+//    b8 h8 s1024 d64 657 vs 635 (8 kept); b2 h32 s1025 d64 366 vs 475 and
+//    b1 h16 s2048 d128 618 vs 839 (4 chosen).
+template <Elt T, Elt OUT, int D, bool CAUSAL>
+static hipError_t launch_attn(const AttnArgs& a, hipStream_t stream) {
+  if constexpr (CAUSAL) {
+    return launch_attn_nw<T, OUT, D, 4, true>(a, stream);
+  } else {
+    const int64_t cus = attn_device_cus();
+    const int64_t bh = a.batch * a.heads;
+    const int64_t w8 = bh * ((a.seq_q + 255) / 256), w4 = bh * ((a.seq_q + 127) / 128);
+    const double t8 = (double)((w8 + cus - 1) / cus);
+    const int64_t rest4 = w4 % (2 * cus);
+    const double t4 = (double)(w4 / (2 * cus)) + (rest4 == 0 ? 0.0 : rest4 <= cus ? 0.6 : 1.0);
+    return t4 < t8 ? launch_attn_nw<T, OUT, D, 4, false>(a, stream)
+                   : launch_attn_nw<T, OUT, D, 8, false>(a, stream);
+  }
 }
 
 // Every (input dtype, output dtype, mask) variant of one head_dim.
