@@ -11,7 +11,9 @@ to bring the GPU to its steady clock, W warm-up launches, then K timed
 launches between device synchronisations): fp16 4096^3 NT,
 fp8-e4m3 4096x8192x8192 with per-tensor scales, int8 4096^3,
 and the flash-attention forward at b4 h32 s4096 d128 bf16, non-causal and
-causal (configs[4]; causal FLOPs counted as half).  The HBM-bound tile ops
+causal (configs[4]; causal FLOPs counted as half).  `projection_sweep` holds
+the 12 bf16 projection GEMMs of configs[2], each against its own roofline
+(HBM or MFMA), with hipBLASLt's time on the same tensors beside it.  The HBM-bound tile ops
 on either side of them (frisk_reduce, frisk_copy with an f32 -> bf16
 conversion, frisk_fill) are reported in GB/s of algorithmic traffic (each
 input byte read once, each output byte written once) against the 8 TB/s
@@ -178,6 +180,45 @@ def time_launches(torch, fn, steps, warmup, settle_s=SETTLE_S):
     return start.elapsed_time(end) / steps  # ms per launch
 
 
+def projection_sweep(torch, rt, steps, warmup, settle_s):
+    """configs[2]: Y[M, N] = X[M, K] . W[N, K]^T in bf16 for (N, K) in
+    {(4096, 4096), (14336, 4096), (4096, 14336)} and M in {16, 128, 1024,
+    8192}, W ~ N(0, 0.02), X ~ N(0, 1).  Each shape is timed like the other
+    workloads, with the split-K workspace allocated before timing, and
+    reported against its own roofline: HBM when its FLOP per algorithmic
+    byte (M.K + N.K + M.N, 2 bytes each) is below the ridge (2.5 PFLOP/s /
+    8 TB/s), MFMA otherwise.  torch.matmul (hipBLASLt) on the same tensors
+    is timed beside it for reference."""
+    g = torch.Generator(device="cuda")
+    out = {}
+    ridge = PEAK["bf16"] * 1e12 / (HBM_PEAK_GBS * 1e9)
+    for n, k in ((4096, 4096), (14336, 4096), (4096, 14336)):
+        g.manual_seed(3)
+        w = (torch.randn(n, k, generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+        for m in (16, 128, 1024, 8192):
+            g.manual_seed(4 + m)
+            x = torch.randn(m, k, generator=g, device="cuda").to(torch.bfloat16)
+            y = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+            need = rt.gemm_workspace_bytes(x, w, y, trans_b=True)
+            ws = torch.empty(need, dtype=torch.uint8, device="cuda") if need > 0 else False
+            ms = time_launches(torch, lambda: rt.gemm(x, w, y, trans_b=True, workspace=ws),
+                               steps, warmup, settle_s)
+            wt = w.t()
+            ms_blas = time_launches(torch, lambda: torch.matmul(x, wt), steps, warmup, settle_s)
+            flops, nbytes = 2.0 * m * n * k, 2.0 * (m * k + n * k + m * n)
+            tf, gbs = flops / ms / 1e9, nbytes / ms / 1e6
+            bound = "hbm" if flops / nbytes < ridge else "mfma"
+            frac = gbs / HBM_PEAK_GBS if bound == "hbm" else tf / PEAK["bf16"]
+            out[f"m{m}_n{n}_k{k}"] = {"us": round(ms * 1e3, 2), "tflops": round(tf, 1),
+                                       "gbs": round(gbs, 1), "bound": bound,
+                                       "frac": round(frac, 4), "split_k": need > 0,
+                                       "hipblaslt_us": round(ms_blas * 1e3, 2)}
+            del x, y, ws
+        del w
+        torch.cuda.empty_cache()
+    return out
+
+
 def fixed_tile_latency(torch, rt):
     """The reference's 64x16 attention tile: single-launch and graph-amortized
     per-launch time in microseconds (see module docstring)."""
@@ -336,6 +377,7 @@ def main():
                      "unit": "TFLOP/s", "frac": round(head["tflops"] / PEAK["bf16"], 4),
                      "traffic": traffic},
         "workloads": results,
+        "projection_sweep": projection_sweep(torch, rt, args.steps, args.warmup, 0.1),
         "fixed_tile_64x16": fixed_tile_latency(torch, rt),
     }
     if not args.no_cpu:

@@ -37,8 +37,6 @@
 
 #pragma once
 
-#include <atomic>
-
 #include "common.h"
 #include "kernels.h"
 
@@ -471,20 +469,6 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(
 #endif  // __HIP_DEVICE_COMPILE__
 }
 
-// Compute units of the current device (cached per device).
-inline int attn_device_cus() {
-  static std::atomic<int> cached[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  int n = cached[dev].load(std::memory_order_relaxed);
-  if (n == 0) {
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-      n = 256;
-    cached[dev].store(n, std::memory_order_relaxed);
-  }
-  return n;
-}
-
 // One workgroup shape: NW waves x 32 queries.
 template <Elt T, Elt OUT, int D, int NW, bool CAUSAL>
 static hipError_t launch_attn_nw(const AttnArgs& a, hipStream_t stream) {
@@ -523,7 +507,7 @@ static hipError_t launch_attn(const AttnArgs& a, hipStream_t stream) {
   if constexpr (CAUSAL) {
     return launch_attn_nw<T, OUT, D, 4, true>(a, stream);
   } else {
-    const int64_t cus = attn_device_cus();
+    const int64_t cus = device_cus();
     const int64_t bh = a.batch * a.heads;
     const int64_t w8 = bh * ((a.seq_q + 255) / 256), w4 = bh * ((a.seq_q + 127) / 128);
     const double t8 = (double)((w8 + cus - 1) / cus);

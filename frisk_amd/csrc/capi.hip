@@ -128,9 +128,15 @@ const char* frisk_last_error(void) { return g_last_error.c_str(); }
 
 int frisk_abi_version(void) { return FRISK_ABI_VERSION; }
 
-int frisk_gemm(const frisk_gemm_desc* d, void* stream) {
-  g_last_error.clear();
-  if (!d) return fail(FRISK_EINVAL, "frisk_gemm: null descriptor");
+// Which kernel family a GEMM descriptor goes to.
+enum class GemmRoute { Skinny, Tn, Generic };
+
+// Checks of frisk_gemm / frisk_gemm_workspace_size, the kernel arguments
+// and the route; 0 or an error code.  With ptrs == false the operand
+// pointers are neither required nor read (alignment is assumed).
+int check_gemm(const frisk_gemm_desc* d, const char* fn, bool ptrs, frisk::GemmArgs& g,
+               GemmRoute& route) {
+  if (!d) return fail(FRISK_EINVAL, "%s: null descriptor", fn);
   if (d->m <= 0 || d->n <= 0 || d->k <= 0)
     return fail(FRISK_EINVAL, "legacy-gemm-shape: M, N, and K must be positive (got %lld, %lld, %lld)",
                 (long long)d->m, (long long)d->n, (long long)d->k);
@@ -140,24 +146,24 @@ int frisk_gemm(const frisk_gemm_desc* d, void* stream) {
   if (!gemm_pair_ok(d->a_type, d->c_type))
     return fail(FRISK_EINVAL, "legacy-gemm-type: unsupported A/B -> C element types %s -> %s",
                 dtype_name(d->a_type), dtype_name(d->c_type));
-  if (!d->a || !d->b || !d->c) return fail(FRISK_EINVAL, "frisk_gemm: null operand pointer");
+  if (ptrs && (!d->a || !d->b || !d->c)) return fail(FRISK_EINVAL, "%s: null operand pointer", fn);
   const int64_t a_cols = d->trans_a ? d->m : d->k;
   const int64_t b_cols = d->trans_b ? d->k : d->n;
   if (d->lda < a_cols || d->ldb < b_cols || d->ldc < d->n)
-    return fail(FRISK_EINVAL, "frisk_gemm: leading dimension too small (lda %lld < %lld, ldb %lld < %lld or ldc %lld < %lld)",
-                (long long)d->lda, (long long)a_cols, (long long)d->ldb, (long long)b_cols,
+    return fail(FRISK_EINVAL, "%s: leading dimension too small (lda %lld < %lld, ldb %lld < %lld or ldc %lld < %lld)",
+                fn, (long long)d->lda, (long long)a_cols, (long long)d->ldb, (long long)b_cols,
                 (long long)d->ldc, (long long)d->n);
   const bool fp8 = d->a_type == FRISK_E4M3;
   if (!fp8 && (d->scale_a != 1.0f || d->scale_b != 1.0f))
-    return fail(FRISK_EINVAL, "frisk_gemm: scale_a/scale_b apply to fp8 inputs only");
+    return fail(FRISK_EINVAL, "%s: scale_a/scale_b apply to fp8 inputs only", fn);
   if (d->m > INT32_MAX / 2 || d->n > INT32_MAX / 2 || d->k > INT32_MAX / 16)
-    return fail(FRISK_EUNSUP, "frisk_gemm: dimension beyond the 32-bit index range of the kernels");
+    return fail(FRISK_EUNSUP, "%s: dimension beyond the 32-bit index range of the kernels", fn);
   if (d->a_type == FRISK_I8 && d->k > 133152)
     // |sum| <= K * 127 * 128 must stay below 2^31 for exact int32 results.
-    return fail(FRISK_EUNSUP, "frisk_gemm: int8 K=%lld could overflow the int32 accumulator",
+    return fail(FRISK_EUNSUP, "%s: int8 K=%lld could overflow the int32 accumulator", fn,
                 (long long)d->k);
+  if (d->workspace_bytes < 0) return fail(FRISK_EINVAL, "%s: negative workspace_bytes", fn);
 
-  frisk::GemmArgs g;
   g.in = (frisk::Elt)d->a_type;
   g.out = (frisk::Elt)d->c_type;
   g.m = d->m; g.n = d->n; g.k = d->k;
@@ -171,14 +177,71 @@ int frisk_gemm(const frisk_gemm_desc* d, void* stream) {
   const int ies = esize(d->a_type), oes = esize(d->c_type);
   const bool mfma_type = d->a_type != FRISK_F32;
   const bool tn = !g.trans_a && g.trans_b;
+  const bool aligned = !ptrs || (aligned16(d->a) && aligned16(d->b) && aligned16(d->c));
   const bool vec_ok = (d->k * ies) % 16 == 0 && (d->lda * ies) % 16 == 0 &&
-                      (d->ldb * ies) % 16 == 0 && aligned16(d->a) && aligned16(d->b) &&
-                      aligned16(d->c) && (d->ldc * oes) % 16 == 0 && d->n % 8 == 0;
+                      (d->ldb * ies) % 16 == 0 && aligned && (d->ldc * oes) % 16 == 0 &&
+                      d->n % 8 == 0;
+  if (mfma_type && tn && vec_ok && frisk::gemm_skinny_supported(g)) route = GemmRoute::Skinny;
+  else if (mfma_type && tn && vec_ok) route = GemmRoute::Tn;
+  else route = GemmRoute::Generic;
+  return 0;
+}
+
+// Small-M rows this many or fewer stay on the skinny kernel when split;
+// more (up to its limit) run split on 128x128 tiles, which share each X
+// tile across the workgroup's waves through LDS.
+constexpr int64_t kSkinnySplitMaxM = 64;
+
+// Workspace bytes of the split-K plan frisk_gemm follows (0: none).
+int64_t gemm_workspace(const frisk::GemmArgs& g, GemmRoute route) {
+  const int cus = frisk::device_cus();
+  if (route == GemmRoute::Skinny) {
+    if (g.m > kSkinnySplitMaxM) return frisk::gemm_tn_split_plan(g, cus).workspace_bytes;
+    return frisk::gemm_skinny_plan(g, cus, true).workspace_bytes;
+  }
+  if (route == GemmRoute::Tn) return frisk::gemm_tn_split_plan(g, cus).workspace_bytes;
+  return 0;
+}
+
+int64_t frisk_gemm_workspace_size(const frisk_gemm_desc* d) {
+  g_last_error.clear();
+  frisk::GemmArgs g;
+  GemmRoute route;
+  const int rc = check_gemm(d, "frisk_gemm_workspace_size", false, g, route);
+  if (rc) return rc;
+  return gemm_workspace(g, route);
+}
+
+int frisk_gemm(const frisk_gemm_desc* d, void* stream) {
+  g_last_error.clear();
+  frisk::GemmArgs g;
+  GemmRoute route;
+  const int rc = check_gemm(d, "frisk_gemm", true, g, route);
+  if (rc) return rc;
+  void* ws = nullptr;
+  int64_t ws_bytes = 0;
+  if (d->workspace) {
+    const int64_t need = gemm_workspace(g, route);
+    if (need > 0) {
+      if (d->workspace_bytes < need)
+        return fail(FRISK_EINVAL, "frisk_gemm: workspace of %lld bytes, this GEMM takes %lld",
+                    (long long)d->workspace_bytes, (long long)need);
+      if ((uintptr_t)d->workspace % 16)
+        return fail(FRISK_EINVAL, "frisk_gemm: workspace must be 16-byte aligned");
+      ws = d->workspace;
+      ws_bytes = d->workspace_bytes;
+    }
+  }
   hipError_t e;
-  if (mfma_type && tn && vec_ok && frisk::gemm_skinny_supported(g))
-    e = frisk::gemm_skinny(g, (hipStream_t)stream);
-  else if (mfma_type && tn && vec_ok) e = frisk::gemm_tn_mfma(g, (hipStream_t)stream);
-  else e = frisk::gemm_generic_any(g, (hipStream_t)stream);
+  if (route == GemmRoute::Skinny && ws && g.m > kSkinnySplitMaxM) {
+    e = frisk::gemm_tn_mfma(g, (hipStream_t)stream, ws, ws_bytes);
+  } else if (route == GemmRoute::Skinny) {
+    e = frisk::gemm_skinny(g, (hipStream_t)stream, ws, ws_bytes);
+  } else if (route == GemmRoute::Tn) {
+    e = frisk::gemm_tn_mfma(g, (hipStream_t)stream, ws, ws_bytes);
+  } else {
+    e = frisk::gemm_generic_any(g, (hipStream_t)stream);
+  }
   if (e != hipSuccess) return hip_fail(e, "frisk_gemm launch");
   return FRISK_OK;
 }

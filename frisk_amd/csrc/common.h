@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 namespace frisk {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -95,6 +97,21 @@ __device__ inline void tile_of_block(int pid, int nblocks, int tiles_m, int tile
   const int in_group = pid % per_group;
   tm = first_m + in_group % rows;
   tn = in_group / rows;
+}
+
+// Compute units of the current device (cached per device; 256 if the
+// query fails).
+inline int device_cus() {
+  static std::atomic<int> cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cached[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
 }
 
 }  // namespace frisk

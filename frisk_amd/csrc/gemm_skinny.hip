@@ -15,7 +15,18 @@
 //  * W rows and the K tail are bounds-checked by raw buffer loads (offsets
 //    past num_records read zeros); X rows past M are clamped (their outputs
 //    are not stored).
+//  * Each workgroup starts its K walk at its own step (and wraps around), so
+//    the workgroups streaming different W columns do not all request the
+//    same X cache lines at once (128x4096x4096: 52.7 -> 39.0 us).
+//  * Split-K (when the caller provides a workspace): blockIdx.z picks a
+//    slice of the k-steps, each workgroup writes its f32 partial tile to
+//    workspace[slice][M][N], and gemm_splitk_sum_kernel adds the slices in
+//    slice order (deterministic) and converts.  Wider column tiles then cut
+//    the number of times X is streamed from L2 (every workgroup reads the
+//    X rows of its K range), and the slices restore the parallelism.
 //  * Roofline: HBM-bound; algorithmic bytes = M.K.2 + N.K.2 + M.N.2.
+
+#include <algorithm>
 
 #include "common.h"
 #include "kernels.h"
@@ -41,16 +52,20 @@ template <> struct Mfma16<Elt::F16> {
 };
 
 constexpr int kSkinnyWaves = 4;
-constexpr int kSkinnyUnroll = 4;  // k-steps loaded ahead per wave
+
+// k-steps loaded ahead per wave: as many as the load registers allow
+// (U (TM + TN) 4 VGPRs beside the TM TN 4 accumulator VGPRs).
+template <int TM, int TN> constexpr int skinny_unroll() { return TM + TN <= 10 ? 4 : 2; }
 
 }  // namespace
 
 template <Elt IN, Elt OUT, int TM, int TN>
 __global__ __launch_bounds__(64 * kSkinnyWaves) void gemm_skinny_kernel(
     const char* __restrict__ A, const char* __restrict__ B, void* __restrict__ C, int M, int N,
-    int Kb, int64_t lda_b, int64_t ldb_b, int64_t ldc, int accumulate) {
+    int Kb, int64_t lda_b, int64_t ldb_b, int64_t ldc, int accumulate, int steps_per_slice,
+    float* __restrict__ partial) {
 #if defined(__HIP_DEVICE_COMPILE__)
-  constexpr int U = kSkinnyUnroll;
+  constexpr int U = skinny_unroll<TM, TN>();
   __shared__ float red[kSkinnyWaves][TM * TN * 4][64];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -79,14 +94,22 @@ __global__ __launch_bounds__(64 * kSkinnyWaves) void gemm_skinny_kernel(
 #pragma unroll
     for (int j = 0; j < TN; ++j) acc[i][j] = f32x4_{0, 0, 0, 0};
 
-  const int nsteps = (Kb + 63) / 64;  // 64 B of K per MFMA k-step
+  // This workgroup's k-steps (64 B of K each): [s_begin, s_begin + nsteps),
+  // walked from a per-workgroup offset `rot`.
+  const int all_steps = (Kb + 63) / 64;
+  const int s_begin = blockIdx.z * steps_per_slice;
+  const int nsteps = min(all_steps - s_begin, steps_per_slice);
+  const int rot = (int)(((unsigned)blockIdx.x * 5u + (unsigned)blockIdx.y * 3u) % (unsigned)nsteps);
   const int kmax = Kb - quad * 16;    // this lane's 16 B chunk is live while kb < kmax
   for (int s0 = wave; s0 < nsteps; s0 += kSkinnyWaves * U) {
     i32x4 av[U][TM], bv[U][TN];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int kb = (s0 + kSkinnyWaves * u) * 64;
-      const bool live = kb < kmax;
+      const int st = s0 + kSkinnyWaves * u;
+      int sr = st + rot;
+      if (sr >= nsteps) sr -= nsteps;
+      const int kb = (s_begin + sr) * 64;
+      const bool live = st < nsteps && kb < kmax;
 #pragma unroll
       for (int t = 0; t < TN; ++t)
         bv[u][t] = __builtin_amdgcn_raw_buffer_load_b128(rsb, live ? b_off[t] + kb : 0x80000000u,
@@ -124,38 +147,133 @@ __global__ __launch_bounds__(64 * kSkinnyWaves) void gemm_skinny_kernel(
     const int row = m0 + i * 16 + 4 * (ln >> 4) + r;
     const int col = n0 + j * 16 + (ln & 15);
     if (row < M && col < N) {
-      const int64_t o = (int64_t)row * ldc + col;
-      if (accumulate) v += load_as_f32<OUT>(C, o);
-      store_from_f32<OUT>(C, o, v);
+      if (partial) {
+        partial[((int64_t)blockIdx.z * M + row) * N + col] = v;
+      } else {
+        const int64_t o = (int64_t)row * ldc + col;
+        if (accumulate) v += load_as_f32<OUT>(C, o);
+        store_from_f32<OUT>(C, o, v);
+      }
     }
   }
 #endif  // __HIP_DEVICE_COMPILE__
 }
 
+// C[row, 4c .. 4c+3] (+)= sum over slices z = 0, 1, ... of
+// partial[z][row][4c .. 4c+3], added in slice order.  N is a multiple of 4.
+template <Elt OUT>
+__global__ __launch_bounds__(256) void gemm_splitk_sum_kernel(const float* __restrict__ partial,
+                                                              int slices, int M, int N,
+                                                              void* __restrict__ C, int64_t ldc,
+                                                              int accumulate) {
+  const int64_t quads = (int64_t)N / 4;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)M * quads) return;
+  const int row = (int)(idx / quads), col = (int)(idx % quads) * 4;
+  f32x4 sum = *(const f32x4*)(partial + (int64_t)row * N + col);
+#pragma unroll 8
+  for (int z = 1; z < slices; ++z) sum += *(const f32x4*)(partial + ((int64_t)z * M + row) * N + col);
+  const int64_t o = (int64_t)row * ldc + col;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    float v = sum[e];
+    if (accumulate) v += load_as_f32<OUT>(C, o + e);
+    store_from_f32<OUT>(C, o + e, v);
+  }
+}
+
+SkinnyPlan gemm_skinny_plan(const GemmArgs& g, int cus, bool split) {
+  SkinnyPlan p;
+  p.tm = g.m <= 16 ? 1 : g.m <= 32 ? 2 : g.m <= 64 ? 4 : 8;
+  p.tn = g.n >= 8192 ? 2 : 1;  // 32-column tiles once N alone gives >= 256 of them
+  const int64_t kb = g.k * 2;   // bf16 / f16
+  const int64_t steps = (kb + 63) / 64;
+  p.steps_per_slice = (int)steps;
+  p.slices = 1;
+  p.workspace_bytes = 0;
+  // Below 64 MiB of W the unsplit kernel ends before a second launch pays
+  // (16 x 4096 x 4096: 10.5 us unsplit, 12.7 us split).
+  if (!split || g.n * kb < ((int64_t)64 << 20)) return p;
+  // Split-K with wider column tiles when the unsplit grid would stream X
+  // from L2 many times over: 64 columns per tile (32 at TM = 8, for
+  // registers); slices until the grid has two workgroups per CU, each slice
+  // at least 4 waves x U k-steps, the f32 partials at most a quarter of the
+  // bytes of W (S.M.N.4 <= N.K.2 / 4).
+  const int tn = p.tm <= 4 ? 4 : 2;
+  const int64_t tiles = ((g.n + 16 * tn - 1) / (16 * tn)) * ((g.m + 16 * p.tm - 1) / (16 * p.tm));
+  const int64_t min_steps = 4 * (p.tm + tn <= 10 ? 4 : 2);
+  int64_t slices = (2 * (int64_t)cus + tiles - 1) / tiles;
+  slices = std::min<int64_t>(slices, steps / min_steps);
+  slices = std::min<int64_t>(slices, kb / (16 * g.m));
+  slices = std::min<int64_t>(slices, 64);
+  if (slices >= 2) {
+    p.tn = tn;
+    p.steps_per_slice = (int)((steps + slices - 1) / slices);
+    p.slices = (int)((steps + p.steps_per_slice - 1) / p.steps_per_slice);
+    p.workspace_bytes = (int64_t)p.slices * g.m * g.n * 4;
+  }
+  return p;
+}
+
+namespace {
+
 template <Elt IN, Elt OUT, int TM, int TN>
-static hipError_t launch_skinny(const GemmArgs& g, hipStream_t stream) {
+hipError_t launch_skinny(const GemmArgs& g, const SkinnyPlan& p, float* partial,
+                         hipStream_t stream) {
   constexpr int kEsz = EltInfo<IN>::bytes;
-  dim3 grid((unsigned)((g.n + 16 * TN - 1) / (16 * TN)), (unsigned)((g.m + 16 * TM - 1) / (16 * TM)));
+  dim3 grid((unsigned)((g.n + 16 * TN - 1) / (16 * TN)), (unsigned)((g.m + 16 * TM - 1) / (16 * TM)),
+            (unsigned)(partial ? p.slices : 1));
+  const int steps = partial ? p.steps_per_slice : (int)((g.k * kEsz + 63) / 64);
   hipLaunchKernelGGL((gemm_skinny_kernel<IN, OUT, TM, TN>), grid, dim3(64 * kSkinnyWaves), 0,
                      stream, (const char*)g.a, (const char*)g.b, g.c, (int)g.m, (int)g.n,
-                     (int)(g.k * kEsz), g.lda * kEsz, g.ldb * kEsz, g.ldc, g.accumulate);
-  return hipGetLastError();
+                     (int)(g.k * kEsz), g.lda * kEsz, g.ldb * kEsz, g.ldc, g.accumulate, steps,
+                     partial);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || !partial) return e;
+  return gemm_splitk_sum(partial, p.slices, g, stream);
 }
 
 template <Elt IN, Elt OUT, int TN>
-static hipError_t skinny_by_m(const GemmArgs& g, hipStream_t s) {
-  if (g.m <= 16) return launch_skinny<IN, OUT, 1, TN>(g, s);
-  if (g.m <= 32) return launch_skinny<IN, OUT, 2, TN>(g, s);
-  if (g.m <= 64) return launch_skinny<IN, OUT, 4, TN>(g, s);
-  return launch_skinny<IN, OUT, 8, TN>(g, s);
+hipError_t skinny_by_m(const GemmArgs& g, const SkinnyPlan& p, float* partial, hipStream_t s) {
+  switch (p.tm) {
+    case 1: return launch_skinny<IN, OUT, 1, TN>(g, p, partial, s);
+    case 2: return launch_skinny<IN, OUT, 2, TN>(g, p, partial, s);
+    case 4: return launch_skinny<IN, OUT, 4, TN>(g, p, partial, s);
+    default: return launch_skinny<IN, OUT, 8, TN>(g, p, partial, s);
+  }
 }
 
-// 32-column tiles once N alone gives >= 256 of them (measured: better for
-// N = 14336, worse for N = 4096).
 template <Elt IN, Elt OUT>
-static hipError_t skinny_by_n(const GemmArgs& g, hipStream_t s) {
-  if (g.n >= 8192) return skinny_by_m<IN, OUT, 2>(g, s);
-  return skinny_by_m<IN, OUT, 1>(g, s);
+hipError_t skinny_by_n(const GemmArgs& g, const SkinnyPlan& p, float* partial, hipStream_t s) {
+  switch (p.tn) {
+    case 1: return skinny_by_m<IN, OUT, 1>(g, p, partial, s);
+    case 2: return skinny_by_m<IN, OUT, 2>(g, p, partial, s);
+    default: return skinny_by_m<IN, OUT, 4>(g, p, partial, s);
+  }
+}
+
+}  // namespace
+
+hipError_t gemm_splitk_sum(const float* partial, int slices, const GemmArgs& g, hipStream_t s) {
+  const int64_t threads = g.m * (g.n / 4);
+  const dim3 grid((unsigned)((threads + 255) / 256));
+  switch (g.out) {
+    case Elt::BF16:
+      hipLaunchKernelGGL((gemm_splitk_sum_kernel<Elt::BF16>), grid, dim3(256), 0, s, partial,
+                         slices, (int)g.m, (int)g.n, g.c, g.ldc, g.accumulate);
+      break;
+    case Elt::F16:
+      hipLaunchKernelGGL((gemm_splitk_sum_kernel<Elt::F16>), grid, dim3(256), 0, s, partial,
+                         slices, (int)g.m, (int)g.n, g.c, g.ldc, g.accumulate);
+      break;
+    case Elt::F32:
+      hipLaunchKernelGGL((gemm_splitk_sum_kernel<Elt::F32>), grid, dim3(256), 0, s, partial,
+                         slices, (int)g.m, (int)g.n, g.c, g.ldc, g.accumulate);
+      break;
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
 }
 
 bool gemm_skinny_supported(const GemmArgs& g) {
@@ -164,12 +282,18 @@ bool gemm_skinny_supported(const GemmArgs& g) {
   return type_ok && g.m <= kSkinnyMaxM && !g.trans_a && g.trans_b;
 }
 
-hipError_t gemm_skinny(const GemmArgs& g, hipStream_t s) {
+hipError_t gemm_skinny(const GemmArgs& g, hipStream_t s, void* workspace, int64_t workspace_bytes) {
+  SkinnyPlan p = gemm_skinny_plan(g, device_cus(), true);
+  float* partial = nullptr;
+  if (p.slices > 1 && workspace && workspace_bytes >= p.workspace_bytes)
+    partial = (float*)workspace;
+  else
+    p = gemm_skinny_plan(g, 0, false);
   switch (((int)g.in << 8) | (int)g.out) {
-    case ((int)Elt::BF16 << 8) | (int)Elt::BF16: return skinny_by_n<Elt::BF16, Elt::BF16>(g, s);
-    case ((int)Elt::BF16 << 8) | (int)Elt::F32: return skinny_by_n<Elt::BF16, Elt::F32>(g, s);
-    case ((int)Elt::F16 << 8) | (int)Elt::F16: return skinny_by_n<Elt::F16, Elt::F16>(g, s);
-    case ((int)Elt::F16 << 8) | (int)Elt::F32: return skinny_by_n<Elt::F16, Elt::F32>(g, s);
+    case ((int)Elt::BF16 << 8) | (int)Elt::BF16: return skinny_by_n<Elt::BF16, Elt::BF16>(g, p, partial, s);
+    case ((int)Elt::BF16 << 8) | (int)Elt::F32: return skinny_by_n<Elt::BF16, Elt::F32>(g, p, partial, s);
+    case ((int)Elt::F16 << 8) | (int)Elt::F16: return skinny_by_n<Elt::F16, Elt::F16>(g, p, partial, s);
+    case ((int)Elt::F16 << 8) | (int)Elt::F32: return skinny_by_n<Elt::F16, Elt::F32>(g, p, partial, s);
     default: return hipErrorInvalidValue;
   }
 }

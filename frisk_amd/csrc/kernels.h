@@ -26,7 +26,21 @@ struct GemmArgs {
 
 // 256x256-tile MFMA kernel; requires trans_a == 0, trans_b == 1 and 16 B
 // aligned, K-contiguous rows (checked by the caller).
-hipError_t gemm_tn_mfma(const GemmArgs& g, hipStream_t s);
+// Split-K plan of the 128x128-tile kernel (bf16/f16 TN only): `slices`
+// slices of kb_slice bytes of K whose f32 partials take workspace_bytes;
+// slices == 1 runs unsplit.
+struct TnSplitPlan {
+  int slices;
+  int64_t kb_slice;
+  int64_t workspace_bytes;
+};
+TnSplitPlan gemm_tn_split_plan(const GemmArgs& g, int cus);
+// With a workspace of at least the plan's bytes (16-byte aligned) the
+// planned split runs; otherwise the unsplit kernels.
+hipError_t gemm_tn_mfma(const GemmArgs& g, hipStream_t s, void* workspace, int64_t workspace_bytes);
+// C (+)= the sum over slices of partial[slice][M][N] (f32, added in slice
+// order), converted to C's type; N is a multiple of 4.
+hipError_t gemm_splitk_sum(const float* partial, int slices, const GemmArgs& g, hipStream_t s);
 // 256x256-tile kernel with four 128x128 waves (gemm4w.hip); same operand
 // contract as gemm_tn_mfma.
 hipError_t gemm_tn_w4(const GemmArgs& g, hipStream_t s);
@@ -39,7 +53,17 @@ hipError_t gemm_generic_any(const GemmArgs& g, hipStream_t s);
 #endif
 constexpr int kSkinnyMaxM = FRISK_SKINNY_MAX_M;
 bool gemm_skinny_supported(const GemmArgs& g);
-hipError_t gemm_skinny(const GemmArgs& g, hipStream_t s);
+// Launch shape of the small-M kernel: TM x TN 16x16 atoms per workgroup
+// (4 waves), `slices` K slices of `steps_per_slice` 64-byte k-steps, and
+// the f32 workspace the slices' partial tiles need (0 without split-K).
+struct SkinnyPlan {
+  int tm, tn, slices, steps_per_slice;
+  int64_t workspace_bytes;
+};
+SkinnyPlan gemm_skinny_plan(const GemmArgs& g, int cus, bool split);
+// Split-K runs when `workspace` holds at least the plan's workspace_bytes
+// (16-byte aligned); otherwise the unsplit kernel runs.
+hipError_t gemm_skinny(const GemmArgs& g, hipStream_t s, void* workspace, int64_t workspace_bytes);
 
 // A validated attention request.
 struct AttnArgs {

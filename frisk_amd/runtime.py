@@ -20,10 +20,11 @@ OK, EINVAL, EUNSUP, EHIP = 0, -1, -2, -3
 DTYPE_NAMES = {F32: "f32", F16: "f16", BF16: "bf16", E4M3: "e4m3", I8: "i8", I32: "i32", F64: "f64"}
 
 # Exported symbols declared by include/frisk_hip.h.
-EXPORTS = ("frisk_gemm", "frisk_attn_fwd", "frisk_reduce", "frisk_reduce_workspace_size",
+EXPORTS = ("frisk_gemm", "frisk_gemm_workspace_size", "frisk_attn_fwd", "frisk_reduce",
+           "frisk_reduce_workspace_size",
            "frisk_copy", "frisk_fill",
            "frisk_last_error", "frisk_abi_version", "frisk_probe_mfma_layout")
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 REDUCE_SUM, REDUCE_MAX, REDUCE_MIN = 0, 1, 2
 REDUCE_KINDS = {"sum": REDUCE_SUM, "add": REDUCE_SUM, "max": REDUCE_MAX, "min": REDUCE_MIN}
@@ -39,6 +40,7 @@ class GemmDesc(ctypes.Structure):
         ("b", ctypes.c_void_p), ("ldb", ctypes.c_int64),
         ("c", ctypes.c_void_p), ("ldc", ctypes.c_int64),
         ("scale_a", ctypes.c_float), ("scale_b", ctypes.c_float),
+        ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_int64),
     ]
 
 
@@ -104,6 +106,8 @@ def load() -> ctypes.CDLL:
     lib = ctypes.CDLL(str(LIB_PATH))
     lib.frisk_gemm.argtypes = [ctypes.POINTER(GemmDesc), ctypes.c_void_p]
     lib.frisk_gemm.restype = ctypes.c_int
+    lib.frisk_gemm_workspace_size.argtypes = [ctypes.POINTER(GemmDesc)]
+    lib.frisk_gemm_workspace_size.restype = ctypes.c_int64
     lib.frisk_attn_fwd.argtypes = [ctypes.POINTER(AttnDesc), ctypes.c_void_p]
     lib.frisk_attn_fwd.restype = ctypes.c_int
     lib.frisk_reduce.argtypes = [ctypes.POINTER(ReduceDesc), ctypes.c_void_p]
@@ -176,14 +180,35 @@ def gemm_desc(a, b, c, *, trans_a=False, trans_b=False, clear_accum=True,
     return GemmDesc(m, n, k, int(bool(trans_a)), int(bool(trans_b)),
                     torch_dtype_code(a.dtype), torch_dtype_code(b.dtype), torch_dtype_code(c.dtype),
                     int(bool(clear_accum)), a.data_ptr(), lda, b.data_ptr(), ldb,
-                    c.data_ptr(), ldc, float(scale_a), float(scale_b))
+                    c.data_ptr(), ldc, float(scale_a), float(scale_b), None, 0)
+
+
+def gemm_workspace_bytes(a, b, c, *, trans_a=False, trans_b=False) -> int:
+    """frisk_gemm_workspace_size for gemm(a, b, c, ...): 0 when no split-K applies."""
+    d = gemm_desc(a, b, c, trans_a=trans_a, trans_b=trans_b)
+    need = int(load().frisk_gemm_workspace_size(ctypes.byref(d)))
+    _check(need if need < 0 else OK, "frisk_gemm_workspace_size")
+    return need
 
 
 def gemm(a, b, c, *, trans_a=False, trans_b=False, clear_accum=True,
-         scale_a=1.0, scale_b=1.0, stream=None):
-    """C = op(A).op(B) (or C += ... with clear_accum=False) on the GPU."""
+         scale_a=1.0, scale_b=1.0, workspace=True, stream=None):
+    """C = op(A).op(B) (or C += ... with clear_accum=False) on the GPU.
+
+    `workspace`: True allocates the scratch frisk_gemm_workspace_size asks
+    for (torch's caching allocator), a device tensor supplies it, False runs
+    the unsplit kernels."""
     d = gemm_desc(a, b, c, trans_a=trans_a, trans_b=trans_b, clear_accum=clear_accum,
                   scale_a=scale_a, scale_b=scale_b)
+    ws = None
+    if workspace is not False:
+        need = load().frisk_gemm_workspace_size(ctypes.byref(d))
+        _check(int(need) if need < 0 else OK, "frisk_gemm_workspace_size")
+        if need > 0:
+            import torch
+            ws = workspace if workspace is not True else \
+                torch.empty(need, dtype=torch.uint8, device=c.device)
+            d.workspace, d.workspace_bytes = ws.data_ptr(), ws.numel() * ws.element_size()
     _check(load().frisk_gemm(ctypes.byref(d), ctypes.c_void_p(_stream_handle(stream))),
            "frisk_gemm")
     return c

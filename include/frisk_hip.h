@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define FRISK_ABI_VERSION 3
+#define FRISK_ABI_VERSION 4
 
 /* Element types (the dtype strings of ffi/ir.cpp:399-411 plus bf16/i8/i32). */
 typedef enum frisk_dtype {
@@ -83,6 +83,13 @@ typedef enum frisk_dtype {
  *   i8   x i8   -> i32              (exact int32 accumulation)
  * scale_a/scale_b are the per-tensor dequantisation factors of fp8 inputs
  * and must be 1.0 for every other type.
+ *
+ * workspace / workspace_bytes: optional device scratch (16-byte aligned)
+ * owned by the caller.  A small-M bf16/f16 GEMM given at least
+ * frisk_gemm_workspace_size() bytes splits K over the whole GPU (f32
+ * partial tiles, added in a fixed order, so the result does not depend on
+ * timing); without it, or when the size is 0, the unsplit kernels run.
+ * Calls that share a workspace must not overlap.
  */
 typedef struct frisk_gemm_desc {
   int64_t m, n, k;
@@ -96,9 +103,17 @@ typedef struct frisk_gemm_desc {
   void* c;
   int64_t ldc;
   float scale_a, scale_b;
+  void* workspace; /* optional, may be NULL */
+  int64_t workspace_bytes;
 } frisk_gemm_desc;
 
 int frisk_gemm(const frisk_gemm_desc* desc, void* stream);
+
+/* Workspace bytes that make frisk_gemm(desc) split K (0: none is used), or
+ * a negative FRISK_E* code for an invalid descriptor.  Pointers in desc are
+ * not read.  No counterpart in the reference (its GEMM ops take no
+ * scratch); callers that have none keep calling frisk_gemm unchanged. */
+int64_t frisk_gemm_workspace_size(const frisk_gemm_desc* desc);
 
 /*
  * Flash-attention forward over [batch, heads, seq, head_dim] tensors:

@@ -242,3 +242,48 @@ def test_reduce_rejects_a_short_workspace():
     rc, msg = reduce_call(axis=0, rows=8192, cols=16384, ld_src=16384, workspace=24,
                           workspace_bytes=8 * 16384 * 4)
     assert rc == rt.EINVAL and "16-byte aligned" in msg, msg
+
+
+def gemm_size(**over):
+    d = rt.GemmDesc(m=128, n=4096, k=4096, trans_a=0, trans_b=1, a_type=rt.BF16, b_type=rt.BF16,
+                    c_type=rt.BF16, clear_accum=1, a=16, lda=4096, b=16, ldb=4096, c=16,
+                    ldc=4096, scale_a=1.0, scale_b=1.0)
+    for key, val in over.items():
+        setattr(d, key, val)
+    return rt.load().frisk_gemm_workspace_size(ctypes.byref(d))
+
+
+def test_gemm_workspace_size_query():
+    # The plan assumes 256 CUs where no device answers (and MI355X has 256).
+    # 128 x 4096 x 4096 on 128 x 128 tiles: 32 tiles; 4 slices of 2 KiB of K
+    # (partials at most a quarter of the bytes of A and B: (M + N).K.2 /
+    # (16 M N) = 4; two workgroups per CU would take 16).
+    assert gemm_size() == 4 * 128 * 4096 * 4
+    # 256 x 4096 x 4096: 64 tiles, 2 slices.
+    assert gemm_size(m=256) == 2 * 256 * 4096 * 4
+    # 16 x 4096 x 14336 on the small-M kernel: 64-column tiles -> 64 tiles,
+    # 8 slices (partials at most a quarter of W).
+    assert gemm_size(m=16, k=14336, lda=14336, ldb=14336) == 8 * 16 * 4096 * 4
+    # 16 x 14336 x 4096: 224 tiles, 3 slices.
+    assert gemm_size(m=16, n=14336, ldc=14336) == 3 * 16 * 14336 * 4
+    # 16 x 4096 x 4096: W below 64 MiB, no split.
+    assert gemm_size(m=16) == 0
+    # No split: grids of at least CUs / 2 256x256 tiles, K too short to
+    # slice, layouts and types without a split kernel.
+    assert gemm_size(m=4096) == 0
+    assert gemm_size(k=256, lda=256, ldb=256) == 0
+    assert gemm_size(trans_b=0) == 0
+    assert gemm_size(a_type=rt.E4M3, b_type=rt.E4M3) == 0
+    assert gemm_size(m=0) == rt.EINVAL
+    assert rt.load().frisk_gemm_workspace_size(None) == rt.EINVAL
+
+
+def test_gemm_rejects_a_short_or_misaligned_workspace():
+    rc, msg = gemm_call(m=128, n=4096, k=4096, lda=4096, ldb=4096, ldc=4096, workspace=16,
+                        workspace_bytes=1000)
+    assert rc == rt.EINVAL and msg.startswith("frisk_gemm: workspace of 1000 bytes"), msg
+    rc, msg = gemm_call(m=128, n=4096, k=4096, lda=4096, ldb=4096, ldc=4096, workspace=24,
+                        workspace_bytes=1 << 30)
+    assert rc == rt.EINVAL and "16-byte aligned" in msg, msg
+    rc, msg = gemm_call(workspace=16, workspace_bytes=-1)
+    assert rc == rt.EINVAL and "negative workspace_bytes" in msg, msg

@@ -201,6 +201,42 @@ def run_sampled(m, n, k, in_dt, out_dt, seed, rows=48, std_a=1.0, std_b=1.0):
     return a, b, c, sa, sb
 
 
+# Small-M kernel split (M <= 64 with >= 64 MiB of W) and 128x128-tile split
+# (64 < M, few tiles), with ragged M, N and K tails.
+SPLIT_SHAPES = [(128, 4096, 4096), (16, 4096, 14336), (100, 1000, 3000), (48, 2600, 16384),
+                (1, 4096, 8192), (256, 520, 8192)]
+
+
+@pytest.mark.parametrize("m,n,k", SPLIT_SHAPES)
+@pytest.mark.parametrize("in_dt,out_dt", [(torch.bfloat16, torch.bfloat16),
+                                          (torch.float16, torch.float32)],
+                         ids=["bf16", "f16-f32"])
+@pytest.mark.parametrize("accumulate", [False, True], ids=["clear", "accum"])
+def test_split_k_small_m(m, n, k, in_dt, out_dt, accumulate):
+    # Small-M shapes that frisk_gemm_workspace_size splits over K: the split
+    # result against the fp64 oracle (C0 + A.B^T when accumulating), the
+    # same call again bit for bit, and the unsplit kernel within tolerance.
+    print(f"case split-k m={m} n={n} k={k} {in_dt}->{out_dt} accumulate={accumulate}", flush=True)
+    a = randn((m, k), 7 + m).to(in_dt)
+    b = randn((n, k), 8 + n).to(in_dt)
+    assert rt.gemm_workspace_bytes(a, b, torch.empty(m, n, dtype=out_dt, device="cuda"),
+                                   trans_b=True) > 0
+    c0 = randn((m, n), 9).to(out_dt)
+    outs = []
+    for ws in (True, True, False):
+        c = c0.clone()
+        rt.gemm(a, b, c, trans_b=True, clear_accum=not accumulate, workspace=ws)
+        torch.cuda.synchronize()
+        outs.append(c)
+    assert torch.equal(outs[0], outs[1])
+    r = sample_rows(m, 32, m + n)
+    ref = reference(a, b, False, True, 1.0, 1.0, rows=r)
+    if accumulate:
+        ref = ref + decode(c0[torch.from_numpy(r).cuda()])
+    for c in (outs[0], outs[2]):
+        check(decode(c[torch.from_numpy(r).cuda()]), ref, in_dt, out_dt)
+
+
 def test_config_c1_fp32_512():
     # fp32 C = A.B, row-major A and B, U[-1, 1].
     rng = np.random.default_rng(0)
