@@ -349,7 +349,8 @@ def main():
         else:
             tf = flops / ms / 1e9
             results[name] = {"dtype": label, "ms": round(ms, 6), "tflops": round(tf, 2),
-                             "frac_peak": round(tf / PEAK[label], 4)}
+                             "frac_peak": round(tf / PEAK[label], 4),
+                             "traffic": traffic_from_profile(name)}
         del fn
         torch.cuda.empty_cache()
 
