@@ -180,6 +180,20 @@ def time_launches(torch, fn, steps, warmup, settle_s=SETTLE_S):
     return start.elapsed_time(end) / steps  # ms per launch
 
 
+def launch_percentiles(torch, fn, n=50):
+    """p10 / p50 / p90 of n individually event-timed launches (ms)."""
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(n)]
+    for a, b in ev:
+        a.record()
+        fn()
+        b.record()
+    torch.cuda.synchronize()
+    t = sorted(a.elapsed_time(b) for a, b in ev)
+    pick = lambda q: t[min(n - 1, int(q * (n - 1) + 0.5))]
+    return {"p10": round(pick(0.1), 6), "p50": round(pick(0.5), 6), "p90": round(pick(0.9), 6)}
+
+
 def projection_sweep(torch, rt, steps, warmup, settle_s):
     """configs[2]: Y[M, N] = X[M, K] . W[N, K]^T in bf16 for (N, K) in
     {(4096, 4096), (14336, 4096), (4096, 14336)} and M in {16, 128, 1024,
@@ -187,24 +201,40 @@ def projection_sweep(torch, rt, steps, warmup, settle_s):
     workloads, with the split-K workspace allocated before timing, and
     reported against its own roofline: HBM when its FLOP per algorithmic
     byte (M.K + N.K + M.N, 2 bytes each) is below the ridge (2.5 PFLOP/s /
-    8 TB/s), MFMA otherwise.  torch.matmul (hipBLASLt) on the same tensors
-    is timed beside it for reference."""
+    8 TB/s), MFMA otherwise.  Consecutive launches cycle through enough
+    copies of X, W and Y (>= 600 MB together) that no launch finds its
+    operands in the 256 MB last-level cache.  torch.matmul (hipBLASLt) on
+    the same tensors, cycled the same way, is timed beside it."""
     g = torch.Generator(device="cuda")
     out = {}
     ridge = PEAK["bf16"] * 1e12 / (HBM_PEAK_GBS * 1e9)
     for n, k in ((4096, 4096), (14336, 4096), (4096, 14336)):
-        g.manual_seed(3)
-        w = (torch.randn(n, k, generator=g, device="cuda") * 0.02).to(torch.bfloat16)
         for m in (16, 128, 1024, 8192):
+            per_copy = 2 * (m * k + n * k + m * n)
+            copies = max(1, -(-600_000_000 // per_copy))
+            g.manual_seed(3)
+            w0 = (torch.randn(n, k, generator=g, device="cuda") * 0.02).to(torch.bfloat16)
             g.manual_seed(4 + m)
-            x = torch.randn(m, k, generator=g, device="cuda").to(torch.bfloat16)
-            y = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
-            need = rt.gemm_workspace_bytes(x, w, y, trans_b=True)
+            x0 = torch.randn(m, k, generator=g, device="cuda").to(torch.bfloat16)
+            ops = [(x0.clone(), w0.clone(), torch.empty(m, n, dtype=torch.bfloat16, device="cuda"))
+                   for _ in range(copies)]
+            del w0, x0
+            need = rt.gemm_workspace_bytes(*ops[0], trans_b=True)
             ws = torch.empty(need, dtype=torch.uint8, device="cuda") if need > 0 else False
-            ms = time_launches(torch, lambda: rt.gemm(x, w, y, trans_b=True, workspace=ws),
-                               steps, warmup, settle_s)
-            wt = w.t()
-            ms_blas = time_launches(torch, lambda: torch.matmul(x, wt), steps, warmup, settle_s)
+            turn = [0]
+
+            def ours():
+                x, w, y = ops[turn[0] % copies]
+                turn[0] += 1
+                rt.gemm(x, w, y, trans_b=True, workspace=ws)
+
+            def blas():
+                x, w, _ = ops[turn[0] % copies]
+                turn[0] += 1
+                torch.matmul(x, w.t())
+
+            ms = time_launches(torch, ours, steps, warmup, settle_s)
+            ms_blas = time_launches(torch, blas, steps, warmup, settle_s)
             flops, nbytes = 2.0 * m * n * k, 2.0 * (m * k + n * k + m * n)
             tf, gbs = flops / ms / 1e9, nbytes / ms / 1e6
             bound = "hbm" if flops / nbytes < ridge else "mfma"
@@ -212,10 +242,10 @@ def projection_sweep(torch, rt, steps, warmup, settle_s):
             out[f"m{m}_n{n}_k{k}"] = {"us": round(ms * 1e3, 2), "tflops": round(tf, 1),
                                        "gbs": round(gbs, 1), "bound": bound,
                                        "frac": round(frac, 4), "split_k": need > 0,
+                                       "operand_copies": copies,
                                        "hipblaslt_us": round(ms_blas * 1e3, 2)}
-            del x, y, ws
-        del w
-        torch.cuda.empty_cache()
+            del ops, ws
+            torch.cuda.empty_cache()
     return out
 
 
@@ -350,6 +380,7 @@ def main():
             tf = flops / ms / 1e9
             results[name] = {"dtype": label, "ms": round(ms, 6), "tflops": round(tf, 2),
                              "frac_peak": round(tf / PEAK[label], 4),
+                             "launch_ms": launch_percentiles(torch, fn),
                              "traffic": traffic_from_profile(name)}
         del fn
         torch.cuda.empty_cache()
