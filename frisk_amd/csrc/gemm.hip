@@ -413,6 +413,7 @@ template <Elt IN, Elt OUT>
 static hipError_t launch_tn(const GemmArgs& g, hipStream_t stream, int cus, float* partial,
                             const TnSplitPlan& p) {
   if constexpr (IN == Elt::BF16 || IN == Elt::F16) {
+    if (partial && p.big) return gemm_tn_w4_split(g, p.slices, p.kb_slice, partial, stream);
     if (partial) return launch_tn_split<IN, OUT>(g, p, partial, stream);
   }
   const int64_t tiles256 = ((g.m + 255) / 256) * ((g.n + 255) / 256);
@@ -431,32 +432,78 @@ static hipError_t launch_generic(const GemmArgs& g, hipStream_t stream) {
 
 #define FRISK_PAIR(i, o) (((int)(i) << 8) | (int)(o))
 
+// Time estimates (seconds) of the split choices, from rates measured on
+// MI355X with operands streaming from HBM: a 128x128-tile workgroup
+// computes about 2.5 TFLOP/s on its CU, a 256x256-tile one about 4.7; the
+// f32 partials are written and read back at about 3.5 TB/s plus one launch.
+namespace {
+constexpr double kRate128 = 2.5e12, kRate256 = 4.7e12, kPartialBw = 3.5e12, kLaunch = 3e-6;
+double rounds(int64_t wgs, int64_t slots) { return (double)((wgs + slots - 1) / slots); }
+double partial_cost(const GemmArgs& g, int64_t slices) {
+  return slices > 1 ? ((double)slices * g.m * g.n * 4 + (double)g.m * g.n * 2) / kPartialBw + kLaunch
+                    : 0.0;
+}
+}  // namespace
+
 TnSplitPlan gemm_tn_split_plan(const GemmArgs& g, int cus) {
-  TnSplitPlan p{1, g.k * 2, 0};
+  TnSplitPlan p{1, g.k * 2, 0, false};
   if ((g.in != Elt::BF16 && g.in != Elt::F16) || g.trans_a || !g.trans_b) return p;
-  // Split only grids that the 128x128 kernel runs (fewer than CUs / 2 big
-  // tiles) and that leave CUs without a tile: slices until two workgroups
-  // per CU, each slice at least 8 stages (8 x 64 B of K), and the f32
-  // partials at most a quarter of the bytes of A and B (their second pass
-  // then costs little).  Measured on the projection sweep: M = 128 runs
-  // 1.6-4.8x faster than on the unsplit small-M kernel (17.0 us at N = K =
-  // 4096 with 4 slices, against 24.0 with 16); M = 1024, N = 4096 (256
-  // tiles) runs 1.3x slower split in two.
+  // Grids of at least CUs / 2 256x256 tiles run unsplit on them.
   const int64_t tiles256 = ((g.m + 255) / 256) * ((g.n + 255) / 256);
   if (tiles256 >= cus / 2) return p;
   const int64_t tiles = ((g.m + 127) / 128) * ((g.n + 127) / 128);
-  if (tiles >= cus) return p;
   const int64_t kb = g.k * 2;
-  int64_t slices = (2 * (int64_t)cus + tiles - 1) / tiles;
-  slices = std::min<int64_t>(slices, kb / (8 * kRow));
-  slices = std::min<int64_t>(slices, (g.m + g.n) * kb / (16 * g.m * g.n));
-  slices = std::min<int64_t>(slices, 64);
-  if (slices < 2) return p;
-  const int64_t chunks = (kb + kRow - 1) / kRow;  // slices start on stage boundaries
-  p.kb_slice = ((chunks + slices - 1) / slices) * kRow;
-  p.slices = (int)((kb + p.kb_slice - 1) / p.kb_slice);
+  // 128x128 tiles.  Split only grids that leave CUs without a tile: slices
+  // until two workgroups per CU, each slice at least 8 stages (8 x 64 B of
+  // K), and the f32 partials at most a quarter of the bytes of A and B
+  // (their second pass then costs little).  Measured on the projection
+  // sweep: M = 128 runs 1.6-4.8x faster than on the unsplit small-M kernel
+  // (17.0 us at N = K = 4096 with 4 slices, against 24.0 with 16); M = 1024,
+  // N = 4096 (256 tiles) runs 1.3x slower split in two.
+  if (tiles < cus) {
+    int64_t slices = (2 * (int64_t)cus + tiles - 1) / tiles;
+    slices = std::min<int64_t>(slices, kb / (8 * kRow));
+    slices = std::min<int64_t>(slices, (g.m + g.n) * kb / (16 * g.m * g.n));
+    slices = std::min<int64_t>(slices, 64);
+    if (slices >= 2) {
+      const int64_t chunks = (kb + kRow - 1) / kRow;  // slices start on stage boundaries
+      p.kb_slice = ((chunks + slices - 1) / slices) * kRow;
+      p.slices = (int)((kb + p.kb_slice - 1) / p.kb_slice);
+      if (p.slices < 2) p = TnSplitPlan{1, kb, 0, false};
+    }
+  }
+  // 256x256 tiles split over K, for M past the small-M range, when the
+  // estimate says they end sooner (by 20%) than the 128x128 choice above:
+  // a 256-tile workgroup does twice the work per CU cycle, the split buys
+  // back the parallelism, the partials cost their traffic.  Slices of at
+  // least 8 stages (8 x 128 B of K).  Measured, operands from HBM:
+  // 512 x 4096 x 4096 53.1 -> 44.1 us, 768 x 2048 x 4096 51.4 -> 38.1,
+  // 1024 x 4096 x 14336 179.5 -> 133.3 (estimated ratios 0.66-0.69);
+  // 1024 x 4096 x 4096 stays on 128x128 tiles (57.6 us split against 54.4)
+  // and 256 x 4096 x 4096 on its 128x128 split (34.9 us on 256x256 tiles
+  // against 33.2; estimated ratio 0.84).
+  if (g.m > kSkinnyMaxM) {
+    const double flop128 = 2.0 * 128 * 128 * (double)(p.kb_slice / 2);
+    const double t128 = rounds(tiles * p.slices, cus) * flop128 / kRate128 + partial_cost(g, p.slices);
+    double best = 0.0;
+    int64_t best_s = 0;
+    for (int64_t sl = 2; sl <= 16 && kb / sl >= 1024; ++sl) {
+      const int64_t kb_slice = ((kb + 127) / 128 + sl - 1) / sl * 128;
+      const double t = rounds(tiles256 * sl, cus) * 2.0 * 256 * 256 * (double)(kb_slice / 2) / kRate256 +
+                       partial_cost(g, sl);
+      if (best_s == 0 || t < best) {
+        best = t;
+        best_s = sl;
+      }
+    }
+    if (best_s > 0 && best < 0.8 * t128) {
+      p.kb_slice = ((kb + 127) / 128 + best_s - 1) / best_s * 128;
+      p.slices = (int)((kb + p.kb_slice - 1) / p.kb_slice);
+      p.big = p.slices > 1;
+      if (!p.big) p = TnSplitPlan{1, kb, 0, false};
+    }
+  }
   p.workspace_bytes = p.slices > 1 ? (int64_t)p.slices * g.m * g.n * 4 : 0;
-  if (p.slices < 2) p = TnSplitPlan{1, kb, 0};
   return p;
 }
 

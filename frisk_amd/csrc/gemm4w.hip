@@ -57,8 +57,13 @@ constexpr int lds_bytes(int kr, int stages) { return stages * 2 * kBT * kr; }
 template <Elt IN, Elt OUT, int KR, int S>
 __global__ __launch_bounds__(g4::kThreads) void gemm_w4_kernel(
     const char* __restrict__ A, const char* __restrict__ B, void* __restrict__ C, int M, int N,
-    int Kb, int64_t lda_b, int64_t ldb_b, int64_t ldc, float scale, int accumulate) {
+    int Kb, int64_t lda_b, int64_t ldb_b, int64_t ldc, float scale, int accumulate, int kb_slice,
+    int64_t c_slice_bytes) {
 #if defined(__HIP_DEVICE_COMPILE__)
+  A += (int64_t)blockIdx.y * kb_slice;
+  B += (int64_t)blockIdx.y * kb_slice;
+  Kb = min(Kb - (int)blockIdx.y * kb_slice, kb_slice);
+  C = (char*)C + (int64_t)blockIdx.y * c_slice_bytes;
   using Op = Mfma32<IN>;
   using Acc = typename Op::Acc;
   using AccS = typename std::conditional<IN == Elt::I8, int32_t, float>::type;
@@ -343,8 +348,36 @@ static hipError_t launch_w4(const GemmArgs& g, hipStream_t stream) {
   const int tiles = (int)(((g.m + g4::kBT - 1) / g4::kBT) * ((g.n + g4::kBT - 1) / g4::kBT));
   hipLaunchKernelGGL(kern, dim3(tiles), dim3(g4::kThreads), kLds, stream, (const char*)g.a,
                      (const char*)g.b, g.c, (int)g.m, (int)g.n, (int)(g.k * kEsz),
-                     g.lda * kEsz, g.ldb * kEsz, g.ldc, g.scale, g.accumulate);
+                     g.lda * kEsz, g.ldb * kEsz, g.ldc, g.scale, g.accumulate,
+                     (int)(g.k * kEsz), (int64_t)0);
   return hipGetLastError();
+}
+
+template <Elt IN>
+static hipError_t launch_w4_split(const GemmArgs& g, int slices, int64_t kb_slice, float* partial,
+                                  hipStream_t stream) {
+  constexpr int KR = FRISK_G4_KR, S = FRISK_G4_STAGES;
+  constexpr int kEsz = EltInfo<IN>::bytes;
+  constexpr int kLds = g4::lds_bytes(KR, S);
+  auto kern = gemm_w4_kernel<IN, Elt::F32, KR, S>;
+  static const hipError_t attr =
+      hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
+  if (attr != hipSuccess) return attr;
+  const int tiles = (int)(((g.m + g4::kBT - 1) / g4::kBT) * ((g.n + g4::kBT - 1) / g4::kBT));
+  hipLaunchKernelGGL(kern, dim3(tiles, slices), dim3(g4::kThreads), kLds, stream, (const char*)g.a,
+                     (const char*)g.b, (void*)partial, (int)g.m, (int)g.n, (int)(g.k * kEsz),
+                     g.lda * kEsz, g.ldb * kEsz, g.n, 1.0f, 0, (int)kb_slice,
+                     (int64_t)g.m * g.n * 4);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  return gemm_splitk_sum(partial, slices, g, stream);
+}
+
+hipError_t gemm_tn_w4_split(const GemmArgs& g, int slices, int64_t kb_slice, float* partial,
+                            hipStream_t s) {
+  if (g.in == Elt::BF16) return launch_w4_split<Elt::BF16>(g, slices, kb_slice, partial, s);
+  if (g.in == Elt::F16) return launch_w4_split<Elt::F16>(g, slices, kb_slice, partial, s);
+  return hipErrorInvalidValue;
 }
 
 #define FRISK_PAIR(i, o) (((int)(i) << 8) | (int)(o))

@@ -33,7 +33,12 @@ struct TnSplitPlan {
   int slices;
   int64_t kb_slice;
   int64_t workspace_bytes;
+  bool big;  // slices run on 256x256 tiles (gemm4w.hip) instead of 128x128
 };
+// Split-K on the 256x256-tile kernel: f32 partials of each K slice into
+// `partial` ([slices][M][N]), then their sum in slice order into C.
+hipError_t gemm_tn_w4_split(const GemmArgs& g, int slices, int64_t kb_slice, float* partial,
+                            hipStream_t s);
 TnSplitPlan gemm_tn_split_plan(const GemmArgs& g, int cus);
 // With a workspace of at least the plan's bytes (16-byte aligned) the
 // planned split runs; otherwise the unsplit kernels.

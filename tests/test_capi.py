@@ -259,8 +259,13 @@ def test_gemm_workspace_size_query():
     # (partials at most a quarter of the bytes of A and B: (M + N).K.2 /
     # (16 M N) = 4; two workgroups per CU would take 16).
     assert gemm_size() == 4 * 128 * 4096 * 4
-    # 256 x 4096 x 4096: 64 tiles, 2 slices.
+    # 256 x 4096 x 4096: 64 tiles, 2 slices (256x256 tiles are estimated
+    # less than 20% faster).
     assert gemm_size(m=256) == 2 * 256 * 4096 * 4
+    # 512 x 4096 x 4096: 32 256x256 tiles in 8 slices of 1 KiB of K.
+    assert gemm_size(m=512) == 8 * 512 * 4096 * 4
+    # 1024 x 4096 x 4096: 256 128x128 tiles already fill the CUs; no split.
+    assert gemm_size(m=1024) == 0
     # 16 x 4096 x 14336 on the small-M kernel: 64-column tiles -> 64 tiles,
     # 8 slices (partials at most a quarter of W).
     assert gemm_size(m=16, k=14336, lda=14336, ldb=14336) == 8 * 16 * 4096 * 4
