@@ -10,8 +10,9 @@
 //  * Operands go straight from global memory into MFMA registers (no LDS):
 //    v_mfma_f32_16x16x32_{bf16,f16} wants lane l to hold 16 contiguous bytes
 //    of row l%16 at k-offset 8*(l/16), i.e. 16 B per lane and 64 B per row
-//    per load instruction.  U k-steps are loaded ahead of their MFMAs to keep
-//    enough bytes in flight to cover HBM latency.
+//    per load instruction.  Batches of U k-steps are double-buffered: batch
+//    b+1 is loaded while batch b is multiplied (operands from HBM:
+//    64x4096x4096 33.0 -> 24.5 us, 16x4096x4096 13.9 -> 11.9 us).
 //  * W rows and the K tail are bounds-checked by raw buffer loads (offsets
 //    past num_records read zeros); X rows past M are clamped (their outputs
 //    are not stored).
@@ -101,8 +102,11 @@ __global__ __launch_bounds__(64 * kSkinnyWaves) void gemm_skinny_kernel(
   const int nsteps = min(all_steps - s_begin, steps_per_slice);
   const int rot = (int)(((unsigned)blockIdx.x * 5u + (unsigned)blockIdx.y * 3u) % (unsigned)nsteps);
   const int kmax = Kb - quad * 16;    // this lane's 16 B chunk is live while kb < kmax
-  for (int s0 = wave; s0 < nsteps; s0 += kSkinnyWaves * U) {
-    i32x4 av[U][TM], bv[U][TN];
+  // Batches of U k-steps, double-buffered: the loads of batch b+1 are in
+  // flight while batch b is multiplied, so a workgroup pays one memory
+  // latency per slice instead of one per batch.  Batches past the end load
+  // nothing (zero reads) and add zero products.
+  auto load = [&](int s0, i32x4 (&av)[U][TM], i32x4 (&bv)[U][TN]) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int st = s0 + kSkinnyWaves * u;
@@ -119,12 +123,24 @@ __global__ __launch_bounds__(64 * kSkinnyWaves) void gemm_skinny_kernel(
         av[u][t] = __builtin_amdgcn_raw_buffer_load_b128(rsa, live ? a_off[t] + kb : 0x80000000u,
                                                          0, 0);
     }
+  };
+  auto mul = [&](const i32x4 (&av)[U][TM], const i32x4 (&bv)[U][TN]) {
 #pragma unroll
     for (int u = 0; u < U; ++u)
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = Mfma16<IN>::run(av[u][i], bv[u][j], acc[i][j]);
+  };
+  constexpr int kBatch = kSkinnyWaves * U;
+  i32x4 a0[U][TM], b0[U][TN], a1[U][TM], b1[U][TN];
+  load(wave, a0, b0);
+  for (int s0 = wave; s0 < nsteps; s0 += 2 * kBatch) {
+    load(s0 + kBatch, a1, b1);
+    mul(a0, b0);
+    if (s0 + kBatch >= nsteps) break;
+    load(s0 + 2 * kBatch, a0, b0);
+    mul(a1, b1);
   }
 
   // Sum the 4 waves' partial tiles.  The 16x16 accumulator holds
