@@ -267,10 +267,10 @@ def test_gemm_workspace_size_query():
     # 1024 x 4096 x 4096: 256 128x128 tiles already fill the CUs; no split.
     assert gemm_size(m=1024) == 0
     # 16 x 4096 x 14336 on the small-M kernel: 64-column tiles -> 64 tiles,
-    # 8 slices (partials at most a quarter of W).
-    assert gemm_size(m=16, k=14336, lda=14336, ldb=14336) == 8 * 16 * 4096 * 4
-    # 16 x 14336 x 4096: 224 tiles, 3 slices.
-    assert gemm_size(m=16, n=14336, ldc=14336) == 3 * 16 * 14336 * 4
+    # 4 slices (one workgroup per CU).
+    assert gemm_size(m=16, k=14336, lda=14336, ldb=14336) == 4 * 16 * 4096 * 4
+    # 16 x 14336 x 4096: 224 tiles, 2 slices.
+    assert gemm_size(m=16, n=14336, ldc=14336) == 2 * 16 * 14336 * 4
     # 16 x 4096 x 4096: W below 64 MiB, no split.
     assert gemm_size(m=16) == 0
     # No split: grids of at least CUs / 2 256x256 tiles, K too short to
