@@ -47,6 +47,26 @@ def test_execute_whole_gemm_accumulates():
     assert G.row_scaled_error(decode(c), ref) <= 1e-5
 
 
+@pytest.mark.parametrize("M,N,K", [(32, 2048, 16384), (512, 1024, 8192)])
+def test_execute_whole_gemm_split_k(M, N, K):
+    # Shapes whose frisk_gemm splits K when given a workspace (the small-M
+    # kernel at M = 32 with 64 MiB of W; an under-filled tile grid at
+    # M = 512): execute() passes one, and the result matches the fp64 oracle
+    # on sampled rows.
+    from frisk_amd import runtime as rt
+    print(f"execute whole gemm split-k {M}x{N}x{K}", flush=True)
+    s, _ = P.whole_gemm(M, N, K, dtype="bf16", out="bf16", trans_b=True)
+    a = randn((M, K), 21).to(torch.bfloat16)
+    b = randn((N, K), 22).to(torch.bfloat16)
+    c = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device="cuda")
+    assert rt.gemm_workspace_bytes(a, b, c, trans_b=True) > 0
+    F.execute(s.module, "gemm", [a, b, c])
+    torch.cuda.synchronize()
+    rows = np.arange(0, M, max(1, M // 32))
+    ref = decode(a)[rows] @ decode(b).T
+    assert G.row_scaled_error(decode(c)[rows], ref) <= 1e-2
+
+
 @pytest.mark.parametrize("k_transposed", [False, True])
 @pytest.mark.parametrize("causal", [False, True])
 def test_execute_attention(k_transposed, causal):
