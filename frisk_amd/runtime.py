@@ -154,6 +154,12 @@ def torch_dtype_code(dt) -> int:
 def _stream_handle(stream) -> int:
     import torch
     if stream is None:
+        # torch's raw accessor returns the current stream's handle without
+        # building a Stream object (0.1 us against 3 us per launch); the
+        # public path stays as the fallback.
+        raw = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+        if raw is not None:
+            return int(raw(torch.cuda.current_device()))
         stream = torch.cuda.current_stream()
     return int(stream.cuda_stream) if hasattr(stream, "cuda_stream") else int(stream)
 
@@ -232,14 +238,17 @@ def probe_mfma_layout(atom: int, out, stream=None):
 
 
 def attn_desc(q, k, v, o, *, causal=False, sm_scale=None, lse=None) -> AttnDesc:
+    shapes, strides = [], []
     for name, t in (("Q", q), ("K", k), ("V", v), ("O", o)):
-        if t.dim() != 4 or t.stride(3) != 1 or not t.is_cuda:
+        sh, st = t.shape, t.stride()
+        if len(sh) != 4 or st[3] != 1 or not t.is_cuda:
             raise ValueError(f"{name} must be a [batch, heads, seq, head_dim] device tensor "
                              "with unit head_dim stride")
-    b, h, sq, d = q.shape
-    sk = k.shape[2]
-    if tuple(k.shape) != (b, h, sk, d) or tuple(v.shape) != (b, h, sk, d) \
-            or tuple(o.shape) != (b, h, sq, d):
+        shapes.append(tuple(sh))
+        strides.append(st)
+    b, h, sq, d = shapes[0]
+    sk = shapes[1][2]
+    if shapes[1] != (b, h, sk, d) or shapes[2] != (b, h, sk, d) or shapes[3] != (b, h, sq, d):
         raise ValueError("attention shapes disagree")
     if not (q.dtype == k.dtype == v.dtype):
         raise ValueError("Q/K/V must share one dtype")
@@ -251,12 +260,13 @@ def attn_desc(q, k, v, o, *, causal=False, sm_scale=None, lse=None) -> AttnDesc:
         raise ValueError("lse must be a contiguous f32 [batch, heads, seq_q] tensor")
     if sm_scale is None:
         sm_scale = d ** -0.5
+    qs, ks, vs, os_ = strides
     return AttnDesc(b, h, sq, sk, d, torch_dtype_code(q.dtype), int(bool(causal)),
                     float(sm_scale),
-                    q.data_ptr(), q.stride(0), q.stride(1), q.stride(2),
-                    k.data_ptr(), k.stride(0), k.stride(1), k.stride(2),
-                    v.data_ptr(), v.stride(0), v.stride(1), v.stride(2),
-                    o.data_ptr(), o.stride(0), o.stride(1), o.stride(2),
+                    q.data_ptr(), qs[0], qs[1], qs[2],
+                    k.data_ptr(), ks[0], ks[1], ks[2],
+                    v.data_ptr(), vs[0], vs[1], vs[2],
+                    o.data_ptr(), os_[0], os_[1], os_[2],
                     lse.data_ptr() if lse is not None else None, torch_dtype_code(o.dtype))
 
 
