@@ -269,8 +269,11 @@ def test_gemm_workspace_size_query():
     # 16 x 4096 x 14336 on the small-M kernel: 64-column tiles -> 64 tiles,
     # 4 slices (one workgroup per CU).
     assert gemm_size(m=16, k=14336, lda=14336, ldb=14336) == 4 * 16 * 4096 * 4
-    # 16 x 14336 x 4096: 224 tiles, 2 slices.
-    assert gemm_size(m=16, n=14336, ldc=14336) == 2 * 16 * 14336 * 4
+    # 16 x 14336 x 4096: 224 tiles fill 7/8 of 256 CUs in one round, no split
+    # (also at M = 64); 16 x 8192 x 8192: 128 tiles, 2 slices.
+    assert gemm_size(m=16, n=14336, ldc=14336) == 0
+    assert gemm_size(m=64, n=14336, ldc=14336) == 0
+    assert gemm_size(m=16, n=8192, k=8192, lda=8192, ldb=8192, ldc=8192) == 2 * 16 * 8192 * 4
     # 16 x 4096 x 4096: W below 64 MiB, no split.
     assert gemm_size(m=16) == 0
     # No split: grids of at least CUs / 2 256x256 tiles, K too short to

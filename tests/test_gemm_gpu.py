@@ -127,6 +127,26 @@ def test_small_m_kernel(m, n, k, in_dt, out_dt):
     check(decode(c), reference(a, b, False, True, 1.0, 1.0) + decode(c0), in_dt, out_dt)
 
 
+@pytest.mark.parametrize("m,n,k", [(16, 14336, 4096), (40, 14000, 4800)])
+def test_small_m_wide_tiles_unsplit(m, n, k):
+    # At least 64 MiB of W in 64-column tiles that fill most CUs in one
+    # round: the small-M kernel runs unsplit, with or without a workspace,
+    # and asks for none (ragged M and N in the second shape).
+    print(f"case skinny wide m={m} n={n} k={k}", flush=True)
+    a, b, _, _ = make_operands(m, n, k, torch.bfloat16, False, True, seed=m + n + k)
+    c = torch.zeros(m, n, dtype=torch.bfloat16, device="cuda")
+    assert rt.gemm_workspace_bytes(a, b, c, trans_b=True) == 0
+    rt.gemm(a, b, c, trans_b=True)
+    torch.cuda.synchronize()
+    ref = reference(a, b, False, True, 1.0, 1.0)
+    check(decode(c), ref, torch.bfloat16, torch.bfloat16)
+    c0 = randn((m, n), 3).to(torch.bfloat16)
+    c = c0.clone()
+    rt.gemm(a, b, c, trans_b=True, clear_accum=False, workspace=False)
+    torch.cuda.synchronize()
+    check(decode(c), ref + decode(c0), torch.bfloat16, torch.bfloat16)
+
+
 BIG_RAGGED = [(4000, 2056, 1000, torch.bfloat16, torch.bfloat16),
               (4096, 4104, 776, torch.float16, torch.float32),
               (3000, 3000, 2000, FP8, torch.float32),
