@@ -36,7 +36,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 PEAK = {"bf16": 2500.0, "f16": 2500.0, "fp8": 5000.0, "int8": 5000.0}  # dense TFLOP/s (TOP/s)
-REF_FIXED_TILE_US = {"single": 21.584, "graph": 6.5386}  # H100
+REF_FIXED_TILE_US = {"single": 21.584, "graph": 6.5386}  # the reference's published H100 figures
 HBM_PEAK_GBS = 8000.0
 SETTLE_S = 0.25  # untimed load before each workload's warm-up, see time_launches
 
@@ -345,7 +345,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
-              "GEMM and attention shard across GPUs without exchange, see DESIGN.md",
+              "GEMM and attention shard across GPUs without exchange",
               file=sys.stderr)
         sys.exit(2)
     import torch
