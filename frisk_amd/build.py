@@ -41,7 +41,7 @@ COMMON = [
 VGPR_FORM = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
 # Files whose MFMA accumulators live in AGPRs: their kernels hold 256
 # accumulator registers per lane and read them only in the epilogue.
-AGPR_ACC = {"gemm4w.hip"}
+AGPR_ACC_PREFIX = "gemm_w4_"
 
 
 def sources() -> list[Path]:
@@ -55,7 +55,7 @@ def build(verbose: bool = False, extra: list[str] | None = None) -> Path:
 
     def compile_one(src: Path) -> Path:
         obj = objdir / (src.stem + ".o")
-        form = [] if src.name in AGPR_ACC else VGPR_FORM
+        form = [] if src.name.startswith(AGPR_ACC_PREFIX) else VGPR_FORM
         cmd = [HIPCC, *flags, *form, "-c", str(src), "-o", str(obj)]
         if verbose:
             print(" ".join(shlex.quote(c) for c in cmd), flush=True)

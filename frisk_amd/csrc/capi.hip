@@ -37,6 +37,11 @@ int hip_fail(hipError_t e, const char* what) {
   return fail(FRISK_EHIP, "%s: %s", what, hipGetErrorString(e));
 }
 
+// Resets the calling thread's HIP error state before a launch, so that the
+// hipGetLastError() after it reports that launch only, not a failure left
+// behind by an unrelated earlier HIP call.
+void clear_stale_error() { (void)hipGetLastError(); }
+
 const char* dtype_name(int t) {
   switch (t) {
     case FRISK_F32: return "f32";
@@ -129,7 +134,11 @@ const char* frisk_last_error(void) { return g_last_error.c_str(); }
 int frisk_abi_version(void) { return FRISK_ABI_VERSION; }
 
 // Which kernel family a GEMM descriptor goes to.
-enum class GemmRoute { Skinny, Tn, Generic };
+enum class GemmRoute { Skinny, Mfma, Generic };
+
+// Rows of the largest operand tile a GEMM kernel addresses from one buffer
+// base (the 256x256 tiles).
+constexpr int64_t kMaxTileRows = 256;
 
 // Checks of frisk_gemm / frisk_gemm_workspace_size, the kernel arguments
 // and the route; 0 or an error code.  With ptrs == false the operand
@@ -158,10 +167,11 @@ int check_gemm(const frisk_gemm_desc* d, const char* fn, bool ptrs, frisk::GemmA
     return fail(FRISK_EINVAL, "%s: scale_a/scale_b apply to fp8 inputs only", fn);
   if (d->m > INT32_MAX / 2 || d->n > INT32_MAX / 2 || d->k > INT32_MAX / 16)
     return fail(FRISK_EUNSUP, "%s: dimension beyond the 32-bit index range of the kernels", fn);
-  if (d->a_type == FRISK_I8 && d->k > 133152)
-    // |sum| <= K * 127 * 128 must stay below 2^31 for exact int32 results.
-    return fail(FRISK_EUNSUP, "%s: int8 K=%lld could overflow the int32 accumulator", fn,
-                (long long)d->k);
+  if (d->a_type == FRISK_I8 && d->k > INT32_MAX / (128 * 128))
+    // Every product of two int8 values has |a b| <= 128 * 128 = 2^14, so
+    // K <= (2^31 - 1) / 2^14 = 131071 keeps every int32 sum exact.
+    return fail(FRISK_EUNSUP, "%s: int8 K=%lld could overflow the int32 accumulator (K <= 131071)",
+                fn, (long long)d->k);
   if (d->workspace_bytes < 0) return fail(FRISK_EINVAL, "%s: negative workspace_bytes", fn);
 
   g.in = (frisk::Elt)d->a_type;
@@ -174,15 +184,28 @@ int check_gemm(const frisk_gemm_desc* d, const char* fn, bool ptrs, frisk::GemmA
   g.scale = fp8 ? d->scale_a * d->scale_b : 1.0f;
   g.accumulate = d->clear_accum ? 0 : 1;
 
+  // The MFMA kernels stage 16 B pieces of operand rows: 16 B aligned bases
+  // and row pitches, and for an operand stored K-major (A not transposed, B
+  // transposed) whole 16 B pieces of K; the epilogue stores 16 B per lane
+  // into C rows.  Their buffer loads take 32-bit offsets from one tile
+  // origin: a K-major operand reaches (rows - 1) pitches plus K, an MN-major
+  // one (K - 1) pitches plus a tile row; beyond 2^31 - 1 bytes the generic
+  // kernel (64-bit indexing) runs instead.
   const int ies = esize(d->a_type), oes = esize(d->c_type);
   const bool mfma_type = d->a_type != FRISK_F32;
-  const bool tn = !g.trans_a && g.trans_b;
+  const bool a_kmajor = !g.trans_a, b_kmajor = g.trans_b;
   const bool aligned = !ptrs || (aligned16(d->a) && aligned16(d->b) && aligned16(d->c));
-  const bool vec_ok = (d->k * ies) % 16 == 0 && (d->lda * ies) % 16 == 0 &&
-                      (d->ldb * ies) % 16 == 0 && aligned && (d->ldc * oes) % 16 == 0 &&
-                      d->n % 8 == 0;
-  if (mfma_type && tn && vec_ok && frisk::gemm_skinny_supported(g)) route = GemmRoute::Skinny;
-  else if (mfma_type && tn && vec_ok) route = GemmRoute::Tn;
+  const bool k_pieces = (!a_kmajor && !b_kmajor) || (d->k * ies) % 16 == 0;
+  const bool vec_ok = aligned && k_pieces && (d->lda * ies) % 16 == 0 &&
+                      (d->ldb * ies) % 16 == 0 && (d->ldc * oes) % 16 == 0;
+  auto reach = [&](bool kmajor, int64_t ld) {
+    return kmajor ? (kMaxTileRows - 1) * ld * ies + d->k * ies
+                  : (d->k - 1) * ld * ies + kMaxTileRows * ies;
+  };
+  const bool offsets_ok = reach(a_kmajor, d->lda) <= INT32_MAX && reach(b_kmajor, d->ldb) <= INT32_MAX;
+  const bool nt = a_kmajor && b_kmajor;
+  if (mfma_type && nt && vec_ok && offsets_ok && frisk::gemm_skinny_supported(g)) route = GemmRoute::Skinny;
+  else if (mfma_type && vec_ok && offsets_ok) route = GemmRoute::Mfma;
   else route = GemmRoute::Generic;
   return 0;
 }
@@ -196,10 +219,10 @@ constexpr int64_t kSkinnySplitMaxM = 64;
 int64_t gemm_workspace(const frisk::GemmArgs& g, GemmRoute route) {
   const int cus = frisk::device_cus();
   if (route == GemmRoute::Skinny) {
-    if (g.m > kSkinnySplitMaxM) return frisk::gemm_tn_split_plan(g, cus).workspace_bytes;
+    if (g.m > kSkinnySplitMaxM) return frisk::gemm_split_plan(g, cus).workspace_bytes;
     return frisk::gemm_skinny_plan(g, cus, true).workspace_bytes;
   }
-  if (route == GemmRoute::Tn) return frisk::gemm_tn_split_plan(g, cus).workspace_bytes;
+  if (route == GemmRoute::Mfma) return frisk::gemm_split_plan(g, cus).workspace_bytes;
   return 0;
 }
 
@@ -210,6 +233,63 @@ int64_t frisk_gemm_workspace_size(const frisk_gemm_desc* d) {
   const int rc = check_gemm(d, "frisk_gemm_workspace_size", false, g, route);
   if (rc) return rc;
   return gemm_workspace(g, route);
+}
+
+const char* mfma_atom(frisk::Elt in) {
+  switch (in) {
+    case frisk::Elt::BF16: return "v_mfma_f32_32x32x16_bf16";
+    case frisk::Elt::F16: return "v_mfma_f32_32x32x16_f16";
+    case frisk::Elt::E4M3: return "v_mfma_scale_f32_32x32x64_f8f6f4";
+    case frisk::Elt::I8: return "v_mfma_i32_32x32x32_i8";
+    default: return "";
+  }
+}
+
+int frisk_gemm_plan(const frisk_gemm_desc* d, char* buf, int64_t len) {
+  g_last_error.clear();
+  frisk::GemmArgs g;
+  GemmRoute route;
+  const int rc = check_gemm(d, "frisk_gemm_plan", false, g, route);
+  if (rc) return rc;
+  if (!buf || len <= 0) return fail(FRISK_EINVAL, "frisk_gemm_plan: no output buffer");
+  const int cus = frisk::device_cus();
+  const int64_t need = gemm_workspace(g, route);
+  const bool ws = need > 0 && d->workspace_bytes >= need;
+  const int ies = esize(d->a_type);
+  const char* a_major = g.trans_a ? "m" : "k";
+  const char* b_major = g.trans_b ? "k" : "n";
+  auto lds_read = [&](bool mn) {
+    return !mn ? "ds_read_b128" : ies == 2 ? "ds_read_b64_tr_b16" : "ds_read_b64_tr_b8";
+  };
+  int n = 0;
+  if (route == GemmRoute::Generic) {
+    n = snprintf(buf, (size_t)len,
+                 "{\"kernel\": \"gemm_generic\", \"tile_m\": 64, \"tile_n\": 64, \"atom\": \"fma\", "
+                 "\"a_major\": \"%s\", \"b_major\": \"%s\", \"slices\": 1, \"workspace_bytes\": 0}",
+                 a_major, b_major);
+  } else if (route == GemmRoute::Skinny && !(ws && g.m > kSkinnySplitMaxM)) {
+    const frisk::SkinnyPlan p = frisk::gemm_skinny_plan(g, cus, ws);
+    n = snprintf(buf, (size_t)len,
+                 "{\"kernel\": \"gemm_skinny\", \"tile_m\": %d, \"tile_n\": %d, "
+                 "\"atom\": \"v_mfma_f32_16x16x32_%s\", \"waves\": [1, 1], \"a_major\": \"k\", "
+                 "\"b_major\": \"k\", \"slices\": %d, \"workspace_bytes\": %lld}",
+                 16 * p.tm, 16 * p.tn, d->a_type == FRISK_BF16 ? "bf16" : "f16", p.slices,
+                 (long long)(p.slices > 1 ? p.workspace_bytes : 0));
+  } else {
+    const frisk::MfmaChoice c = frisk::gemm_mfma_choice(g, cus, ws);
+    const int tile = c.big ? 256 : 128;
+    n = snprintf(buf, (size_t)len,
+                 "{\"kernel\": \"%s\", \"tile_m\": %d, \"tile_n\": %d, \"atom\": \"%s\", "
+                 "\"waves\": [2, 2], \"wave_tile\": [%d, %d], \"stage_bytes\": %d, "
+                 "\"a_major\": \"%s\", \"b_major\": \"%s\", \"lds_read_a\": \"%s\", "
+                 "\"lds_read_b\": \"%s\", \"slices\": %d, \"workspace_bytes\": %lld}",
+                 c.big ? "gemm_w4" : "gemm_128", tile, tile, mfma_atom(g.in), tile / 2, tile / 2,
+                 c.big ? 128 : 64, a_major, b_major, lds_read(g.trans_a), lds_read(!g.trans_b),
+                 c.slices, (long long)(c.slices > 1 ? need : 0));
+  }
+  if (n < 0 || n >= len)
+    return fail(FRISK_EINVAL, "frisk_gemm_plan: buffer of %lld bytes is too small", (long long)len);
+  return FRISK_OK;
 }
 
 int frisk_gemm(const frisk_gemm_desc* d, void* stream) {
@@ -232,13 +312,14 @@ int frisk_gemm(const frisk_gemm_desc* d, void* stream) {
       ws_bytes = d->workspace_bytes;
     }
   }
+  clear_stale_error();
   hipError_t e;
   if (route == GemmRoute::Skinny && ws && g.m > kSkinnySplitMaxM) {
-    e = frisk::gemm_tn_mfma(g, (hipStream_t)stream, ws, ws_bytes);
+    e = frisk::gemm_mfma(g, (hipStream_t)stream, ws, ws_bytes);
   } else if (route == GemmRoute::Skinny) {
     e = frisk::gemm_skinny(g, (hipStream_t)stream, ws, ws_bytes);
-  } else if (route == GemmRoute::Tn) {
-    e = frisk::gemm_tn_mfma(g, (hipStream_t)stream, ws, ws_bytes);
+  } else if (route == GemmRoute::Mfma) {
+    e = frisk::gemm_mfma(g, (hipStream_t)stream, ws, ws_bytes);
   } else {
     e = frisk::gemm_generic_any(g, (hipStream_t)stream);
   }
@@ -277,6 +358,14 @@ int frisk_attn_fwd(const frisk_attn_desc* d, void* stream) {
     return fail(FRISK_EINVAL, "frisk_attn_fwd: sm_scale must be positive and finite");
   if (d->seq_q > INT32_MAX / 2 || d->seq_k > INT32_MAX / 2 || d->batch * d->heads > INT32_MAX / 2)
     return fail(FRISK_EUNSUP, "frisk_attn_fwd: sizes beyond the 32-bit index range");
+  // K and V are read through buffer loads with 32-bit offsets from the
+  // head's first row: the last key row must end within 2^31 - 1 bytes.
+  const int64_t kv_reach = (d->seq_k - 1) * std::max(d->k_stride_s, d->v_stride_s) * 2 +
+                           d->head_dim * 2;
+  if (kv_reach > INT32_MAX)
+    return fail(FRISK_EUNSUP, "frisk_attn_fwd: K/V rows span %lld bytes of one head, beyond the "
+                              "2^31 - 1 bytes the kernel addresses",
+                (long long)kv_reach);
 
   frisk::AttnArgs a;
   a.dtype = (frisk::Elt)d->dtype;
@@ -290,6 +379,7 @@ int frisk_attn_fwd(const frisk_attn_desc* d, void* stream) {
   a.v = d->v; a.v_sb = d->v_stride_b; a.v_sh = d->v_stride_h; a.v_ss = d->v_stride_s;
   a.o = d->o; a.o_sb = d->o_stride_b; a.o_sh = d->o_stride_h; a.o_ss = d->o_stride_s;
   a.lse = d->lse;
+  clear_stale_error();
   hipError_t e = frisk::attn_fwd(a, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "frisk_attn_fwd launch");
   return FRISK_OK;
@@ -386,6 +476,7 @@ int frisk_reduce(const frisk_reduce_desc* d, void* stream) {
   a.rows = d->rows; a.cols = d->cols;
   a.src = d->src; a.ld = d->ld_src;
   a.dst = d->dst; a.dst_stride = d->dst_stride;
+  clear_stale_error();
   hipError_t e = frisk::tile_reduce(a, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "frisk_reduce launch");
   return FRISK_OK;
@@ -426,6 +517,7 @@ int frisk_copy(const frisk_copy_desc* d, void* stream) {
     a.ld_src = a.ld_dst = a.cols;
     a.rows = 1;
   }
+  clear_stale_error();
   hipError_t e = frisk::tile_copy(a, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "frisk_copy launch");
   return FRISK_OK;
@@ -458,20 +550,38 @@ int frisk_fill(const frisk_fill_desc* d, void* stream) {
     a.ld = a.cols;
     a.rows = 1;
   }
+  clear_stale_error();
   hipError_t e = frisk::tile_fill(a, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "frisk_fill launch");
   return FRISK_OK;
 }
 
 int frisk_probe_mfma_layout(int atom, float* out, int64_t out_floats, void* stream) {
+  g_last_error.clear();
   const int need = frisk::mfma_probe_floats(atom);
   if (need == 0) return fail(FRISK_EINVAL, "mfma-probe: unknown atom %d (0, 1 or 2)", atom);
   if (!out) return fail(FRISK_EINVAL, "mfma-probe: null output");
   if (out_floats < need)
     return fail(FRISK_EINVAL, "mfma-probe: atom %d writes %d floats, buffer holds %lld", atom, need,
                 (long long)out_floats);
+  clear_stale_error();
   hipError_t e = frisk::mfma_layout_probe(atom, out, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "mfma-probe launch");
+  return FRISK_OK;
+}
+
+int frisk_probe_lds_transpose(int bits, uint16_t* out, int64_t out_elems, void* stream) {
+  g_last_error.clear();
+  if (bits != 8 && bits != 16)
+    return fail(FRISK_EINVAL, "lds-transpose-probe: bits must be 8 or 16 (got %d)", bits);
+  if (!out) return fail(FRISK_EINVAL, "lds-transpose-probe: null output");
+  const int64_t need = bits == 16 ? 256 : 512;
+  if (out_elems < need)
+    return fail(FRISK_EINVAL, "lds-transpose-probe: %d-bit read writes %lld values, buffer holds %lld",
+                bits, (long long)need, (long long)out_elems);
+  clear_stale_error();
+  hipError_t e = frisk::lds_transpose_probe(bits, out, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "lds-transpose-probe launch");
   return FRISK_OK;
 }
 

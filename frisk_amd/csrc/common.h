@@ -27,6 +27,15 @@ template <> struct EltInfo<Elt::BF16> { using T = __bf16; static constexpr int b
 template <> struct EltInfo<Elt::E4M3> { using T = uint8_t; static constexpr int bytes = 1; };
 template <> struct EltInfo<Elt::I8> { using T = int8_t; static constexpr int bytes = 1; };
 template <> struct EltInfo<Elt::I32> { using T = int32_t; static constexpr int bytes = 4; };
+// Element bytes of a runtime element kind.
+inline int elt_bytes(Elt e) {
+  switch (e) {
+    case Elt::F16: case Elt::BF16: return 2;
+    case Elt::E4M3: case Elt::I8: return 1;
+    case Elt::F64: return 8;
+    default: return 4;
+  }
+}
 
 // OCP float8 e4m3fn -> f32, from the format definition: 1 sign, 4 exponent
 // (bias 7), 3 mantissa bits, no infinities, S.1111.111 is NaN.

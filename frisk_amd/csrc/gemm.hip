@@ -1,31 +1,11 @@
-// MFMA GEMM kernels for gfx950 (MI355X): the 128x128-tile kernel, the
-// generic fallback and the launch policy.  The 256x256-tile kernel lives in
-// gemm4w.hip.
+// GEMM dispatch for gfx950 (MI355X): the generic fallback kernel, the
+// split-K planner and the choice between the LDS-staged MFMA kernels
+// (gemm_w4.h: 256x256 tiles; gemm_128.h: 128x128 tiles), both of which take
+// every storage order of A and B.
 //
 // Semantics follow frisk.gemm (include/Dialect/Frisk/IR/FriskOps.td:252-292):
-// C = op(A).op(B) when clear_accum, else C += op(A).op(B).  The reference
-// lowers one 64xN tile of that op to SM90 wgmma text
-// (benchmark/layout/execution/backend.py:383-431); here the whole problem is
-// tiled for CDNA4:
+// C = op(A).op(B) when clear_accum, else C += op(A).op(B).
 //
-//  * 128x128 output tile per 256-thread workgroup (4 waves, 2x2), each wave
-//    owning a 64x64 sub-tile as 2x2 v_mfma 32x32 accumulators; two
-//    workgroups share a CU.
-//  * K is consumed in stages of 64 bytes per row (32 bf16/f16, 64 fp8/i8),
-//    loaded by LDS-DMA (buffer_load_dwordx4 ... lds: no VGPRs stage the
-//    data) into kStages rotating LDS slots, one barrier per stage.
-//  * LDS rows are 4 chunks of 16 B, chunk c of row r stored at chunk
-//    c ^ swz(r); the XOR spreads the 32 rows of a fragment read over distinct
-//    bank groups.  swz is an F2-linear map of the row bits (a GF(2) layout in
-//    the sense of the reference's bit-linear shared layouts,
-//    SM90GemmConstraints.cpp:106-150).
-//  * The epilogue stages each 32-row f32 slice of a wave through LDS so the
-//    global stores are row-contiguous 16 B per lane.
-//
-// Operand contract of the fast kernel: A is [M, K] and B is [N, K] (both
-// K-contiguous, i.e. trans_a == 0, trans_b == 1), K*esize % 16 == 0, 16 B
-// aligned rows; the generic kernel covers every other layout and type.
-
 #include <algorithm>
 
 #include "common.h"
@@ -34,265 +14,6 @@
 #include "kernels.h"
 
 namespace frisk {
-
-// ---------------------------------------------------------------------------
-// Tiling.  Each stage holds 64 bytes of K per row (32 bf16/f16, 64 fp8/i8)
-// for the BT A rows and BT B rows (2 x 8 KiB at BT = 128).  kStages rotate
-// through LDS; a stage is filled by LDS-DMA (buffer_load_dwordx4 ... lds),
-// so no VGPRs stage the data and the loads of kStages-2 stages are in
-// flight while one stage is multiplied.
-//
-// LDS row = 4 chunks of 16 B.  Chunk c of row r is stored at physical chunk
-// c ^ swz(r), swz(r) = (r >> 2) & 3.  A 32x32 MFMA fragment read has lanes
-// 0-31 read one logical chunk of 32 consecutive rows (lanes 32-63 the next
-// chunk).  gfx950 serves ds_read_b128 at 256 B/clk (64 banks of 4 B, 16
-// lanes per cycle); under this map the 16 rows of a lane group cover the 16
-// distinct 16 B bank groups of a 256 B line ((r & 3) picks the quarter,
-// swz the chunk), and rocprofv3 counts SQ_LDS_BANK_CONFLICT = 0 for it,
-// where ((r >> 1) ^ (r >> 3)) & 3 measured 2-way conflicts and no swizzle
-// 4-way.  swz is linear over GF(2) in the row bits (a bit-linear shared
-// layout); the DMA side applies it by choosing which chunk a lane fetches.
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ int swz(int row) { return (row >> 2) & 3; }
-
-constexpr int kRow = 64;  // bytes of K per row per stage
-#ifndef FRISK_GEMM_STAGES
-#define FRISK_GEMM_STAGES 4
-#endif
-constexpr int kStages = FRISK_GEMM_STAGES;
-// LDS bytes of a BT x BT tile pipeline: kStages stages of (A, B) tiles.
-constexpr int lds_bytes(int bt) { return kStages * 2 * bt * kRow; }
-static_assert(2 * lds_bytes(128) <= 160 * 1024, "two 128x128 workgroups per CU");
-
-// One workgroup per BT x BT output tile; WM x WN waves tile it, each wave
-// owning a (BT/WM) x (BT/WN) sub-tile as TM x TN 32x32 accumulators.
-//
-// Split-K: blockIdx.y is a K slice of kb_slice bytes; the slice's A and B
-// columns start kb_slice * y bytes in, and its output is the tile of C
-// c_slice_bytes * y bytes further (the f32 partial of that slice).
-template <Elt IN, Elt OUT, int BT, int WM, int WN>
-__global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_tn(const char* __restrict__ A,
-                                                             const char* __restrict__ B,
-                                                             void* __restrict__ C, int M, int N,
-                                                             int Kb, int64_t lda_b, int64_t ldb_b,
-                                                             int64_t ldc, float scale,
-                                                             int accumulate, int kb_slice,
-                                                             int64_t c_slice_bytes) {
-  // The body is device code only; the host pass just needs the kernel stub.
-#if defined(__HIP_DEVICE_COMPILE__)
-  A += (int64_t)blockIdx.y * kb_slice;
-  B += (int64_t)blockIdx.y * kb_slice;
-  Kb = min(Kb - (int)blockIdx.y * kb_slice, kb_slice);
-  C = (char*)C + (int64_t)blockIdx.y * c_slice_bytes;
-  using Op = Mfma32<IN>;
-  using Acc = typename Op::Acc;
-  using AccS = typename std::conditional<IN == Elt::I8, int32_t, float>::type;
-  constexpr int kWaves = WM * WN;
-  constexpr int kBM = BT, kBN = BT;
-  constexpr int kTileBytes = BT * kRow;  // one operand, one stage
-  constexpr int kStageBytes = 2 * kTileBytes;
-  constexpr int kLdsBytes = lds_bytes(BT);
-  constexpr int TM = kBM / WM / 32, TN = kBN / WN / 32;
-  constexpr int kStepChunks = Op::kBytes / 16;  // 16 B chunks per row per MFMA
-  constexpr int kLaneChunks = kStepChunks / 2;  // chunks per lane per MFMA
-  constexpr int kSteps = kRow / Op::kBytes;     // MFMA k-steps per stage (2 or 1)
-  constexpr int kBlocks = kTileBytes / 1024 / kWaves;  // 1 KiB DMA blocks per wave per operand
-  constexpr int kLoads = 2 * kBlocks;                  // DMA loads per lane per stage
-  constexpr int kFragReads = (TM + TN) * kLaneChunks;  // ds_read_b128 per lane per k-step
-
-  extern __shared__ __attribute__((aligned(1024))) char smem[];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave / WN, wn = wave % WN;
-  const int l32 = lane & 31, half = lane >> 5;
-
-  const int tiles_m = (M + kBM - 1) / kBM, tiles_n = (N + kBN - 1) / kBN;
-  int tm, tn;
-  tile_of_block<4>(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
-  const int row0 = tm * kBM, col0 = tn * kBN;
-
-  // ---- LDS-DMA mapping ----------------------------------------------------
-  // DMA instruction i of wave w writes the 1 KiB block of rows
-  // (kBlocks w + i) * 16 .. +16 of a tile; lane L lands at row +L/4,
-  // physical chunk L%4, so it fetches logical chunk (L%4) ^ swz(row) of that
-  // row.  Loads are raw buffer loads based at the tile's first row: an
-  // offset past num_records returns zeros, which zero-fills the K tail
-  // without branches.
-  const char* a_base = A + (int64_t)row0 * lda_b;
-  const char* b_base = B + (int64_t)col0 * ldb_b;
-  const int64_t a_left = (int64_t)(M - 1 - row0) * lda_b + Kb;
-  const int64_t b_left = (int64_t)(N - 1 - col0) * ldb_b + Kb;
-  const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)a_base, (short)0, (int)min(a_left, (int64_t)0x7fffffff), 0x00020000);
-  const __amdgpu_buffer_rsrc_t rsb = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)b_base, (short)0, (int)min(b_left, (int64_t)0x7fffffff), 0x00020000);
-  uint32_t a_off[kBlocks], b_off[kBlocks];
-  int kmax[kBlocks];
-#pragma unroll
-  for (int i = 0; i < kBlocks; ++i) {
-    const int r = (kBlocks * wave + i) * 16 + (lane >> 2);
-    const int c = (lane & 3) ^ swz(r);
-    // Rows past the matrix edge are clamped: they only feed output rows or
-    // columns that are never stored.
-    a_off[i] = (uint32_t)(min(r, M - 1 - row0) * lda_b) + c * 16;
-    b_off[i] = (uint32_t)(min(r, N - 1 - col0) * ldb_b) + c * 16;
-    kmax[i] = Kb - c * 16;  // the chunk is live while kb < kmax
-  }
-  auto issue_stage = [&](int stage, int slot) {
-    const int kb = stage * kRow;
-    char* dst = smem + slot * kStageBytes + wave * kBlocks * 1024;
-#pragma unroll
-    for (int i = 0; i < kBlocks; ++i) {
-      const bool live = kb < kmax[i];
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (lds_ptr_t)(dst + i * 1024), 16,
-                                               live ? a_off[i] + kb : 0x80000000u, 0, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsb, (lds_ptr_t)(dst + kTileBytes + i * 1024), 16,
-                                               live ? b_off[i] + kb : 0x80000000u, 0, 0, 0);
-    }
-  };
-
-  // ---- fragment reads -----------------------------------------------------
-  int fa_off[TM], fb_off[TN], fa_sw[TM], fb_sw[TN];
-#pragma unroll
-  for (int t = 0; t < TM; ++t) {
-    const int r = wm * (32 * TM) + t * 32 + l32;
-    fa_off[t] = r * kRow;
-    fa_sw[t] = swz(r);
-  }
-#pragma unroll
-  for (int t = 0; t < TN; ++t) {
-    const int r = wn * (32 * TN) + t * 32 + l32;
-    fb_off[t] = kTileBytes + r * kRow;
-    fb_sw[t] = swz(r);
-  }
-  using Frag = Frags<TM, TN, kLaneChunks>;
-  auto load_frags = [&](int slot, int s, Frag& f) {
-    const char* base = smem + slot * kStageBytes;
-#pragma unroll
-    for (int j = 0; j < kLaneChunks; ++j) {
-      const int chunk = s * kStepChunks + half * kLaneChunks + j;
-#pragma unroll
-      for (int t = 0; t < TM; ++t)
-        f.a[t][j] = *(const i32x4*)(base + fa_off[t] + ((chunk ^ fa_sw[t]) << 4));
-#pragma unroll
-      for (int t = 0; t < TN; ++t)
-        f.b[t][j] = *(const i32x4*)(base + fb_off[t] + ((chunk ^ fb_sw[t]) << 4));
-    }
-  };
-
-  Acc acc[TM][TN];
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j) acc[i][j] = Acc{};
-  auto mfma_rows = [&](const Frag& f, int i0, int i1) {
-#pragma unroll
-    for (int i = i0; i < i1; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j) acc[i][j] = Op::run(f.a[i], f.b[j], acc[i][j]);
-  };
-
-  // ---- pipeline -----------------------------------------------------------
-  // Stage kt lives in slot kt % kStages.  Before the second half of the last
-  // k-step of stage kt a barrier (after waiting for this lane's loads of
-  // stage kt+1) makes stage kt+1 readable and proves every wave is done
-  // with slot (kt-1) % kStages, which then receives stage kt+kStages-1.
-  // Every iteration issues exactly kLoads loads (stages past the end reload
-  // the last stage into a slot nobody reads), so vmcnt bookkeeping is static.
-  const int nk = (Kb + kRow - 1) / kRow;
-#pragma unroll
-  for (int st = 0; st < kStages - 1; ++st) issue_stage(min(st, nk - 1), st);
-  FRISK_WAIT_VMCNT(kLoads * (kStages - 2));
-  __builtin_amdgcn_s_barrier();
-
-  Frag fr[2];
-  load_frags(0, 0, fr[0]);
-  // Drain every LGKM operation issued so far (the prologue's fragment reads
-  // and the scalar loads of the epilogue's kernel arguments).  With scalar
-  // loads still pending at the loop entry the LGKM counter is unordered, and
-  // the compiler then waits for lgkmcnt(0) at the top of every iteration,
-  // i.e. for the fragment read it has just issued.
-  __builtin_amdgcn_s_waitcnt(0xC07F);
-  int slot = 0;
-  for (int kt = 0; kt < nk; ++kt) {
-#pragma unroll
-    for (int s = 0; s < kSteps; ++s) {
-      const int cur = s & 1, nxt = cur ^ 1;
-      if (s + 1 < kSteps) {
-        load_frags(slot, s + 1, fr[nxt]);
-        mfma_rows(fr[cur], 0, TM);
-        // Fragment reads first, each under one MFMA.
-#pragma unroll
-        for (int i = 0; i < kFragReads; ++i) {
-          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-        }
-        __builtin_amdgcn_sched_barrier(0);
-      } else {
-        mfma_rows(fr[cur], 0, TM / 2);
-        __builtin_amdgcn_sched_barrier(0);
-        FRISK_WAIT_VMCNT(kLoads * (kStages - 3));
-        __builtin_amdgcn_s_barrier();
-        const int nslot = slot + 1 == kStages ? 0 : slot + 1;
-        const int fslot = slot == 0 ? kStages - 1 : slot - 1;
-        issue_stage(min(kt + kStages - 1, nk - 1), fslot);
-        load_frags(nslot, 0, fr[kSteps & 1 ? nxt : 0]);
-        mfma_rows(fr[cur], TM / 2, TM);
-        // DMA issue and next-stage fragment reads interleaved with the
-        // remaining MFMAs.
-#pragma unroll
-        for (int i = 0; i < kLoads; ++i) {
-          __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM (LDS-DMA)
-          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        slot = nslot;
-      }
-    }
-    if constexpr (kSteps == 1) fr[0] = fr[1];
-  }
-  // Drain the trailing DMA loads before the stage buffers are reused.
-  FRISK_WAIT_VMCNT(0);
-  __syncthreads();
-
-  // Epilogue: per wave, stage a 32 x (32 TN) slice (one accumulator row
-  // block) as 32-bit values, then each lane stores 8 consecutive columns.
-  // The MFMA 32x32 accumulator holds D[8*(r/4) + 4*(lane/32) + r%4][lane%32]
-  // in element r.
-  constexpr int kPitch = 32 * TN + 4;
-  static_assert(kWaves * 32 * kPitch * 4 <= kLdsBytes, "epilogue staging fits in the stage buffers");
-  AccS* stage = (AccS*)(smem + wave * (32 * kPitch * 4));
-  constexpr int kGroups = 32 * TN / 8;  // 8-column groups per staged row
-#pragma unroll
-  for (int i = 0; i < TM; ++i) {
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int rr = 8 * (r >> 2) + 4 * half + (r & 3);
-        stage[rr * kPitch + j * 32 + l32] = acc[i][j][r];
-      }
-    __syncthreads();
-#pragma unroll
-    for (int it = 0; it < 32 * kGroups / 64; ++it) {
-      const int q = it * 64 + lane;
-      const int rr = q / kGroups, g = q % kGroups;
-      const int gr = row0 + wm * (32 * TM) + i * 32 + rr;
-      const int gc = col0 + wn * (32 * TN) + g * 8;
-      if (gr < M && gc < N) {
-        AccS v[8];
-        *(i32x4*)&v[0] = *(const i32x4*)&stage[rr * kPitch + g * 8];
-        *(i32x4*)&v[4] = *(const i32x4*)&stage[rr * kPitch + g * 8 + 4];
-        store8<OUT>(C, (int64_t)gr * ldc + gc, v, accumulate != 0, scale);
-      }
-    }
-    __syncthreads();
-  }
-#endif  // __HIP_DEVICE_COMPILE__
-}
 
 // ---------------------------------------------------------------------------
 // Generic kernel: any layout, any supported type, any shape.  64x64 output
@@ -366,61 +87,6 @@ __global__ __launch_bounds__(256) void gemm_generic(const void* __restrict__ A,
 // ---------------------------------------------------------------------------
 // Launchers.
 // ---------------------------------------------------------------------------
-template <Elt IN, Elt OUT, int BT, int WM, int WN>
-static hipError_t launch_tn_cfg(const GemmArgs& g, hipStream_t stream) {
-  constexpr int kEsz = EltInfo<IN>::bytes;
-  constexpr int kLds = lds_bytes(BT);
-  auto kern = gemm_mfma_tn<IN, OUT, BT, WM, WN>;
-  // Thread-safe one-time opt-in to more than 64 KiB of dynamic LDS.
-  static const hipError_t attr =
-      hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
-  if (attr != hipSuccess) return attr;
-  const int tiles = (int)(((g.m + BT - 1) / BT) * ((g.n + BT - 1) / BT));
-  const int kb = (int)(g.k * kEsz);
-  hipLaunchKernelGGL(kern, dim3(tiles), dim3(64 * WM * WN), kLds, stream, (const char*)g.a,
-                     (const char*)g.b, g.c, (int)g.m, (int)g.n, kb, g.lda * kEsz, g.ldb * kEsz,
-                     g.ldc, g.scale, g.accumulate, kb, (int64_t)0);
-  return hipGetLastError();
-}
-
-// Split-K on 128x128 tiles: f32 partial tiles of each K slice into
-// `partial` ([slices][M][N]), then their sum in slice order into C.
-template <Elt IN, Elt OUT>
-static hipError_t launch_tn_split(const GemmArgs& g, const TnSplitPlan& p, float* partial,
-                                  hipStream_t stream) {
-  constexpr int kEsz = EltInfo<IN>::bytes;
-  constexpr int kLds = lds_bytes(128);
-  auto kern = gemm_mfma_tn<IN, Elt::F32, 128, 2, 2>;
-  static const hipError_t attr =
-      hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
-  if (attr != hipSuccess) return attr;
-  const int tiles = (int)(((g.m + 127) / 128) * ((g.n + 127) / 128));
-  hipLaunchKernelGGL(kern, dim3(tiles, p.slices), dim3(256), kLds, stream, (const char*)g.a,
-                     (const char*)g.b, (void*)partial, (int)g.m, (int)g.n, (int)(g.k * kEsz),
-                     g.lda * kEsz, g.ldb * kEsz, g.n, 1.0f, 0, (int)p.kb_slice,
-                     (int64_t)g.m * g.n * 4);
-  const hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  return gemm_splitk_sum(partial, p.slices, g, stream);
-}
-
-// 256x256 tiles (gemm4w.hip: 4 waves of 128x128, one workgroup per CU)
-// when there are at least half as many as CUs; otherwise 128x128 tiles
-// (4 waves of 64x64, two workgroups per CU), which keep more CUs busy
-// (measured on the projection sweep: M=1024, N=4096 runs 2x faster on
-// 128x128 tiles, N=14336 (224 big tiles) runs faster on 256x256).
-template <Elt IN, Elt OUT>
-static hipError_t launch_tn(const GemmArgs& g, hipStream_t stream, int cus, float* partial,
-                            const TnSplitPlan& p) {
-  if constexpr (IN == Elt::BF16 || IN == Elt::F16) {
-    if (partial && p.big) return gemm_tn_w4_split(g, p.slices, p.kb_slice, partial, stream);
-    if (partial) return launch_tn_split<IN, OUT>(g, p, partial, stream);
-  }
-  const int64_t tiles256 = ((g.m + 255) / 256) * ((g.n + 255) / 256);
-  if (tiles256 >= cus / 2) return gemm_tn_w4(g, stream);
-  return launch_tn_cfg<IN, OUT, 128, 2, 2>(g, stream);
-}
-
 template <Elt IN, Elt OUT>
 static hipError_t launch_generic(const GemmArgs& g, hipStream_t stream) {
   dim3 grid((unsigned)((g.n + 63) / 64), (unsigned)((g.m + 63) / 64));
@@ -445,9 +111,14 @@ double partial_cost(const GemmArgs& g, int64_t slices) {
 }
 }  // namespace
 
-TnSplitPlan gemm_tn_split_plan(const GemmArgs& g, int cus) {
-  TnSplitPlan p{1, g.k * 2, 0, false};
-  if ((g.in != Elt::BF16 && g.in != Elt::F16) || g.trans_a || !g.trans_b) return p;
+// Bytes of K per pipeline stage of the 128x128-tile kernel (gemm_128.h).
+constexpr int64_t kRow = 64;
+
+SplitPlan gemm_split_plan(const GemmArgs& g, int cus) {
+  SplitPlan p{1, g.k * 2, 0, false};
+  // bf16 / f16 only (the partials carry no fp8 scale); the slice sum reads
+  // rows of 4 floats.
+  if ((g.in != Elt::BF16 && g.in != Elt::F16) || g.n % 4 != 0) return p;
   // Grids of at least CUs / 2 256x256 tiles run unsplit on them.
   const int64_t tiles256 = ((g.m + 255) / 256) * ((g.n + 255) / 256);
   if (tiles256 >= cus / 2) return p;
@@ -469,7 +140,7 @@ TnSplitPlan gemm_tn_split_plan(const GemmArgs& g, int cus) {
       const int64_t chunks = (kb + kRow - 1) / kRow;  // slices start on stage boundaries
       p.kb_slice = ((chunks + slices - 1) / slices) * kRow;
       p.slices = (int)((kb + p.kb_slice - 1) / p.kb_slice);
-      if (p.slices < 2) p = TnSplitPlan{1, kb, 0, false};
+      if (p.slices < 2) p = SplitPlan{1, kb, 0, false};
     }
   }
   // 256x256 tiles split over K, for M past the small-M range, when the
@@ -500,29 +171,51 @@ TnSplitPlan gemm_tn_split_plan(const GemmArgs& g, int cus) {
       p.kb_slice = ((kb + 127) / 128 + best_s - 1) / best_s * 128;
       p.slices = (int)((kb + p.kb_slice - 1) / p.kb_slice);
       p.big = p.slices > 1;
-      if (!p.big) p = TnSplitPlan{1, kb, 0, false};
+      if (!p.big) p = SplitPlan{1, kb, 0, false};
     }
   }
   p.workspace_bytes = p.slices > 1 ? (int64_t)p.slices * g.m * g.n * 4 : 0;
   return p;
 }
 
-hipError_t gemm_tn_mfma(const GemmArgs& g, hipStream_t s, void* workspace,
-                        int64_t workspace_bytes) {
+MfmaChoice gemm_mfma_choice(const GemmArgs& g, int cus, bool workspace) {
+  const SplitPlan p = gemm_split_plan(g, cus);
+  if (workspace && p.slices > 1) return MfmaChoice{p.big, p.slices, p.kb_slice};
+  // 256x256 tiles (4 waves of 128x128, one workgroup per CU) when there are
+  // at least half as many as CUs; otherwise 128x128 tiles (4 waves of 64x64,
+  // two workgroups per CU), which keep more CUs busy (measured on the
+  // projection sweep: M=1024, N=4096 runs 2x faster on 128x128 tiles,
+  // N=14336 (224 big tiles) runs faster on 256x256).
+  const int64_t tiles256 = ((g.m + 255) / 256) * ((g.n + 255) / 256);
+  return MfmaChoice{tiles256 >= cus / 2, 1, g.k * elt_bytes(g.in)};
+}
+
+namespace {
+
+// One storage order: AM = A stored [K, M] (trans_a), BM = B stored [K, N]
+// (not trans_b).
+template <bool AM, bool BM>
+hipError_t run_layout(const GemmArgs& g, hipStream_t s, const MfmaChoice& c, float* partial) {
+  if (c.slices > 1) {
+    if (c.big) return gemm_w4_split_layout<AM, BM>(g, c.slices, c.kb_slice, partial, s);
+    return gemm_128_split_layout<AM, BM>(g, c.slices, c.kb_slice, partial, s);
+  }
+  if (c.big) return gemm_w4_layout<AM, BM>(g, s);
+  return gemm_128_layout<AM, BM>(g, s);
+}
+
+}  // namespace
+
+hipError_t gemm_mfma(const GemmArgs& g, hipStream_t s, void* workspace, int64_t workspace_bytes) {
   const int cus = device_cus();
-  TnSplitPlan p = gemm_tn_split_plan(g, cus);
-  float* partial = p.slices > 1 && workspace && workspace_bytes >= p.workspace_bytes
-                       ? (float*)workspace : nullptr;
-  switch (FRISK_PAIR(g.in, g.out)) {
-    case FRISK_PAIR(Elt::BF16, Elt::BF16): return launch_tn<Elt::BF16, Elt::BF16>(g, s, cus, partial, p);
-    case FRISK_PAIR(Elt::BF16, Elt::F32): return launch_tn<Elt::BF16, Elt::F32>(g, s, cus, partial, p);
-    case FRISK_PAIR(Elt::F16, Elt::F16): return launch_tn<Elt::F16, Elt::F16>(g, s, cus, partial, p);
-    case FRISK_PAIR(Elt::F16, Elt::F32): return launch_tn<Elt::F16, Elt::F32>(g, s, cus, partial, p);
-    case FRISK_PAIR(Elt::E4M3, Elt::BF16): return launch_tn<Elt::E4M3, Elt::BF16>(g, s, cus, partial, p);
-    case FRISK_PAIR(Elt::E4M3, Elt::F16): return launch_tn<Elt::E4M3, Elt::F16>(g, s, cus, partial, p);
-    case FRISK_PAIR(Elt::E4M3, Elt::F32): return launch_tn<Elt::E4M3, Elt::F32>(g, s, cus, partial, p);
-    case FRISK_PAIR(Elt::I8, Elt::I32): return launch_tn<Elt::I8, Elt::I32>(g, s, cus, partial, p);
-    default: return hipErrorInvalidValue;
+  const bool ws = workspace && workspace_bytes >= gemm_split_plan(g, cus).workspace_bytes;
+  const MfmaChoice c = gemm_mfma_choice(g, cus, ws);
+  float* partial = c.slices > 1 ? (float*)workspace : nullptr;
+  switch ((g.trans_a ? 2 : 0) | (g.trans_b ? 0 : 1)) {
+    case 0: return run_layout<false, false>(g, s, c, partial);  // A [M,K], B [N,K]
+    case 1: return run_layout<false, true>(g, s, c, partial);   // A [M,K], B [K,N]
+    case 2: return run_layout<true, false>(g, s, c, partial);   // A [K,M], B [N,K]
+    default: return run_layout<true, true>(g, s, c, partial);   // A [K,M], B [K,N]
   }
 }
 

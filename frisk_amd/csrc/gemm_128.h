@@ -1,0 +1,326 @@
+// 128x128-tile MFMA GEMM for gfx950 (MI355X): the kernel for grids too small
+// for the 256x256 tiles of gemm_w4.h, and the split-K slices of medium M.
+//
+// Semantics follow frisk.gemm (include/Dialect/Frisk/IR/FriskOps.td:252-292):
+// C = op(A).op(B) when clear_accum, else C += op(A).op(B).  The reference
+// lowers one 64xN tile of that op to SM90 wgmma text
+// (benchmark/layout/execution/backend.py:383-431); here the whole problem is
+// tiled for CDNA4:
+//
+//  * 128x128 output tile per 256-thread workgroup (4 waves, 2x2), each wave
+//    owning a 64x64 sub-tile as 2x2 v_mfma 32x32 accumulators; two
+//    workgroups share a CU.
+//  * K is consumed in stages of 64 bytes per row (32 bf16/f16, 64 fp8/i8),
+//    loaded by LDS-DMA (buffer_load_dwordx4 ... lds: no VGPRs stage the
+//    data) into kStages rotating LDS slots, one barrier per stage.
+//  * Operand tiles, their XOR swizzles and the fragment reads for either
+//    storage order of A and B (template flags AM / BM, MN-major when set)
+//    are those of gemm_tile.h.  For the K-major 64 B rows the swizzle is
+//    swz(r) = (r >> 2) & 3: a 32x32 fragment read has lanes 0-31 read one
+//    logical chunk of 32 consecutive rows; the 16 rows of a 16-lane cycle
+//    then cover the 16 distinct 16 B bank groups of a 256 B line, and
+//    rocprofv3 counts SQ_LDS_BANK_CONFLICT = 0 for it, where
+//    ((r >> 1) ^ (r >> 3)) & 3 measured 2-way conflicts and no swizzle 4-way.
+//  * The epilogue stages each 32-row f32 slice of a wave through LDS so the
+//    global stores are row-contiguous 16 B per lane.
+//
+// gemm_128_a*b*.hip instantiate one layout each.
+#pragma once
+
+#include <algorithm>
+
+#include "common.h"
+#include "gemm_common.h"
+#include "gemm_tile.h"
+#include "kernels.h"
+
+namespace frisk {
+
+namespace g128 {
+
+constexpr int kRow = 64;  // bytes of K per row per stage
+#ifndef FRISK_GEMM_STAGES
+#define FRISK_GEMM_STAGES 4
+#endif
+constexpr int kStages = FRISK_GEMM_STAGES;
+// LDS bytes of a BT x BT tile pipeline: kStages stages of (A, B) tiles.
+constexpr int lds_bytes(int bt) { return kStages * 2 * bt * kRow; }
+static_assert(2 * lds_bytes(128) <= 160 * 1024, "two 128x128 workgroups per CU");
+
+}  // namespace g128
+
+// One workgroup per BT x BT output tile; WM x WN waves tile it, each wave
+// owning a (BT/WM) x (BT/WN) sub-tile as TM x TN 32x32 accumulators.
+//
+// Split-K: blockIdx.y is a K slice of kb_slice bytes; the slice's A and B
+// start kb_slice bytes of K further per slice, and its output is the tile
+// of C c_slice_bytes * y bytes further (the f32 partial of that slice).
+template <Elt IN, Elt OUT, bool AM, bool BM, int BT, int WM, int WN>
+__global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_128(const char* __restrict__ A,
+                                                              const char* __restrict__ B,
+                                                              void* __restrict__ C, int M, int N,
+                                                              int Kb, int64_t lda_b, int64_t ldb_b,
+                                                              int64_t ldc, float scale,
+                                                              int accumulate, int kb_slice,
+                                                              int64_t c_slice_bytes) {
+  // The body is device code only; the host pass just needs the kernel stub.
+#if defined(__HIP_DEVICE_COMPILE__)
+  constexpr int kRow = g128::kRow, kStages = g128::kStages;
+  using TA = OpTile<IN, AM, BT, kRow>;
+  using TB = OpTile<IN, BM, BT, kRow>;
+  A += TA::slice_shift((int64_t)blockIdx.y * kb_slice, lda_b);
+  B += TB::slice_shift((int64_t)blockIdx.y * kb_slice, ldb_b);
+  Kb = min(Kb - (int)blockIdx.y * kb_slice, kb_slice);
+  C = (char*)C + (int64_t)blockIdx.y * c_slice_bytes;
+  using Op = Mfma32<IN>;
+  using Acc = typename Op::Acc;
+  using AccS = typename std::conditional<IN == Elt::I8, int32_t, float>::type;
+  constexpr int kWaves = WM * WN;
+  constexpr int kBM = BT, kBN = BT;
+  constexpr int kTileBytes = BT * kRow;  // one operand, one stage
+  constexpr int kStageBytes = 2 * kTileBytes;
+  constexpr int kLdsBytes = g128::lds_bytes(BT);
+  constexpr int TM = kBM / WM / 32, TN = kBN / WN / 32;
+  constexpr int kLaneChunks = TA::kLaneChunks;         // 16 B pieces per lane per MFMA
+  constexpr int kSteps = kRow / Op::kBytes;            // MFMA k-steps per stage (2 or 1)
+  constexpr int kBlocks = kTileBytes / 1024 / kWaves;  // 1 KiB DMA blocks per wave per operand
+  constexpr int kLoads = 2 * kBlocks;                  // DMA loads per lane per stage
+  constexpr int kFragReads =                           // LDS reads per lane per k-step
+      (TM * TA::kReadsPerChunk + TN * TB::kReadsPerChunk) * kLaneChunks;
+
+  extern __shared__ __attribute__((aligned(1024))) char smem[];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+  const int l32 = lane & 31, half = lane >> 5;
+
+  const int tiles_m = (M + kBM - 1) / kBM, tiles_n = (N + kBN - 1) / kBN;
+  int tm, tn;
+  tile_of_block<4>(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
+  const int row0 = tm * kBM, col0 = tn * kBN;
+
+  // ---- LDS-DMA mapping (gemm_tile.h) --------------------------------------
+  const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)TA::origin(A, row0, lda_b), (short)0,
+      (int)min(TA::records(M, row0, Kb, lda_b), (int64_t)0x7fffffff), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rsb = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)TB::origin(B, col0, ldb_b), (short)0,
+      (int)min(TB::records(N, col0, Kb, ldb_b), (int64_t)0x7fffffff), 0x00020000);
+  typename TA::template Dma<kBlocks> da;
+  typename TB::template Dma<kBlocks> db;
+#pragma unroll
+  for (int i = 0; i < kBlocks; ++i) {
+    TA::dma_setup(da, i, kBlocks * wave + i, lane, M, row0, Kb, lda_b);
+    TB::dma_setup(db, i, kBlocks * wave + i, lane, N, col0, Kb, ldb_b);
+  }
+  TA::dma_adv(da, lda_b);
+  TB::dma_adv(db, ldb_b);
+  auto issue_stage = [&](int stage, int slot) {
+    char* dst = smem + slot * kStageBytes + wave * kBlocks * 1024;
+#pragma unroll
+    for (int i = 0; i < kBlocks; ++i) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (lds_ptr_t)(dst + i * 1024), 16,
+                                               TA::offset(da, i, stage), 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsb, (lds_ptr_t)(dst + kTileBytes + i * 1024), 16,
+                                               TB::offset(db, i, stage), 0, 0, 0);
+    }
+  };
+
+  // ---- fragment reads -----------------------------------------------------
+  typename TA::Frag fa[TM];
+  typename TB::Frag fb[TN];
+#pragma unroll
+  for (int t = 0; t < TM; ++t) fa[t] = TA::frag(wm * (32 * TM) + t * 32, lane);
+#pragma unroll
+  for (int t = 0; t < TN; ++t) fb[t] = TB::frag(wn * (32 * TN) + t * 32, lane);
+  using Frag = Frags<TM, TN, kLaneChunks>;
+  auto load_frags = [&](int slot, int s, Frag& f) {
+    const char* base = smem + slot * kStageBytes;
+#pragma unroll
+    for (int t = 0; t < TM; ++t) TA::read(base, fa[t], s, f.a[t]);
+#pragma unroll
+    for (int t = 0; t < TN; ++t) TB::read(base + kTileBytes, fb[t], s, f.b[t]);
+  };
+
+  Acc acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = Acc{};
+  auto mfma_rows = [&](const Frag& f, int i0, int i1) {
+#pragma unroll
+    for (int i = i0; i < i1; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) acc[i][j] = Op::run(f.a[i], f.b[j], acc[i][j]);
+  };
+
+  // ---- pipeline -----------------------------------------------------------
+  // Stage kt lives in slot kt % kStages.  Before the second half of the last
+  // k-step of stage kt a barrier (after waiting for this lane's loads of
+  // stage kt+1) makes stage kt+1 readable and proves every wave is done
+  // with slot (kt-1) % kStages, which then receives stage kt+kStages-1.
+  // Every iteration issues exactly kLoads loads (stages past the end reload
+  // the last stage into a slot nobody reads), so vmcnt bookkeeping is static.
+  const int nk = (Kb + kRow - 1) / kRow;
+#pragma unroll
+  for (int st = 0; st < kStages - 1; ++st) issue_stage(min(st, nk - 1), st);
+  FRISK_WAIT_VMCNT(kLoads * (kStages - 2));
+  __builtin_amdgcn_s_barrier();
+
+  Frag fr[2];
+  load_frags(0, 0, fr[0]);
+  // Drain every LGKM operation issued so far (the prologue's fragment reads
+  // and the scalar loads of the epilogue's kernel arguments).  With scalar
+  // loads still pending at the loop entry the LGKM counter is unordered, and
+  // the compiler then waits for lgkmcnt(0) at the top of every iteration,
+  // i.e. for the fragment read it has just issued.
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  int slot = 0;
+  for (int kt = 0; kt < nk; ++kt) {
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) {
+      const int cur = s & 1, nxt = cur ^ 1;
+      if (s + 1 < kSteps) {
+        load_frags(slot, s + 1, fr[nxt]);
+        mfma_rows(fr[cur], 0, TM);
+        // Fragment reads first, each under one MFMA.
+#pragma unroll
+        for (int i = 0; i < kFragReads; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      } else {
+        mfma_rows(fr[cur], 0, TM / 2);
+        __builtin_amdgcn_sched_barrier(0);
+        FRISK_WAIT_VMCNT(kLoads * (kStages - 3));
+        __builtin_amdgcn_s_barrier();
+        const int nslot = slot + 1 == kStages ? 0 : slot + 1;
+        const int fslot = slot == 0 ? kStages - 1 : slot - 1;
+        issue_stage(min(kt + kStages - 1, nk - 1), fslot);
+        load_frags(nslot, 0, fr[kSteps & 1 ? nxt : 0]);
+        mfma_rows(fr[cur], TM / 2, TM);
+        // DMA issue and next-stage fragment reads interleaved with the
+        // remaining MFMAs.
+#pragma unroll
+        for (int i = 0; i < kLoads; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM (LDS-DMA)
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        slot = nslot;
+      }
+    }
+    if constexpr (kSteps == 1) fr[0] = fr[1];
+  }
+  // Drain the trailing DMA loads before the stage buffers are reused.
+  FRISK_WAIT_VMCNT(0);
+  __syncthreads();
+
+  // Epilogue: per wave, stage a 32 x (32 TN) slice (one accumulator row
+  // block) as 32-bit values, then each lane stores 8 consecutive columns
+  // (the ragged last group of a row one element at a time).  The MFMA 32x32
+  // accumulator holds D[8*(r/4) + 4*(lane/32) + r%4][lane%32] in element r.
+  constexpr int kPitch = 32 * TN + 4;
+  static_assert(kWaves * 32 * kPitch * 4 <= kLdsBytes, "epilogue staging fits in the stage buffers");
+  AccS* stage = (AccS*)(smem + wave * (32 * kPitch * 4));
+  constexpr int kGroups = 32 * TN / 8;  // 8-column groups per staged row
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int rr = 8 * (r >> 2) + 4 * half + (r & 3);
+        stage[rr * kPitch + j * 32 + l32] = acc[i][j][r];
+      }
+    __syncthreads();
+#pragma unroll
+    for (int it = 0; it < 32 * kGroups / 64; ++it) {
+      const int q = it * 64 + lane;
+      const int rr = q / kGroups, g = q % kGroups;
+      const int gr = row0 + wm * (32 * TM) + i * 32 + rr;
+      const int gc = col0 + wn * (32 * TN) + g * 8;
+      if (gr < M && gc < N) {
+        AccS v[8];
+        *(i32x4*)&v[0] = *(const i32x4*)&stage[rr * kPitch + g * 8];
+        *(i32x4*)&v[4] = *(const i32x4*)&stage[rr * kPitch + g * 8 + 4];
+        if (gc + 8 <= N) store8<OUT>(C, (int64_t)gr * ldc + gc, v, accumulate != 0, scale);
+        else store_n<OUT>(C, (int64_t)gr * ldc + gc, v, N - gc, accumulate != 0, scale);
+      }
+    }
+    __syncthreads();
+  }
+#endif  // __HIP_DEVICE_COMPILE__
+}
+
+template <Elt IN, Elt OUT, bool AM, bool BM>
+static hipError_t launch_128(const GemmArgs& g, hipStream_t stream) {
+  constexpr int kEsz = EltInfo<IN>::bytes;
+  constexpr int kLds = g128::lds_bytes(128);
+  auto kern = gemm_mfma_128<IN, OUT, AM, BM, 128, 2, 2>;
+  // Thread-safe one-time opt-in to more than 64 KiB of dynamic LDS.
+  static const hipError_t attr =
+      hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
+  if (attr != hipSuccess) return attr;
+  const int tiles = (int)(((g.m + 127) / 128) * ((g.n + 127) / 128));
+  const int kb = (int)(g.k * kEsz);
+  hipLaunchKernelGGL(kern, dim3(tiles), dim3(256), kLds, stream, (const char*)g.a,
+                     (const char*)g.b, g.c, (int)g.m, (int)g.n, kb, g.lda * kEsz, g.ldb * kEsz,
+                     g.ldc, g.scale, g.accumulate, kb, (int64_t)0);
+  return hipGetLastError();
+}
+
+// Split-K on 128x128 tiles: f32 partial tiles of each K slice into
+// `partial` ([slices][M][N]), then their sum in slice order into C
+// (bf16 / f16 inputs, scale 1).
+template <Elt IN, bool AM, bool BM>
+static hipError_t launch_128_split(const GemmArgs& g, int slices, int64_t kb_slice, float* partial,
+                                   hipStream_t stream) {
+  constexpr int kEsz = EltInfo<IN>::bytes;
+  constexpr int kLds = g128::lds_bytes(128);
+  auto kern = gemm_mfma_128<IN, Elt::F32, AM, BM, 128, 2, 2>;
+  static const hipError_t attr =
+      hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
+  if (attr != hipSuccess) return attr;
+  const int tiles = (int)(((g.m + 127) / 128) * ((g.n + 127) / 128));
+  hipLaunchKernelGGL(kern, dim3(tiles, slices), dim3(256), kLds, stream, (const char*)g.a,
+                     (const char*)g.b, (void*)partial, (int)g.m, (int)g.n, (int)(g.k * kEsz),
+                     g.lda * kEsz, g.ldb * kEsz, g.n, 1.0f, 0, (int)kb_slice,
+                     (int64_t)g.m * g.n * 4);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  return gemm_splitk_sum(partial, slices, g, stream);
+}
+
+template <bool AM, bool BM>
+hipError_t gemm_128_split_layout(const GemmArgs& g, int slices, int64_t kb_slice, float* partial,
+                                 hipStream_t s) {
+  if (g.in == Elt::BF16) return launch_128_split<Elt::BF16, AM, BM>(g, slices, kb_slice, partial, s);
+  if (g.in == Elt::F16) return launch_128_split<Elt::F16, AM, BM>(g, slices, kb_slice, partial, s);
+  return hipErrorInvalidValue;
+}
+
+#define FRISK_PAIR(i, o) (((int)(i) << 8) | (int)(o))
+
+template <bool AM, bool BM>
+hipError_t gemm_128_layout(const GemmArgs& g, hipStream_t s) {
+  switch (FRISK_PAIR(g.in, g.out)) {
+    case FRISK_PAIR(Elt::BF16, Elt::BF16): return launch_128<Elt::BF16, Elt::BF16, AM, BM>(g, s);
+    case FRISK_PAIR(Elt::BF16, Elt::F32): return launch_128<Elt::BF16, Elt::F32, AM, BM>(g, s);
+    case FRISK_PAIR(Elt::F16, Elt::F16): return launch_128<Elt::F16, Elt::F16, AM, BM>(g, s);
+    case FRISK_PAIR(Elt::F16, Elt::F32): return launch_128<Elt::F16, Elt::F32, AM, BM>(g, s);
+    case FRISK_PAIR(Elt::E4M3, Elt::BF16): return launch_128<Elt::E4M3, Elt::BF16, AM, BM>(g, s);
+    case FRISK_PAIR(Elt::E4M3, Elt::F16): return launch_128<Elt::E4M3, Elt::F16, AM, BM>(g, s);
+    case FRISK_PAIR(Elt::E4M3, Elt::F32): return launch_128<Elt::E4M3, Elt::F32, AM, BM>(g, s);
+    case FRISK_PAIR(Elt::I8, Elt::I32): return launch_128<Elt::I8, Elt::I32, AM, BM>(g, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+#undef FRISK_PAIR
+
+}  // namespace frisk

@@ -209,7 +209,8 @@ SkinnyPlan gemm_skinny_plan(const GemmArgs& g, int cus, bool split) {
   p.workspace_bytes = 0;
   // Below 64 MiB of W the unsplit kernel ends before a second launch pays
   // (16 x 4096 x 4096: 10.5 us unsplit, 12.7 us split).
-  if (!split || g.n * kb < ((int64_t)64 << 20)) {
+  // (The slice sum reads rows of 4 floats, so N % 4 != 0 runs unsplit too.)
+  if (!split || g.n * kb < ((int64_t)64 << 20) || g.n % 4 != 0) {
     // 32 < M <= 64 with under 64 MiB of W: 32x32 tiles instead of 64x16,
     // the same workgroup count with a fifth fewer operand loads per k-step
     // (64 x 4096 x 4096, operands from HBM: 24.1 -> 19.6 us).

@@ -1,0 +1,218 @@
+// Operand tiles of the LDS-staged MFMA GEMM kernels (gemm_w4.h: 256x256
+// tiles, gemm_128.h: 128x128 tiles): how one operand of one pipeline stage
+// is copied from global memory into LDS and how the MFMA fragments are read
+// back, for either storage order of the operand.
+//
+// frisk.gemm takes A as [M, K] or, with transA, stored [K, M]; B as [K, N]
+// or, with transB, stored [N, K] (ffi/ir.cpp:335-337; the builder's default
+// is transA = transB = false, and the reference's own GEMM tile program
+// tmp/ir.mlir:2-16 keeps B as [K, N]).  Per operand that is one of:
+//
+//  * K-major (A with trans_a == 0, B with trans_b == 1): the stage tile is
+//    BT rows (M or N indices) of KR bytes of K.  A lane's MFMA operand is 16
+//    contiguous bytes of one row: one ds_read_b128.
+//  * MN-major (A with trans_a == 1, B with trans_b == 0): the stage tile is
+//    KR / esize k-rows of BT * esize bytes, each a contiguous piece of one
+//    stored row.  A lane's MFMA operand is a run of consecutive k of one
+//    column of that tile, delivered by the gfx950 transposing LDS reads.
+//    Inside each group of 16 lanes,
+//      ds_read_b64_tr_b16: lane j receives element j%4 of the 8 B that lanes
+//                          4e + j/4 (e = 0..3) address,
+//      ds_read_b64_tr_b8:  lane j receives byte j%8 of the 8 B that lanes
+//                          2e + j/8 (e = 0..7) address
+//    (pinned on the device by frisk_probe_lds_transpose).  So when lane
+//    4e + q addresses k-row k0 + e at columns c0 + 4q .. +3 (16-bit), lane j
+//    receives column c0 + j at k0 .. k0+3; two reads (k0 and k0 + 4) give
+//    the 8 consecutive k of a 16-bit operand.  For 8-bit types lane 2e + b
+//    addresses k-row k0 + e at columns c0 + 8b .. +7 and lane j receives 8
+//    consecutive k of column c0 + j; 2 (i8) or 4 (fp8) reads give 16 or 32.
+//    The k order equals the K-major ds_read_b128's, so A and B fragments
+//    agree whatever the storage order of either.
+//
+// LDS swizzles (16 B chunk c of tile row r is stored at chunk c ^ swz(r)).
+// A read is conflict-free when the lanes served together hit distinct banks
+// (64 banks of 4 B: a 256 B window).
+//  * K-major: a ds_read_b128 has 16 lanes per cycle reading one logical
+//    chunk of 16 consecutive rows; swz sends them to 16 distinct chunks of
+//    the window (rocprofv3 SQ_LDS_BANK_CONFLICT = 0 for both maps).
+//  * MN-major 16-bit (rows of 512 or 256 B): 32 lanes read 4 k-rows (e) x
+//    64 B; swz(r) = (r & 3) << 2 moves row e to the 64 B quarter
+//    (c / 4) ^ e, four distinct quarters.
+//  * MN-major 8-bit, 256 B rows: 32 lanes read 8 k-rows x 32 B;
+//    swz(r) = (r & 7) << 1 gives each row its own 32 B pair of chunks.
+//  * MN-major 8-bit, 128 B rows: two rows share a window (r & 1 picks the
+//    half); swz(r) = ((r >> 1) & 3) << 1 separates the four pairs of rows.
+// Every swizzle is an XOR of row bits into chunk bits, i.e. a GF(2)-linear
+// shared layout, and only reads row bits below 3, which k-row bases
+// (multiples of 8) never change.
+#pragma once
+
+#include "common.h"
+#include "gemm_common.h"
+
+namespace frisk {
+
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+template <Elt IN, bool MN, int BT, int KR>
+struct OpTile {
+  using Op = Mfma32<IN>;
+  static constexpr int kEsz = EltInfo<IN>::bytes;
+  static constexpr int kRB = MN ? BT * kEsz : KR;  // bytes per LDS row
+  static constexpr int kRows = MN ? KR / kEsz : BT;
+  static constexpr int kKS = KR / kEsz;            // k per stage
+  static constexpr int kChunks = kRB / 16;         // 16 B chunks per LDS row
+  static constexpr int kRowsPerBlock = 1024 / kRB; // rows per 1 KiB DMA block
+  static constexpr int kBytes = BT * KR;           // the tile, one stage
+  static constexpr int kStepChunks = Op::kBytes / 16;
+  static constexpr int kLaneChunks = kStepChunks / 2;
+  static constexpr int kReadsPerChunk = MN ? 2 : 1;  // LDS reads per 16 B of operand
+  static_assert(kRows * kRB == kBytes && kRowsPerBlock >= 1, "tile geometry");
+  static_assert(!MN || kRB >= 128, "MN-major rows of at least 128 B");
+
+  __device__ static __forceinline__ int swz(int r) {
+    if constexpr (!MN) {
+      if constexpr (KR == 128) return (r & 7) ^ ((r >> 3) & 1);
+      else return (r >> 2) & 3;  // KR == 64
+    } else if constexpr (kEsz == 2) {
+      return (r & 3) << 2;
+    } else if constexpr (kRB >= 256) {
+      return (r & 7) << 1;
+    } else {
+      return ((r >> 1) & 3) << 1;
+    }
+  }
+
+  // ---- LDS-DMA ------------------------------------------------------------
+  // One buffer_load ... lds instruction fills a 1 KiB block of the tile:
+  // lane L lands in block row L / kChunks at physical chunk L % kChunks, so
+  // it fetches logical chunk (L % kChunks) ^ swz(row).  Loads are raw buffer
+  // loads based at the tile's origin; the offset 0x80000000 lies past every
+  // range and reads zeros.
+  //  K-major: tile origin = row0 of the operand; rows past the edge are
+  //    clamped (they only feed outputs that are never stored); a chunk is
+  //    live while its K bytes exist.
+  //  MN-major: tile origin = column row0 of every k-row; chunks starting
+  //    past the edge and k-rows past K read zeros.
+  // Stage `phys` (in units of KR bytes of K) loads at off + phys * adv while
+  // phys * step < lim.
+  template <int NB>
+  struct Dma {
+    uint32_t off[NB];
+    int lim[NB];
+    uint32_t adv;
+  };
+  static constexpr int kStep = MN ? kKS : KR;
+
+  // Global origin of the tile and the number of bytes addressable from it.
+  __device__ static __forceinline__ const char* origin(const char* X, int row0, int64_t ld_b) {
+    return MN ? X + (int64_t)row0 * kEsz : X + (int64_t)row0 * ld_b;
+  }
+  __device__ static __forceinline__ int64_t records(int extent, int row0, int Kb, int64_t ld_b) {
+    if constexpr (MN) return (int64_t)(Kb / kEsz - 1) * ld_b + (int64_t)(extent - row0) * kEsz;
+    else return (int64_t)(extent - 1 - row0) * ld_b + Kb;
+  }
+
+  // Block `blk` (tile-relative, 1 KiB each) of lane `lane`.
+  template <int NB>
+  __device__ static __forceinline__ void dma_setup(Dma<NB>& d, int i, int blk, int lane, int extent,
+                                                   int row0, int Kb, int64_t ld_b) {
+    const int r = blk * kRowsPerBlock + lane / kChunks;
+    const int c = (lane % kChunks) ^ swz(r);
+    if constexpr (MN) {
+      d.off[i] = (uint32_t)(r * ld_b) + c * 16;
+      const bool col_ok = (row0 + c * (16 / kEsz)) < extent;
+      d.lim[i] = col_ok ? Kb / kEsz - r : 0;
+    } else {
+      d.off[i] = (uint32_t)(min(r, extent - 1 - row0) * ld_b) + c * 16;
+      d.lim[i] = Kb - c * 16;
+    }
+  }
+  template <int NB>
+  __device__ static __forceinline__ void dma_adv(Dma<NB>& d, int64_t ld_b) {
+    d.adv = MN ? (uint32_t)(kKS * ld_b) : (uint32_t)KR;
+  }
+  template <int NB>
+  __device__ static __forceinline__ uint32_t offset(const Dma<NB>& d, int i, int phys) {
+    return phys * kStep < d.lim[i] ? d.off[i] + (uint32_t)phys * d.adv : 0x80000000u;
+  }
+  // Bytes to advance the operand pointer by for a K slice starting kb bytes in.
+  __device__ static __forceinline__ int64_t slice_shift(int64_t kb, int64_t ld_b) {
+    return MN ? (kb / kEsz) * ld_b : kb;
+  }
+
+  // ---- fragment reads ------------------------------------------------------
+  // Fragment of the 32 tile rows r0 .. r0+31 (r0 a multiple of 32) for lane
+  // `lane`: a byte offset from the operand's stage base (plus, K-major, the
+  // row's swizzle XOR the lane half's first chunk: the chunk index
+  // s * kStepChunks + half * kLaneChunks + j has disjoint bit fields, so
+  // XOR-ing the half in once equals adding it).
+  struct Frag {
+    int off, sw;
+  };
+  __device__ static __forceinline__ Frag frag(int r0, int lane) {
+    const int l32 = lane & 31, half = lane >> 5;
+    if constexpr (!MN) {
+      return Frag{(r0 + l32) * KR, swz(r0 + l32) ^ (half * kLaneChunks)};
+    } else if constexpr (kEsz == 2) {
+      // Lane 16G + 4e + q: k-row 8 half + e, columns r0 + 16 (G & 1) + 4q.
+      const int dg = (lane >> 4) & 1, e = (lane >> 2) & 3, q = lane & 3;
+      const int chunk = (r0 >> 3) + 2 * dg + (q >> 1);
+      return Frag{(8 * half + e) * kRB + ((chunk ^ swz(e)) << 4) + 8 * (q & 1), 0};
+    } else {
+      // Lane 16G + 2e + b: k-row kLaneK half + e, columns r0 + 16 (G & 1) + 8b.
+      constexpr int kLaneK = Op::kBytes / 2;
+      const int dg = (lane >> 4) & 1, e = (lane >> 1) & 7, b = lane & 1;
+      const int chunk = (r0 >> 4) + dg;
+      return Frag{(kLaneK * half + e) * kRB + ((chunk ^ swz(e)) << 4) + 8 * b, 0};
+    }
+  }
+  // The lane's operand of MFMA k-step s (Op::kBytes of K per row).
+  __device__ static __forceinline__ void read(const char* base, const Frag& f, int s,
+                                              i32x4 (&out)[kLaneChunks]) {
+    if constexpr (!MN) {
+#pragma unroll
+      for (int j = 0; j < kLaneChunks; ++j) {
+        const int chunk = s * kStepChunks + j;
+        out[j] = *(const i32x4*)(base + f.off + ((chunk ^ f.sw) << 4));
+      }
+    } else if constexpr (kEsz == 2) {
+      static_assert(kLaneChunks == 1, "16-bit operand: 8 k per lane");
+      const char* p = base + f.off + s * 16 * kRB;
+      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p);
+      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p + 4 * kRB));
+      const i32x2 a = __builtin_bit_cast(i32x2, lo), b = __builtin_bit_cast(i32x2, hi);
+      out[0] = i32x4{a[0], a[1], b[0], b[1]};
+    } else {
+      const char* p = base + f.off + s * Op::kBytes * kRB;
+#pragma unroll
+      for (int j = 0; j < kLaneChunks; ++j) {
+        const i32x2 a = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2*)(p + 16 * j * kRB));
+        const i32x2 b = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2*)(p + (16 * j + 8) * kRB));
+        out[j] = i32x4{a[0], a[1], b[0], b[1]};
+      }
+    }
+  }
+};
+
+// Stores the first n (< 8) of 8 consecutive outputs at C[idx ..] one
+// element at a time: the ragged last column group of a row.
+template <Elt OUT, typename AccS>
+__device__ inline void store_n(void* c, int64_t idx, const AccS* v, int n, bool accumulate,
+                               float scale) {
+  for (int e = 0; e < n; ++e) {
+    if constexpr (OUT == Elt::I32) {
+      int32_t* p = (int32_t*)c + idx + e;
+      *p = accumulate ? *p + (int32_t)v[e] : (int32_t)v[e];
+    } else {
+      float f = (float)v[e] * scale;
+      if (accumulate) f += load_as_f32<OUT>(c, idx + e);
+      store_from_f32<OUT>(c, idx + e, f);
+    }
+  }
+}
+
+}  // namespace frisk

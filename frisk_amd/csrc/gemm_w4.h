@@ -1,11 +1,16 @@
 // Large-tile MFMA GEMM for gfx950: one 256x256 output tile per workgroup of
 // four waves, one wave per SIMD, each wave owning a 128x128 sub-tile as 4x4
 // accumulators of the 32x32 MFMA (256 accumulator registers per lane, held
-// in AGPRs; this file is compiled without the VGPR-form MFMA option).
+// in AGPRs; the files that instantiate it are compiled without the
+// VGPR-form MFMA option).
 //
-// Semantics are those of gemm.hip's fast kernel (frisk.gemm with
-// trans_a == 0, trans_b == 1: C[m, n] = scale * sum_k A[m, k] B[n, k]
-// (+ C when accumulating); include/Dialect/Frisk/IR/FriskOps.td:252-292).
+// Semantics: frisk.gemm (include/Dialect/Frisk/IR/FriskOps.td:252-292),
+// C[m, n] = scale * sum_k op(A)[m, k] op(B)[k, n] (+ C when accumulating).
+// AM / BM select the storage order of A and B (MN-major: A stored [K, M],
+// i.e. trans_a; B stored [K, N], i.e. not trans_b); gemm_tile.h stages
+// either order into LDS and reads fragments in one common k order, so the
+// pipeline below is the same for all four layouts.  gemm_w4_a*b*.hip
+// instantiate one layout each.
 //
 // Why four waves of 128x128 rather than eight of 128x64: per k-step a wave
 // reads (TM + TN) fragments for TM * TN MFMAs, so the 128x128 sub-tile
@@ -18,8 +23,11 @@
 // SIMD nothing else can fill a stall, so every fragment read and DMA issue
 // is placed between MFMAs explicitly (sched_group_barrier).
 
+#pragma once
+
 #include "common.h"
 #include "gemm_common.h"
+#include "gemm_tile.h"
 #include "kernels.h"
 
 namespace frisk {
@@ -41,27 +49,20 @@ namespace g4 {
 constexpr int kBT = 256;
 constexpr int kThreads = 256;
 
-// LDS row swizzles (physical 16 B chunk = logical chunk ^ swz(row)).  A
-// fragment read has 16 lanes per LDS cycle reading one logical chunk of 16
-// consecutive rows; the swizzle sends those rows to 16 distinct 16 B bank
-// groups.  rocprofv3 measured SQ_LDS_BANK_CONFLICT = 0 for both maps on
-// ds_read_b128.
-template <int KR> __device__ __forceinline__ int swz(int r);
-template <> __device__ __forceinline__ int swz<64>(int r) { return (r >> 2) & 3; }
-template <> __device__ __forceinline__ int swz<128>(int r) { return (r & 7) ^ ((r >> 3) & 1); }
-
 constexpr int lds_bytes(int kr, int stages) { return stages * 2 * kBT * kr; }
 
 }  // namespace g4
 
-template <Elt IN, Elt OUT, int KR, int S>
+template <Elt IN, Elt OUT, bool AM, bool BM, int KR, int S>
 __global__ __launch_bounds__(g4::kThreads) void gemm_w4_kernel(
     const char* __restrict__ A, const char* __restrict__ B, void* __restrict__ C, int M, int N,
     int Kb, int64_t lda_b, int64_t ldb_b, int64_t ldc, float scale, int accumulate, int kb_slice,
     int64_t c_slice_bytes) {
 #if defined(__HIP_DEVICE_COMPILE__)
-  A += (int64_t)blockIdx.y * kb_slice;
-  B += (int64_t)blockIdx.y * kb_slice;
+  using TA = OpTile<IN, AM, g4::kBT, KR>;
+  using TB = OpTile<IN, BM, g4::kBT, KR>;
+  A += TA::slice_shift((int64_t)blockIdx.y * kb_slice, lda_b);
+  B += TB::slice_shift((int64_t)blockIdx.y * kb_slice, ldb_b);
   Kb = min(Kb - (int)blockIdx.y * kb_slice, kb_slice);
   C = (char*)C + (int64_t)blockIdx.y * c_slice_bytes;
   using Op = Mfma32<IN>;
@@ -69,16 +70,16 @@ __global__ __launch_bounds__(g4::kThreads) void gemm_w4_kernel(
   using AccS = typename std::conditional<IN == Elt::I8, int32_t, float>::type;
   constexpr int BT = g4::kBT;
   constexpr int TM = 4, TN = 4;                 // 32x32 atoms per wave
-  constexpr int kChunks = KR / 16;              // 16 B chunks per LDS row
-  constexpr int kRowsPerBlock = 1024 / KR;      // rows per 1 KiB DMA block
   constexpr int kTileBytes = BT * KR;           // one operand, one stage
   constexpr int kStageBytes = 2 * kTileBytes;
-  constexpr int kStepChunks = Op::kBytes / 16;  // chunks per row per MFMA
-  constexpr int kLaneChunks = kStepChunks / 2;  // chunks per lane per MFMA
+  constexpr int kLaneChunks = TA::kLaneChunks;  // 16 B pieces per lane per MFMA
   constexpr int kSteps = KR / Op::kBytes;       // MFMA k-steps per stage
-  constexpr int kBlocks = kTileBytes / 1024 / 4;       // DMA blocks per wave per operand
-  constexpr int kLoads = 2 * kBlocks;                  // DMA loads per lane per stage
-  constexpr int kFragReads = (TM + TN) * kLaneChunks;  // ds_read_b128 per lane per k-step
+  constexpr int kBlocks = kTileBytes / 1024 / 4;  // DMA blocks per wave per operand
+  constexpr int kLoads = 2 * kBlocks;             // DMA loads per lane per stage
+  // LDS read instructions per lane per k-step (two per 16 B of an MN-major
+  // operand, one of a K-major one).
+  constexpr int kFragReads =
+      (TM * TA::kReadsPerChunk + TN * TB::kReadsPerChunk) * kLaneChunks;
   static_assert(S >= 2 && kSteps >= 1, "pipeline shape");
 
   extern __shared__ __attribute__((aligned(1024))) char smem[];
@@ -95,32 +96,25 @@ __global__ __launch_bounds__(g4::kThreads) void gemm_w4_kernel(
   const int row0 = tm * BT, col0 = tn * BT;
 
   // ---- LDS-DMA mapping ----------------------------------------------------
-  // DMA instruction i of wave w fills 1 KiB block (kBlocks w + i) of a tile:
-  // rows kRowsPerBlock * block + lane / kChunks, physical chunk
-  // lane % kChunks, i.e. logical chunk (lane % kChunks) ^ swz(row).  Raw
-  // buffer loads based at the tile's first row: an offset past num_records
-  // reads zeros, which covers the K tail and the stages past the last one
+  // DMA instruction i of wave w fills 1 KiB block (kBlocks w + i) of each
+  // operand tile (gemm_tile.h): an offset past num_records reads zeros,
+  // which covers the K tail, the edges and the stages past the last one
   // without branches (and without memory traffic).
-  const char* a_base = A + (int64_t)row0 * lda_b;
-  const char* b_base = B + (int64_t)col0 * ldb_b;
-  const int64_t a_left = (int64_t)(M - 1 - row0) * lda_b + Kb;
-  const int64_t b_left = (int64_t)(N - 1 - col0) * ldb_b + Kb;
   const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)a_base, (short)0, (int)min(a_left, (int64_t)0x7fffffff), 0x00020000);
+      (void*)TA::origin(A, row0, lda_b), (short)0,
+      (int)min(TA::records(M, row0, Kb, lda_b), (int64_t)0x7fffffff), 0x00020000);
   const __amdgpu_buffer_rsrc_t rsb = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)b_base, (short)0, (int)min(b_left, (int64_t)0x7fffffff), 0x00020000);
-  uint32_t a_off[kBlocks], b_off[kBlocks];
-  int kmax[kBlocks];
+      (void*)TB::origin(B, col0, ldb_b), (short)0,
+      (int)min(TB::records(N, col0, Kb, ldb_b), (int64_t)0x7fffffff), 0x00020000);
+  typename TA::template Dma<kBlocks> da;
+  typename TB::template Dma<kBlocks> db;
 #pragma unroll
   for (int i = 0; i < kBlocks; ++i) {
-    const int r = (kBlocks * wave + i) * kRowsPerBlock + lane / kChunks;
-    const int c = (lane % kChunks) ^ g4::swz<KR>(r);
-    // Rows past the matrix edge are clamped: they only feed output rows or
-    // columns that are never stored.
-    a_off[i] = (uint32_t)(min(r, M - 1 - row0) * lda_b) + c * 16;
-    b_off[i] = (uint32_t)(min(r, N - 1 - col0) * ldb_b) + c * 16;
-    kmax[i] = Kb - c * 16;  // the chunk is live while kb < kmax
+    TA::dma_setup(da, i, kBlocks * wave + i, lane, M, row0, Kb, lda_b);
+    TB::dma_setup(db, i, kBlocks * wave + i, lane, N, col0, Kb, ldb_b);
   }
+  TA::dma_adv(da, lda_b);
+  TB::dma_adv(db, ldb_b);
   // The DMA of a stage goes out in kParts parts, one in each of the first
   // kParts k-steps of an iteration; part p covers blocks
   // [p kBlocks / kParts, (p+1) kBlocks / kParts).  With three or more slots
@@ -144,13 +138,11 @@ __global__ __launch_bounds__(g4::kThreads) void gemm_w4_kernel(
     int phys = stage + krot;
     if (phys >= nk_all) phys -= nk_all;
     if (stage >= nk_all) phys = stage;
-    const int kb = phys * KR;
     char* dst = smem + slot * kStageBytes + wave * kBlocks * 1024;
 #pragma unroll
     for (int i = p * kBlocks / kParts; i < (p + 1) * kBlocks / kParts; ++i) {
-      const bool live = kb < kmax[i];
-      uint32_t oa = live ? a_off[i] + kb : 0x80000000u;
-      uint32_t ob = live ? b_off[i] + kb : 0x80000000u;
+      uint32_t oa = TA::offset(da, i, phys);
+      uint32_t ob = TB::offset(db, i, phys);
       // Keep the selects as selects: otherwise the backend may turn them
       // into branches around two copies of each load.
       asm("" : "+v"(oa));
@@ -162,32 +154,19 @@ __global__ __launch_bounds__(g4::kThreads) void gemm_w4_kernel(
   };
 
   // ---- fragment reads -----------------------------------------------------
-  int fa_off[TM], fb_off[TN], fa_sw[TM], fb_sw[TN];
+  typename TA::Frag fa[TM];
+  typename TB::Frag fb[TN];
 #pragma unroll
-  for (int t = 0; t < TM; ++t) {
-    const int r = wm * (32 * TM) + t * 32 + l32;
-    fa_off[t] = r * KR;
-    fa_sw[t] = g4::swz<KR>(r);
-  }
+  for (int t = 0; t < TM; ++t) fa[t] = TA::frag(wm * (32 * TM) + t * 32, lane);
 #pragma unroll
-  for (int t = 0; t < TN; ++t) {
-    const int r = wn * (32 * TN) + t * 32 + l32;
-    fb_off[t] = kTileBytes + r * KR;
-    fb_sw[t] = g4::swz<KR>(r);
-  }
+  for (int t = 0; t < TN; ++t) fb[t] = TB::frag(wn * (32 * TN) + t * 32, lane);
   using Frag = Frags<TM, TN, kLaneChunks>;
   auto load_frags = [&](int slot, int s, Frag& f) {
     const char* base = smem + slot * kStageBytes;
 #pragma unroll
-    for (int j = 0; j < kLaneChunks; ++j) {
-      const int chunk = s * kStepChunks + half * kLaneChunks + j;
+    for (int t = 0; t < TM; ++t) TA::read(base, fa[t], s, f.a[t]);
 #pragma unroll
-      for (int t = 0; t < TM; ++t)
-        f.a[t][j] = *(const i32x4*)(base + fa_off[t] + ((chunk ^ fa_sw[t]) << 4));
-#pragma unroll
-      for (int t = 0; t < TN; ++t)
-        f.b[t][j] = *(const i32x4*)(base + fb_off[t] + ((chunk ^ fb_sw[t]) << 4));
-    }
+    for (int t = 0; t < TN; ++t) TB::read(base + kTileBytes, fb[t], s, f.b[t]);
   };
 
   Acc acc[TM][TN];
@@ -326,7 +305,8 @@ __global__ __launch_bounds__(g4::kThreads) void gemm_w4_kernel(
         AccS v[8];
         *(i32x4*)&v[0] = *(const i32x4*)&stage[rr * kPitch + g * 8];
         *(i32x4*)&v[4] = *(const i32x4*)&stage[rr * kPitch + g * 8 + 4];
-        store8<OUT>(C, (int64_t)gr * ldc + gc, v, accumulate != 0, scale);
+        if (gc + 8 <= N) store8<OUT>(C, (int64_t)gr * ldc + gc, v, accumulate != 0, scale);
+        else store_n<OUT>(C, (int64_t)gr * ldc + gc, v, N - gc, accumulate != 0, scale);
       }
     }
     __syncthreads();
@@ -334,13 +314,13 @@ __global__ __launch_bounds__(g4::kThreads) void gemm_w4_kernel(
 #endif  // __HIP_DEVICE_COMPILE__
 }
 
-template <Elt IN, Elt OUT>
+template <Elt IN, Elt OUT, bool AM, bool BM>
 static hipError_t launch_w4(const GemmArgs& g, hipStream_t stream) {
   constexpr int KR = FRISK_G4_KR, S = FRISK_G4_STAGES;
   constexpr int kEsz = EltInfo<IN>::bytes;
   constexpr int kLds = g4::lds_bytes(KR, S);
   static_assert(kLds <= 160 * 1024, "LDS budget of one CU");
-  auto kern = gemm_w4_kernel<IN, OUT, KR, S>;
+  auto kern = gemm_w4_kernel<IN, OUT, AM, BM, KR, S>;
   // Thread-safe one-time opt-in to more than 64 KiB of dynamic LDS.
   static const hipError_t attr =
       hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
@@ -353,13 +333,15 @@ static hipError_t launch_w4(const GemmArgs& g, hipStream_t stream) {
   return hipGetLastError();
 }
 
-template <Elt IN>
+// Split-K: f32 partials of each K slice into `partial` ([slices][M][N]),
+// then their sum in slice order into C (bf16 / f16 inputs, scale 1).
+template <Elt IN, bool AM, bool BM>
 static hipError_t launch_w4_split(const GemmArgs& g, int slices, int64_t kb_slice, float* partial,
                                   hipStream_t stream) {
   constexpr int KR = FRISK_G4_KR, S = FRISK_G4_STAGES;
   constexpr int kEsz = EltInfo<IN>::bytes;
   constexpr int kLds = g4::lds_bytes(KR, S);
-  auto kern = gemm_w4_kernel<IN, Elt::F32, KR, S>;
+  auto kern = gemm_w4_kernel<IN, Elt::F32, AM, BM, KR, S>;
   static const hipError_t attr =
       hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
   if (attr != hipSuccess) return attr;
@@ -373,27 +355,31 @@ static hipError_t launch_w4_split(const GemmArgs& g, int slices, int64_t kb_slic
   return gemm_splitk_sum(partial, slices, g, stream);
 }
 
-hipError_t gemm_tn_w4_split(const GemmArgs& g, int slices, int64_t kb_slice, float* partial,
-                            hipStream_t s) {
-  if (g.in == Elt::BF16) return launch_w4_split<Elt::BF16>(g, slices, kb_slice, partial, s);
-  if (g.in == Elt::F16) return launch_w4_split<Elt::F16>(g, slices, kb_slice, partial, s);
+template <bool AM, bool BM>
+hipError_t gemm_w4_split_layout(const GemmArgs& g, int slices, int64_t kb_slice, float* partial,
+                                hipStream_t s) {
+  if (g.in == Elt::BF16) return launch_w4_split<Elt::BF16, AM, BM>(g, slices, kb_slice, partial, s);
+  if (g.in == Elt::F16) return launch_w4_split<Elt::F16, AM, BM>(g, slices, kb_slice, partial, s);
   return hipErrorInvalidValue;
 }
 
 #define FRISK_PAIR(i, o) (((int)(i) << 8) | (int)(o))
 
-hipError_t gemm_tn_w4(const GemmArgs& g, hipStream_t s) {
+template <bool AM, bool BM>
+hipError_t gemm_w4_layout(const GemmArgs& g, hipStream_t s) {
   switch (FRISK_PAIR(g.in, g.out)) {
-    case FRISK_PAIR(Elt::BF16, Elt::BF16): return launch_w4<Elt::BF16, Elt::BF16>(g, s);
-    case FRISK_PAIR(Elt::BF16, Elt::F32): return launch_w4<Elt::BF16, Elt::F32>(g, s);
-    case FRISK_PAIR(Elt::F16, Elt::F16): return launch_w4<Elt::F16, Elt::F16>(g, s);
-    case FRISK_PAIR(Elt::F16, Elt::F32): return launch_w4<Elt::F16, Elt::F32>(g, s);
-    case FRISK_PAIR(Elt::E4M3, Elt::BF16): return launch_w4<Elt::E4M3, Elt::BF16>(g, s);
-    case FRISK_PAIR(Elt::E4M3, Elt::F16): return launch_w4<Elt::E4M3, Elt::F16>(g, s);
-    case FRISK_PAIR(Elt::E4M3, Elt::F32): return launch_w4<Elt::E4M3, Elt::F32>(g, s);
-    case FRISK_PAIR(Elt::I8, Elt::I32): return launch_w4<Elt::I8, Elt::I32>(g, s);
+    case FRISK_PAIR(Elt::BF16, Elt::BF16): return launch_w4<Elt::BF16, Elt::BF16, AM, BM>(g, s);
+    case FRISK_PAIR(Elt::BF16, Elt::F32): return launch_w4<Elt::BF16, Elt::F32, AM, BM>(g, s);
+    case FRISK_PAIR(Elt::F16, Elt::F16): return launch_w4<Elt::F16, Elt::F16, AM, BM>(g, s);
+    case FRISK_PAIR(Elt::F16, Elt::F32): return launch_w4<Elt::F16, Elt::F32, AM, BM>(g, s);
+    case FRISK_PAIR(Elt::E4M3, Elt::BF16): return launch_w4<Elt::E4M3, Elt::BF16, AM, BM>(g, s);
+    case FRISK_PAIR(Elt::E4M3, Elt::F16): return launch_w4<Elt::E4M3, Elt::F16, AM, BM>(g, s);
+    case FRISK_PAIR(Elt::E4M3, Elt::F32): return launch_w4<Elt::E4M3, Elt::F32, AM, BM>(g, s);
+    case FRISK_PAIR(Elt::I8, Elt::I32): return launch_w4<Elt::I8, Elt::I32, AM, BM>(g, s);
     default: return hipErrorInvalidValue;
   }
 }
+
+#undef FRISK_PAIR
 
 }  // namespace frisk

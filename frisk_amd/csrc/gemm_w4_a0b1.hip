@@ -1,0 +1,9 @@
+// The 256x256-tile MFMA GEMM (gemm_w4.h) for trans_a = 0, trans_b = 1:
+// A stored [M, K], B stored [N, K].
+#include "gemm_w4.h"
+
+namespace frisk {
+template hipError_t gemm_w4_layout<false, false>(const GemmArgs&, hipStream_t);
+template hipError_t gemm_w4_split_layout<false, false>(const GemmArgs&, int, int64_t, float*,
+                                                  hipStream_t);
+}  // namespace frisk

@@ -24,31 +24,46 @@ struct GemmArgs {
   int accumulate;
 };
 
-// 256x256-tile MFMA kernel; requires trans_a == 0, trans_b == 1 and 16 B
-// aligned, K-contiguous rows (checked by the caller).
-// Split-K plan of the 128x128-tile kernel (bf16/f16 TN only): `slices`
-// slices of kb_slice bytes of K whose f32 partials take workspace_bytes;
-// slices == 1 runs unsplit.
-struct TnSplitPlan {
+// Split-K plan of the LDS-staged MFMA kernels (bf16/f16): `slices` slices
+// of kb_slice bytes of K whose f32 partials take workspace_bytes; slices == 1
+// runs unsplit.
+struct SplitPlan {
   int slices;
   int64_t kb_slice;
   int64_t workspace_bytes;
-  bool big;  // slices run on 256x256 tiles (gemm4w.hip) instead of 128x128
+  bool big;  // slices run on 256x256 tiles (gemm_w4.h) instead of 128x128
 };
-// Split-K on the 256x256-tile kernel: f32 partials of each K slice into
-// `partial` ([slices][M][N]), then their sum in slice order into C.
-hipError_t gemm_tn_w4_split(const GemmArgs& g, int slices, int64_t kb_slice, float* partial,
-                            hipStream_t s);
-TnSplitPlan gemm_tn_split_plan(const GemmArgs& g, int cus);
-// With a workspace of at least the plan's bytes (16-byte aligned) the
-// planned split runs; otherwise the unsplit kernels.
-hipError_t gemm_tn_mfma(const GemmArgs& g, hipStream_t s, void* workspace, int64_t workspace_bytes);
+SplitPlan gemm_split_plan(const GemmArgs& g, int cus);
+// The launch gemm_mfma makes: 256x256 tiles (big) or 128x128, and the K
+// slices (1: unsplit) of kb_slice bytes; `workspace` = a large enough
+// workspace is at hand.
+struct MfmaChoice {
+  bool big;
+  int slices;
+  int64_t kb_slice;
+};
+MfmaChoice gemm_mfma_choice(const GemmArgs& g, int cus, bool workspace);
+// LDS-staged MFMA GEMM, any storage order of A and B; the caller checked 16 B
+// aligned operands with 16 B row pitches, K * esize % 16 == 0 for every
+// K-major operand and a 16 B row pitch of C.  With a workspace of at least
+// the plan's bytes (16-byte aligned) the planned split runs; otherwise the
+// unsplit kernels.
+hipError_t gemm_mfma(const GemmArgs& g, hipStream_t s, void* workspace, int64_t workspace_bytes);
 // C (+)= the sum over slices of partial[slice][M][N] (f32, added in slice
 // order), converted to C's type; N is a multiple of 4.
 hipError_t gemm_splitk_sum(const float* partial, int slices, const GemmArgs& g, hipStream_t s);
-// 256x256-tile kernel with four 128x128 waves (gemm4w.hip); same operand
-// contract as gemm_tn_mfma.
-hipError_t gemm_tn_w4(const GemmArgs& g, hipStream_t s);
+// The kernels of one storage order (AM: A stored [K, M]; BM: B stored
+// [K, N]), instantiated in gemm_w4_a*b*.hip (256x256 tiles) and
+// gemm_128_a*b*.hip (128x128 tiles).  The split variants write f32 partials of
+// `slices` K slices of kb_slice bytes to `partial` and then sum them into C.
+template <bool AM, bool BM> hipError_t gemm_w4_layout(const GemmArgs& g, hipStream_t s);
+template <bool AM, bool BM>
+hipError_t gemm_w4_split_layout(const GemmArgs& g, int slices, int64_t kb_slice, float* partial,
+                                hipStream_t s);
+template <bool AM, bool BM> hipError_t gemm_128_layout(const GemmArgs& g, hipStream_t s);
+template <bool AM, bool BM>
+hipError_t gemm_128_split_layout(const GemmArgs& g, int slices, int64_t kb_slice, float* partial,
+                                 hipStream_t s);
 // Any layout / shape; LDS-tiled FMA kernel.
 hipError_t gemm_generic_any(const GemmArgs& g, hipStream_t s);
 // Small-M kernel (M <= kSkinnyMaxM, bf16/f16, trans_a == 0, trans_b == 1,
@@ -161,5 +176,8 @@ hipError_t tile_fill(const FillArgs& a, hipStream_t s);
 // floats.
 int mfma_probe_floats(int atom);
 hipError_t mfma_layout_probe(int atom, float* out, hipStream_t stream);
+// Transposing LDS read probe (probe.hip): bits 16 = ds_read_b64_tr_b16
+// (256 outputs), 8 = ds_read_b64_tr_b8 (512 outputs).
+hipError_t lds_transpose_probe(int bits, uint16_t* out, hipStream_t stream);
 
 }  // namespace frisk

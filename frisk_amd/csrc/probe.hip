@@ -74,7 +74,55 @@ __global__ __launch_bounds__(64) void probe_i8_32(float* out) {
 #endif
 }
 
+// Transposing LDS reads: LDS holds the identity pattern (16-bit element e
+// holds e; for the 8-bit read byte address a holds a, written as two passes
+// of its low and high byte), every lane addresses the 8 bytes at lane * 8,
+// and the lane's returned elements are recorded: the LDS element id (16-bit)
+// or byte address (8-bit) each one came from.
+__global__ __launch_bounds__(64) void probe_tr16(uint16_t* out) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __shared__ uint16_t lds[256];
+  const int lane = threadIdx.x;
+  for (int i = lane; i < 256; i += 64) lds[i] = (uint16_t)i;
+  __syncthreads();
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_s16x4*)((__attribute__((address_space(3))) char*)lds + lane * 8));
+#pragma unroll
+  for (int e = 0; e < 4; ++e) out[lane * 4 + e] = (uint16_t)v[e];
+#endif
+}
+
+__global__ __launch_bounds__(64) void probe_tr8(uint16_t* out) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __shared__ uint8_t lds[512];
+  typedef int i32x2 __attribute__((ext_vector_type(2)));
+  typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
+  const int lane = threadIdx.x;
+  uint16_t got[8] = {};
+  for (int pass = 0; pass < 2; ++pass) {
+    for (int i = lane; i < 512; i += 64) lds[i] = (uint8_t)(pass ? i >> 8 : i & 255);
+    __syncthreads();
+    const i32x2 v = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+        (lds_i32x2*)((__attribute__((address_space(3))) char*)lds + lane * 8));
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < 8; ++e) got[e] |= (uint16_t)(((v[e >> 2] >> (8 * (e & 3))) & 255) << (8 * pass));
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) out[lane * 8 + e] = got[e];
+#endif
+}
+
 }  // namespace
+
+hipError_t lds_transpose_probe(int bits, uint16_t* out, hipStream_t stream) {
+  if (bits == 16) hipLaunchKernelGGL(probe_tr16, dim3(1), dim3(64), 0, stream, out);
+  else if (bits == 8) hipLaunchKernelGGL(probe_tr8, dim3(1), dim3(64), 0, stream, out);
+  else return hipErrorInvalidValue;
+  return hipGetLastError();
+}
 
 int mfma_probe_floats(int atom) {
   switch (atom) {

@@ -20,11 +20,12 @@ OK, EINVAL, EUNSUP, EHIP = 0, -1, -2, -3
 DTYPE_NAMES = {F32: "f32", F16: "f16", BF16: "bf16", E4M3: "e4m3", I8: "i8", I32: "i32", F64: "f64"}
 
 # Exported symbols declared by include/frisk_hip.h.
-EXPORTS = ("frisk_gemm", "frisk_gemm_workspace_size", "frisk_attn_fwd", "frisk_reduce",
-           "frisk_reduce_workspace_size",
+EXPORTS = ("frisk_gemm", "frisk_gemm_workspace_size", "frisk_gemm_plan", "frisk_attn_fwd",
+           "frisk_reduce", "frisk_reduce_workspace_size",
            "frisk_copy", "frisk_fill",
-           "frisk_last_error", "frisk_abi_version", "frisk_probe_mfma_layout")
-ABI_VERSION = 4
+           "frisk_last_error", "frisk_abi_version", "frisk_probe_mfma_layout",
+           "frisk_probe_lds_transpose")
+ABI_VERSION = 5
 
 REDUCE_SUM, REDUCE_MAX, REDUCE_MIN = 0, 1, 2
 REDUCE_KINDS = {"sum": REDUCE_SUM, "add": REDUCE_SUM, "max": REDUCE_MAX, "min": REDUCE_MIN}
@@ -108,6 +109,8 @@ def load() -> ctypes.CDLL:
     lib.frisk_gemm.restype = ctypes.c_int
     lib.frisk_gemm_workspace_size.argtypes = [ctypes.POINTER(GemmDesc)]
     lib.frisk_gemm_workspace_size.restype = ctypes.c_int64
+    lib.frisk_gemm_plan.argtypes = [ctypes.POINTER(GemmDesc), ctypes.c_char_p, ctypes.c_int64]
+    lib.frisk_gemm_plan.restype = ctypes.c_int
     lib.frisk_attn_fwd.argtypes = [ctypes.POINTER(AttnDesc), ctypes.c_void_p]
     lib.frisk_attn_fwd.restype = ctypes.c_int
     lib.frisk_reduce.argtypes = [ctypes.POINTER(ReduceDesc), ctypes.c_void_p]
@@ -125,6 +128,9 @@ def load() -> ctypes.CDLL:
     lib.frisk_probe_mfma_layout.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_int64,
                                             ctypes.c_void_p]
     lib.frisk_probe_mfma_layout.restype = ctypes.c_int
+    lib.frisk_probe_lds_transpose.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_int64,
+                                              ctypes.c_void_p]
+    lib.frisk_probe_lds_transpose.restype = ctypes.c_int
     if lib.frisk_abi_version() != ABI_VERSION:
         raise RuntimeError("libfrisk_hip.so ABI version mismatch; rebuild it")
     _lib = lib
@@ -197,6 +203,25 @@ def gemm_workspace_bytes(a, b, c, *, trans_a=False, trans_b=False) -> int:
     return need
 
 
+def plan_of(desc: GemmDesc) -> dict:
+    """frisk_gemm_plan for a descriptor: the launch frisk_gemm would make."""
+    import json
+    buf = ctypes.create_string_buffer(512)
+    _check(load().frisk_gemm_plan(ctypes.byref(desc), buf, len(buf)), "frisk_gemm_plan")
+    return json.loads(buf.value.decode())
+
+
+def gemm_plan(a, b, c, *, trans_a=False, trans_b=False, workspace=True) -> dict:
+    """The launch gemm(a, b, c, ..., workspace=workspace) makes (frisk_gemm_plan):
+    kernel, tiles, MFMA atom, operand storage order and LDS reads, split-K."""
+    d = gemm_desc(a, b, c, trans_a=trans_a, trans_b=trans_b)
+    if workspace is not False:
+        need = int(load().frisk_gemm_workspace_size(ctypes.byref(d)))
+        _check(need if need < 0 else OK, "frisk_gemm_workspace_size")
+        d.workspace_bytes = need if workspace is True else workspace.numel() * workspace.element_size()
+    return plan_of(d)
+
+
 def gemm(a, b, c, *, trans_a=False, trans_b=False, clear_accum=True,
          scale_a=1.0, scale_b=1.0, workspace=True, stream=None):
     """C = op(A).op(B) (or C += ... with clear_accum=False) on the GPU.
@@ -234,6 +259,16 @@ def probe_mfma_layout(atom: int, out, stream=None):
     _check(load().frisk_probe_mfma_layout(int(atom), ctypes.c_void_p(out.data_ptr()), out.numel(),
                                           ctypes.c_void_p(_stream_handle(stream))),
            "frisk_probe_mfma_layout")
+    return out
+
+
+def probe_lds_transpose(bits: int, out, stream=None):
+    """Run the transposing LDS read probe into the int16/uint16 device tensor `out`."""
+    if out.element_size() != 2 or not out.is_contiguous() or not out.is_cuda:
+        raise ValueError("out must be a contiguous 16-bit device tensor")
+    _check(load().frisk_probe_lds_transpose(int(bits), ctypes.c_void_p(out.data_ptr()), out.numel(),
+                                            ctypes.c_void_p(_stream_handle(stream))),
+           "frisk_probe_lds_transpose")
     return out
 
 

@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define FRISK_ABI_VERSION 4
+#define FRISK_ABI_VERSION 5
 
 /* Element types (the dtype strings of ffi/ir.cpp:399-411 plus bf16/i8/i32). */
 typedef enum frisk_dtype {
@@ -109,11 +109,34 @@ typedef struct frisk_gemm_desc {
 
 int frisk_gemm(const frisk_gemm_desc* desc, void* stream);
 
+/* Every storage order of A and B runs on the matrix cores (bf16/f16/fp8/i8)
+ * when the operands have 16-byte aligned bases and row pitches, K * esize is
+ * a multiple of 16 for an operand stored K-contiguous (A without trans_a, B
+ * with trans_b), C's row pitch is a multiple of 16 bytes, and every buffer a
+ * tile addresses spans less than 2^31 bytes; anything else (and f32) runs a
+ * correct but slower generic kernel. */
+
 /* Workspace bytes that make frisk_gemm(desc) split K (0: none is used), or
  * a negative FRISK_E* code for an invalid descriptor.  Pointers in desc are
  * not read.  No counterpart in the reference (its GEMM ops take no
  * scratch); callers that have none keep calling frisk_gemm unchanged. */
 int64_t frisk_gemm_workspace_size(const frisk_gemm_desc* desc);
+
+/* The launch frisk_gemm(desc) makes, as one line of JSON written to buf
+ * (len bytes including the terminating NUL): "kernel" (gemm_w4 = 256x256
+ * tiles, gemm_128 = 128x128 tiles, gemm_skinny = small M, gemm_generic),
+ * "tile_m"/"tile_n", the MFMA "atom", "waves" and "wave_tile" (the wave
+ * grid and each wave's sub-tile), "stage_bytes" (K bytes per LDS stage),
+ * "a_major"/"b_major" ("k" = K-contiguous storage, "m"/"n" otherwise), the
+ * LDS fragment read of each operand ("lds_read_a"/"lds_read_b":
+ * ds_read_b128, or ds_read_b64_tr_b16 / _tr_b8 for an M/N-major operand),
+ * "slices" (split-K) and "workspace_bytes".  desc->workspace_bytes is taken
+ * as the workspace a call would pass; pointers are not read.  No
+ * counterpart in the reference, whose execution packet records the chosen
+ * instruction contract instead (ExportExecution.cpp:46-295): this reports
+ * the contract of the kernel the C-ABI selects, for layout checks and
+ * tests. */
+int frisk_gemm_plan(const frisk_gemm_desc* desc, char* buf, int64_t len);
 
 /*
  * Flash-attention forward over [batch, heads, seq, head_dim] tensors:
@@ -254,6 +277,15 @@ int frisk_abi_version(void);
  * element it holds.  `out` is a device buffer of at least K * 64 * R floats
  * (16384, 8192 and 32768). */
 int frisk_probe_mfma_layout(int atom, float* out, int64_t out_floats, void* stream);
+
+/* Transposing LDS read probe: LDS holds the identity pattern, every lane of
+ * one wave addresses the 8 bytes at lane * 8 through ds_read_b64_tr_b16
+ * (bits 16: out[lane * 4 + e] = the 16-bit element id returned as element
+ * e, 256 values) or ds_read_b64_tr_b8 (bits 8: out[lane * 8 + e] = the byte
+ * address returned as byte e, 512 values).  Pins the lane map the GEMM
+ * kernels assume for M/N-major operands.  No counterpart in the reference
+ * (SM90 has no such instruction). */
+int frisk_probe_lds_transpose(int bits, uint16_t* out, int64_t out_elems, void* stream);
 
 #ifdef __cplusplus
 }

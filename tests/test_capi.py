@@ -50,6 +50,9 @@ def gemm_call(**over):
     (dict(scale_a=2.0), rt.EINVAL, "frisk_gemm: scale"),
     (dict(a_type=rt.I8, b_type=rt.I8, c_type=rt.I32, k=200000, lda=200000, ldb=200000),
      rt.EUNSUP, "frisk_gemm: int8"),
+    # |a b| <= 128 * 128 = 2^14: K = 131072 could reach 2^31 (all -128).
+    (dict(a_type=rt.I8, b_type=rt.I8, c_type=rt.I32, k=131072, lda=131072, ldb=131072),
+     rt.EUNSUP, "frisk_gemm: int8"),
 ])
 def test_gemm_rejects_invalid_requests(over, code, prefix):
     rc, msg = gemm_call(**over)
@@ -280,7 +283,9 @@ def test_gemm_workspace_size_query():
     # slice, layouts and types without a split kernel.
     assert gemm_size(m=4096) == 0
     assert gemm_size(k=256, lda=256, ldb=256) == 0
-    assert gemm_size(trans_b=0) == 0
+    # Every storage order splits alike (the kernels take all four).
+    assert gemm_size(trans_b=0) == 4 * 128 * 4096 * 4
+    assert gemm_size(trans_a=1, lda=128) == 4 * 128 * 4096 * 4
     assert gemm_size(a_type=rt.E4M3, b_type=rt.E4M3) == 0
     assert gemm_size(m=0) == rt.EINVAL
     assert rt.load().frisk_gemm_workspace_size(None) == rt.EINVAL
@@ -295,3 +300,70 @@ def test_gemm_rejects_a_short_or_misaligned_workspace():
     assert rc == rt.EINVAL and "16-byte aligned" in msg, msg
     rc, msg = gemm_call(workspace=16, workspace_bytes=-1)
     assert rc == rt.EINVAL and "negative workspace_bytes" in msg, msg
+
+
+def plan(**over):
+    d = rt.GemmDesc(m=4096, n=4096, k=4096, trans_a=0, trans_b=1, a_type=rt.BF16, b_type=rt.BF16,
+                    c_type=rt.BF16, clear_accum=1, a=16, lda=4096, b=16, ldb=4096, c=16,
+                    ldc=4096, scale_a=1.0, scale_b=1.0)
+    for key, val in over.items():
+        setattr(d, key, val)
+    return rt.plan_of(d)
+
+
+def test_gemm_plan_every_layout_runs_on_the_matrix_cores():
+    # 4096^3 in each storage order: the 256x256-tile kernel; M/N-major
+    # operands are read from LDS with the transposing reads.
+    for ta in (0, 1):
+        for tb in (0, 1):
+            p = plan(trans_a=ta, trans_b=tb)
+            assert p["kernel"] == "gemm_w4" and p["tile_m"] == 256, p
+            assert p["atom"] == "v_mfma_f32_32x32x16_bf16" and p["waves"] == [2, 2]
+            assert p["a_major"] == ("m" if ta else "k") and p["b_major"] == ("k" if tb else "n")
+            assert p["lds_read_a"] == ("ds_read_b64_tr_b16" if ta else "ds_read_b128")
+            assert p["lds_read_b"] == ("ds_read_b128" if tb else "ds_read_b64_tr_b16")
+    p = plan(trans_b=0, a_type=rt.E4M3, b_type=rt.E4M3, c_type=rt.BF16)
+    assert p["atom"] == "v_mfma_scale_f32_32x32x64_f8f6f4" and p["lds_read_b"] == "ds_read_b64_tr_b8"
+    p = plan(trans_a=1, a_type=rt.I8, b_type=rt.I8, c_type=rt.I32)
+    assert p["atom"] == "v_mfma_i32_32x32x32_i8" and p["lds_read_a"] == "ds_read_b64_tr_b8"
+    # Fewer than 128 256x256 tiles: 128x128 tiles, in every layout.
+    assert plan(m=1024, trans_b=0)["kernel"] == "gemm_128"
+    assert plan(m=1024, trans_a=1, lda=1024)["kernel"] == "gemm_128"
+    # Small M with K-contiguous operands: the small-M kernel.
+    p = plan(m=16)
+    assert p["kernel"] == "gemm_skinny" and p["atom"] == "v_mfma_f32_16x16x32_bf16"
+    # Split-K shows up in the plan when the workspace is there.
+    p = plan(m=128, trans_b=0, workspace_bytes=1 << 30)
+    assert p["kernel"] == "gemm_128" and p["slices"] == 4
+    assert p["workspace_bytes"] == 4 * 128 * 4096 * 4
+    assert plan(m=128, trans_b=0)["slices"] == 1
+
+
+def test_gemm_plan_generic_cases():
+    # f32, 16 B misalignment of a pitch, a K-contiguous operand without whole
+    # 16 B pieces of K, and a pitch whose tile reaches past 2^31 bytes run the
+    # generic kernel.
+    assert plan(a_type=rt.F32, b_type=rt.F32, c_type=rt.F32)["kernel"] == "gemm_generic"
+    assert plan(lda=4100)["kernel"] == "gemm_generic"
+    assert plan(k=4092, lda=4096, ldb=4096)["kernel"] == "gemm_generic"
+    # ...but an M/N-major operand takes any K (its K tail is per k-row).
+    assert plan(k=4092, lda=4096, trans_a=1, trans_b=0)["kernel"] == "gemm_w4"
+    big = (1 << 31) // (255 * 2) + 8
+    assert plan(lda=big - big % 8)["kernel"] == "gemm_generic"
+    assert plan(lda=(1 << 31) // (256 * 2) - 4096)["kernel"] == "gemm_w4"
+    # M/N-major: (K - 1) pitches plus a tile row.
+    assert plan(trans_b=0, ldb=(1 << 31) // (4095 * 2) + 8)["kernel"] == "gemm_generic"
+    # Ragged N with a 16 B pitch of C stays on the matrix cores.
+    assert plan(n=4090, ldb=4096)["kernel"] == "gemm_w4"
+    assert plan(n=4090, ldb=4096, ldc=4090)["kernel"] == "gemm_generic"
+    with pytest.raises(ValueError, match="legacy-gemm-shape"):
+        plan(m=0)
+
+
+def test_attn_rejects_kv_rows_beyond_32bit_offsets():
+    # 32 heads x 128 dims viewed [b, s, h, d] -> [b, h, s, d]: a key row is
+    # 8 KiB apart, so key 2^18 (the 2^18 + 1st) starts at 2 GiB.
+    rc, msg = attn_call(seq_q=64, seq_k=262145, k_stride_s=4096, v_stride_s=4096,
+                        k_stride_b=4096 * 262145, v_stride_b=4096 * 262145, k_stride_h=128,
+                        v_stride_h=128)
+    assert rc == rt.EUNSUP and "2^31 - 1 bytes" in msg, msg

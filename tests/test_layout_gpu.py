@@ -43,6 +43,35 @@ def test_mfma_fragment_map_matches_hardware(atom):
         assert np.array_equal(got, expect), f"k0={k0}"
 
 
+@pytest.mark.parametrize("bits", [16, 8])
+def test_transposing_lds_reads_match_the_gemm_lane_map(bits):
+    # The GEMM kernels read M/N-major operand tiles with ds_read_b64_tr_b16 /
+    # _tr_b8 assuming: inside each 16-lane group G, lane j receives element
+    # j % per of the 8 bytes that lane 16 G + (16 / per) e + j // per
+    # addressed, as its element e (per = elements in 8 bytes).
+    per = 4 if bits == 16 else 8
+    print(f"lds transpose probe bits={bits}", flush=True)
+    out = torch.full((64 * per,), -1, dtype=torch.int16, device="cuda")
+    rt.probe_lds_transpose(bits, out)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().view(np.uint16).reshape(64, per).astype(np.int64)
+    expect = np.empty((64, per), np.int64)
+    for lane in range(64):
+        grp, j = divmod(lane, 16)
+        for e in range(per):
+            src = 16 * grp + (16 // per) * e + j // per
+            expect[lane, e] = per * src + j % per
+    assert np.array_equal(got, expect)
+
+
+def test_lds_probe_rejects_bad_requests():
+    out = torch.zeros(16, dtype=torch.int16, device="cuda")
+    with pytest.raises(ValueError, match="buffer holds"):
+        rt.probe_lds_transpose(16, out)
+    with pytest.raises(ValueError, match="bits must be"):
+        rt.probe_lds_transpose(4, out)
+
+
 def test_probe_rejects_bad_requests():
     out = torch.zeros(16, dtype=torch.float32, device="cuda")
     with pytest.raises(ValueError, match="buffer holds"):
