@@ -62,26 +62,32 @@ def make_workloads(torch, rt):
         g.manual_seed(seed)
         return g
 
-    def gemm(m, n, k, kind):
+    def gemm(m, n, k, kind, trans_a=False, trans_b=True):
+        # A stored [M, K] ([K, M] with trans_a), B stored [N, K] ([K, N]
+        # without trans_b).
+        a_shape = (k, m) if trans_a else (m, k)
+        b_shape = (n, k) if trans_b else (k, n)
+
         def setup():
             if kind == "int8":
-                a = torch.randint(-127, 128, (m, k), generator=gen(1), device=dev, dtype=torch.int8)
-                b = torch.randint(-127, 128, (n, k), generator=gen(2), device=dev, dtype=torch.int8)
+                a = torch.randint(-127, 128, a_shape, generator=gen(1), device=dev, dtype=torch.int8)
+                b = torch.randint(-127, 128, b_shape, generator=gen(2), device=dev, dtype=torch.int8)
                 c = torch.empty(m, n, dtype=torch.int32, device=dev)
-                return lambda: rt.gemm(a, b, c, trans_b=True)
+                return lambda: rt.gemm(a, b, c, trans_a=trans_a, trans_b=trans_b)
             if kind == "fp8":
-                a = torch.randn(m, k, generator=gen(1), device=dev)
-                b = torch.randn(n, k, generator=gen(2), device=dev)
+                a = torch.randn(a_shape, generator=gen(1), device=dev)
+                b = torch.randn(b_shape, generator=gen(2), device=dev)
                 sa, sb = 448.0 / float(a.abs().max()), 448.0 / float(b.abs().max())
                 a8, b8 = (a * sa).to(torch.float8_e4m3fn), (b * sb).to(torch.float8_e4m3fn)
                 del a, b
                 c = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
-                return lambda: rt.gemm(a8, b8, c, trans_b=True, scale_a=1 / sa, scale_b=1 / sb)
+                return lambda: rt.gemm(a8, b8, c, trans_a=trans_a, trans_b=trans_b,
+                                       scale_a=1 / sa, scale_b=1 / sb)
             dt = torch.bfloat16 if kind == "bf16" else torch.float16
-            a = torch.randn(m, k, generator=gen(1), device=dev).to(dt)
-            b = torch.randn(n, k, generator=gen(2), device=dev).to(dt)
+            a = torch.randn(a_shape, generator=gen(1), device=dev).to(dt)
+            b = torch.randn(b_shape, generator=gen(2), device=dev).to(dt)
             c = torch.empty(m, n, dtype=dt, device=dev)
-            return lambda: rt.gemm(a, b, c, trans_b=True)
+            return lambda: rt.gemm(a, b, c, trans_a=trans_a, trans_b=trans_b)
         return setup
 
     def attn(causal):
@@ -136,6 +142,12 @@ def make_workloads(torch, rt):
     fa = 4.0 * 4 * 32 * 4096 * 4096 * 128
     return {
         "gemm_bf16_4096": ("bf16", 2.0 * 4096 ** 3, gemm(4096, 4096, 4096, "bf16")),
+        # The other storage orders of the headline GEMM: NN is the builder's
+        # default (transA = transB = False) and the reference's GEMM tile
+        # program's B [K, N] (tmp/ir.mlir:2-16).
+        "gemm_bf16_4096_nn": ("bf16", 2.0 * 4096 ** 3, gemm(4096, 4096, 4096, "bf16", False, False)),
+        "gemm_bf16_4096_tn": ("bf16", 2.0 * 4096 ** 3, gemm(4096, 4096, 4096, "bf16", True, True)),
+        "gemm_bf16_4096_tt": ("bf16", 2.0 * 4096 ** 3, gemm(4096, 4096, 4096, "bf16", True, False)),
         "gemm_f16_4096_nt": ("f16", 2.0 * 4096 ** 3, gemm(4096, 4096, 4096, "f16")),
         "gemm_fp8_4096x8192x8192": ("fp8", 2.0 * 4096 * 8192 * 8192,
                                     gemm(4096, 8192, 8192, "fp8")),

@@ -57,6 +57,23 @@ typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
+// Transposing LDS reads through a restrict pointer.  The intrinsics carry
+// no pointer information of their own beyond the address, and without an
+// alias scope the waitcnt insertion makes every one of them wait for all
+// LDS-DMA loads in flight (vmcnt(0)), although those write another stage
+// slot: a stall of the whole memory latency in the middle of a stage.  The
+// scope of the restrict parameter lets them issue like the plain
+// ds_read_b128 loads of K-major tiles.  For both, the true dependency (a
+// stage's DMA before its first read) is ordered by the kernels themselves:
+// each wave waits for its own DMA (vmcnt) and a workgroup barrier follows,
+// before any wave reads the stage.
+__device__ __forceinline__ s16x4 lds_read_tr16(const char* __restrict__ p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p);
+}
+__device__ __forceinline__ i32x2 lds_read_tr8(const char* __restrict__ p) {
+  return __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2*)p);
+}
+
 template <Elt IN, bool MN, int BT, int KR>
 struct OpTile {
   using Op = Mfma32<IN>;
@@ -137,7 +154,12 @@ struct OpTile {
   }
   template <int NB>
   __device__ static __forceinline__ uint32_t offset(const Dma<NB>& d, int i, int phys) {
-    return phys * kStep < d.lim[i] ? d.off[i] + (uint32_t)phys * d.adv : 0x80000000u;
+    uint32_t o = d.off[i] + (uint32_t)phys * d.adv;
+    // Materialise the live offset in every lane, so that the select stays a
+    // v_cndmask: otherwise the backend turns it into exec-masked code, whose
+    // EXEC writes split the scheduling regions the pipeline relies on.
+    asm("" : "+v"(o));
+    return phys * kStep < d.lim[i] ? o : 0x80000000u;
   }
   // Bytes to advance the operand pointer by for a K slice starting kb bytes in.
   __device__ static __forceinline__ int64_t slice_shift(int64_t kb, int64_t ld_b) {
@@ -182,16 +204,16 @@ struct OpTile {
     } else if constexpr (kEsz == 2) {
       static_assert(kLaneChunks == 1, "16-bit operand: 8 k per lane");
       const char* p = base + f.off + s * 16 * kRB;
-      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p);
-      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p + 4 * kRB));
+      const s16x4 lo = lds_read_tr16(p);
+      const s16x4 hi = lds_read_tr16(p + 4 * kRB);
       const i32x2 a = __builtin_bit_cast(i32x2, lo), b = __builtin_bit_cast(i32x2, hi);
       out[0] = i32x4{a[0], a[1], b[0], b[1]};
     } else {
       const char* p = base + f.off + s * Op::kBytes * kRB;
 #pragma unroll
       for (int j = 0; j < kLaneChunks; ++j) {
-        const i32x2 a = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2*)(p + 16 * j * kRB));
-        const i32x2 b = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2*)(p + (16 * j + 8) * kRB));
+        const i32x2 a = lds_read_tr8(p + 16 * j * kRB);
+        const i32x2 b = lds_read_tr8(p + (16 * j + 8) * kRB);
         out[j] = i32x4{a[0], a[1], b[0], b[1]};
       }
     }
