@@ -13,6 +13,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 #include <string>
 
 #include "../../include/frisk_hip.h"
@@ -133,6 +134,10 @@ const char* frisk_last_error(void) { return g_last_error.c_str(); }
 
 int frisk_abi_version(void) { return FRISK_ABI_VERSION; }
 
+}  // extern "C"
+
+namespace {
+
 // Which kernel family a GEMM descriptor goes to.
 enum class GemmRoute { Skinny, Mfma, Generic };
 
@@ -226,15 +231,6 @@ int64_t gemm_workspace(const frisk::GemmArgs& g, GemmRoute route) {
   return 0;
 }
 
-int64_t frisk_gemm_workspace_size(const frisk_gemm_desc* d) {
-  g_last_error.clear();
-  frisk::GemmArgs g;
-  GemmRoute route;
-  const int rc = check_gemm(d, "frisk_gemm_workspace_size", false, g, route);
-  if (rc) return rc;
-  return gemm_workspace(g, route);
-}
-
 const char* mfma_atom(frisk::Elt in) {
   switch (in) {
     case frisk::Elt::BF16: return "v_mfma_f32_32x32x16_bf16";
@@ -243,6 +239,37 @@ const char* mfma_atom(frisk::Elt in) {
     case frisk::Elt::I8: return "v_mfma_i32_32x32x32_i8";
     default: return "";
   }
+}
+
+// Launches a validated GEMM on its route with an optional split-K scratch.
+int launch_gemm(const frisk::GemmArgs& g, GemmRoute route, void* ws, int64_t ws_bytes,
+                void* stream, const char* fn) {
+  clear_stale_error();
+  hipError_t e;
+  if (route == GemmRoute::Skinny && ws && g.m > kSkinnySplitMaxM) {
+    e = frisk::gemm_mfma(g, (hipStream_t)stream, ws, ws_bytes);
+  } else if (route == GemmRoute::Skinny) {
+    e = frisk::gemm_skinny(g, (hipStream_t)stream, ws, ws_bytes);
+  } else if (route == GemmRoute::Mfma) {
+    e = frisk::gemm_mfma(g, (hipStream_t)stream, ws, ws_bytes);
+  } else {
+    e = frisk::gemm_generic_any(g, (hipStream_t)stream);
+  }
+  if (e != hipSuccess) return fail(FRISK_EHIP, "%s launch: %s", fn, hipGetErrorString(e));
+  return FRISK_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int64_t frisk_gemm_workspace_size(const frisk_gemm_desc* d) {
+  g_last_error.clear();
+  frisk::GemmArgs g;
+  GemmRoute route;
+  const int rc = check_gemm(d, "frisk_gemm_workspace_size", false, g, route);
+  if (rc) return rc;
+  return gemm_workspace(g, route);
 }
 
 int frisk_gemm_plan(const frisk_gemm_desc* d, char* buf, int64_t len) {
@@ -312,19 +339,7 @@ int frisk_gemm(const frisk_gemm_desc* d, void* stream) {
       ws_bytes = d->workspace_bytes;
     }
   }
-  clear_stale_error();
-  hipError_t e;
-  if (route == GemmRoute::Skinny && ws && g.m > kSkinnySplitMaxM) {
-    e = frisk::gemm_mfma(g, (hipStream_t)stream, ws, ws_bytes);
-  } else if (route == GemmRoute::Skinny) {
-    e = frisk::gemm_skinny(g, (hipStream_t)stream, ws, ws_bytes);
-  } else if (route == GemmRoute::Mfma) {
-    e = frisk::gemm_mfma(g, (hipStream_t)stream, ws, ws_bytes);
-  } else {
-    e = frisk::gemm_generic_any(g, (hipStream_t)stream);
-  }
-  if (e != hipSuccess) return hip_fail(e, "frisk_gemm launch");
-  return FRISK_OK;
+  return launch_gemm(g, route, ws, ws_bytes, stream, "frisk_gemm");
 }
 
 int frisk_attn_fwd(const frisk_attn_desc* d, void* stream) {
@@ -583,6 +598,72 @@ int frisk_probe_lds_transpose(int bits, uint16_t* out, int64_t out_elems, void* 
   hipError_t e = frisk::lds_transpose_probe(bits, out, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "lds-transpose-probe launch");
   return FRISK_OK;
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Allocation-free GEMM.  frisk_gemm_noalloc runs exactly what frisk_gemm
+// runs with a workspace of frisk_gemm_workspace_size() bytes, but its
+// split-K partials live in `scratch`, a file-scope device array: the call
+// allocates nothing.  Each GPU the library runs on holds its own copy of the
+// array until the process ends.  In host code the name `scratch` is only a
+// host-side stand-in: its device address on the current GPU comes from
+// hipGetSymbolAddress, taken once per device and kept in g_scratch, and only
+// that address is ever passed to a kernel.
+// ---------------------------------------------------------------------------
+namespace {
+
+constexpr int64_t kNoAllocScratchBytes = FRISK_GEMM_NOALLOC_SCRATCH_BYTES;
+__device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch[kMaxDevices];  // device address of `scratch` per device
+
+// The current device's address of `scratch` (resolved on first use).
+int scratch_address(void** out, const char* fn) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(FRISK_EHIP, "%s: hipGetDevice: %s", fn, hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(FRISK_EUNSUP, "%s: device %d beyond the %d this library tracks", fn, dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(FRISK_EHIP, "%s: hipGetSymbolAddress(scratch): %s", fn, hipGetErrorString(e));
+    g_scratch[dev] = p;
+  }
+  *out = g_scratch[dev];
+  return FRISK_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int frisk_gemm_noalloc(const frisk_gemm_desc* d, void* stream) {
+  g_last_error.clear();
+  frisk::GemmArgs g;
+  GemmRoute route;
+  const int rc = check_gemm(d, "frisk_gemm_noalloc", true, g, route);
+  if (rc) return rc;
+  if (d->workspace || d->workspace_bytes)
+    return fail(FRISK_EINVAL, "frisk_gemm_noalloc: takes no workspace (its scratch is the "
+                              "library's own); pass workspace = NULL, workspace_bytes = 0");
+  const int64_t need = gemm_workspace(g, route);
+  if (need > kNoAllocScratchBytes)
+    return fail(FRISK_EUNSUP, "frisk_gemm_noalloc: this GEMM splits K over %lld bytes of partials, "
+                              "beyond the %lld-byte scratch; call frisk_gemm with a workspace",
+                (long long)need, (long long)kNoAllocScratchBytes);
+  void* ws = nullptr;
+  if (need > 0) {
+    const int src = scratch_address(&ws, "frisk_gemm_noalloc");
+    if (src) return src;
+  }
+  return launch_gemm(g, route, ws, need > 0 ? kNoAllocScratchBytes : 0, stream, "frisk_gemm_noalloc");
 }
 
 }  // extern "C"

@@ -20,7 +20,8 @@ OK, EINVAL, EUNSUP, EHIP = 0, -1, -2, -3
 DTYPE_NAMES = {F32: "f32", F16: "f16", BF16: "bf16", E4M3: "e4m3", I8: "i8", I32: "i32", F64: "f64"}
 
 # Exported symbols declared by include/frisk_hip.h.
-EXPORTS = ("frisk_gemm", "frisk_gemm_workspace_size", "frisk_gemm_plan", "frisk_attn_fwd",
+EXPORTS = ("frisk_gemm", "frisk_gemm_workspace_size", "frisk_gemm_plan", "frisk_gemm_noalloc",
+           "frisk_attn_fwd",
            "frisk_reduce", "frisk_reduce_workspace_size",
            "frisk_copy", "frisk_fill",
            "frisk_last_error", "frisk_abi_version", "frisk_probe_mfma_layout",
@@ -111,6 +112,8 @@ def load() -> ctypes.CDLL:
     lib.frisk_gemm_workspace_size.restype = ctypes.c_int64
     lib.frisk_gemm_plan.argtypes = [ctypes.POINTER(GemmDesc), ctypes.c_char_p, ctypes.c_int64]
     lib.frisk_gemm_plan.restype = ctypes.c_int
+    lib.frisk_gemm_noalloc.argtypes = [ctypes.POINTER(GemmDesc), ctypes.c_void_p]
+    lib.frisk_gemm_noalloc.restype = ctypes.c_int
     lib.frisk_attn_fwd.argtypes = [ctypes.POINTER(AttnDesc), ctypes.c_void_p]
     lib.frisk_attn_fwd.restype = ctypes.c_int
     lib.frisk_reduce.argtypes = [ctypes.POINTER(ReduceDesc), ctypes.c_void_p]
@@ -242,6 +245,21 @@ def gemm(a, b, c, *, trans_a=False, trans_b=False, clear_accum=True,
             d.workspace, d.workspace_bytes = ws.data_ptr(), ws.numel() * ws.element_size()
     _check(load().frisk_gemm(ctypes.byref(d), ctypes.c_void_p(_stream_handle(stream))),
            "frisk_gemm")
+    return c
+
+
+# FRISK_GEMM_NOALLOC_SCRATCH_BYTES of include/frisk_hip.h.
+NOALLOC_SCRATCH_BYTES = 64 << 20
+
+
+def gemm_noalloc(a, b, c, *, trans_a=False, trans_b=False, clear_accum=True,
+                 scale_a=1.0, scale_b=1.0, stream=None):
+    """frisk_gemm_noalloc: gemm() with the split-K partials in the library's
+    own device scratch; nothing is allocated."""
+    d = gemm_desc(a, b, c, trans_a=trans_a, trans_b=trans_b, clear_accum=clear_accum,
+                  scale_a=scale_a, scale_b=scale_b)
+    _check(load().frisk_gemm_noalloc(ctypes.byref(d), ctypes.c_void_p(_stream_handle(stream))),
+           "frisk_gemm_noalloc")
     return c
 
 

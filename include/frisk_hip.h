@@ -116,6 +116,23 @@ int frisk_gemm(const frisk_gemm_desc* desc, void* stream);
  * tile addresses spans less than 2^31 bytes; anything else (and f32) runs a
  * correct but slower generic kernel. */
 
+/* frisk_gemm without any device allocation by the library or the caller:
+ * no hipMalloc, hipFree or allocating library routine is called.  No
+ * counterpart in the reference; it is for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * allocation).  It runs the same kernels as frisk_gemm given a workspace of
+ * frisk_gemm_workspace_size(desc) bytes, with the split-K partials in a
+ * device array of FRISK_GEMM_NOALLOC_SCRATCH_BYTES that the library holds on
+ * every GPU it runs on until the process ends.  desc->workspace must be NULL
+ * and workspace_bytes 0.  A GEMM whose split needs more scratch than that is
+ * rejected with FRISK_EUNSUP (call frisk_gemm with a workspace instead).
+ * Calls on one GPU share that array: calls that overlap in time on one GPU
+ * (different streams, or host threads) race on it and must be serialised by
+ * the caller; calls ordered on one stream are safe.  The first call on a
+ * device looks the array up there (hipGetSymbolAddress). */
+#define FRISK_GEMM_NOALLOC_SCRATCH_BYTES (64ll << 20)
+int frisk_gemm_noalloc(const frisk_gemm_desc* desc, void* stream);
+
 /* Workspace bytes that make frisk_gemm(desc) split K (0: none is used), or
  * a negative FRISK_E* code for an invalid descriptor.  Pointers in desc are
  * not read.  No counterpart in the reference (its GEMM ops take no

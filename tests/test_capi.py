@@ -367,3 +367,28 @@ def test_attn_rejects_kv_rows_beyond_32bit_offsets():
                         k_stride_b=4096 * 262145, v_stride_b=4096 * 262145, k_stride_h=128,
                         v_stride_h=128)
     assert rc == rt.EUNSUP and "2^31 - 1 bytes" in msg, msg
+
+
+def noalloc_call(**over):
+    d = rt.GemmDesc(m=64, n=64, k=64, trans_a=0, trans_b=1, a_type=rt.BF16, b_type=rt.BF16,
+                    c_type=rt.BF16, clear_accum=1, a=16, lda=64, b=16, ldb=64, c=16, ldc=64,
+                    scale_a=1.0, scale_b=1.0)
+    for key, val in over.items():
+        setattr(d, key, val)
+    lib = rt.load()
+    rc = lib.frisk_gemm_noalloc(ctypes.byref(d), None)
+    return rc, lib.frisk_last_error().decode()
+
+
+def test_gemm_noalloc_rejects_before_any_device_work():
+    # The usual contract checks, a caller workspace, and a split whose
+    # partials exceed the library's scratch (768 x 8192 x 28672 splits into
+    # 120 MiB of partials; the scratch holds 64 MiB).
+    rc, msg = noalloc_call(m=0)
+    assert rc == rt.EINVAL and msg.startswith("legacy-gemm-shape"), msg
+    rc, msg = noalloc_call(workspace=16, workspace_bytes=1 << 20)
+    assert rc == rt.EINVAL and "takes no workspace" in msg, msg
+    rc, msg = noalloc_call(m=768, n=8192, k=28672, lda=28672, ldb=28672, ldc=8192)
+    assert rc == rt.EUNSUP and "beyond the 67108864-byte scratch" in msg, msg
+    assert rt.NOALLOC_SCRATCH_BYTES == 64 << 20
+    assert "#define FRISK_GEMM_NOALLOC_SCRATCH_BYTES (64ll << 20)" in HEADER.read_text()
