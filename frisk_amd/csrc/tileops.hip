@@ -291,7 +291,7 @@ __global__ __launch_bounds__(kColThreads) void reduce_cols_kernel(
 template <Elt E, int KIND>
 __global__ __launch_bounds__(tile::kThreads) void reduce_cols_blocks_kernel(
     const void* __restrict__ src, int64_t ld, int64_t rows, int64_t cols, int sps_log2,
-    int b_log2, float* __restrict__ partial) {
+    int b_log2, float* __restrict__ partial, int vec_ok) {
   using namespace tile;
   constexpr int kEsz = EltInfo<E>::bytes;
   __shared__ float part[kThreads * 4];
@@ -303,7 +303,9 @@ __global__ __launch_bounds__(tile::kThreads) void reduce_cols_blocks_kernel(
   const int64_t gb = ((int64_t)1 << b_log2) / groups;  // rows per group, >= 8
   const int64_t r0 = ((int64_t)blockIdx.y << b_log2) + g * gb;
   const int64_t r1 = min(rows, r0 + gb);
-  const bool full = c0 + 4 <= cols;
+  // Four-element vector loads need the source and its rows aligned to them
+  // (element-aligned views such as x[:, 1:] take element loads).
+  const bool full = vec_ok && c0 + 4 <= cols;
 
   // gb <= 2^12 (cols_split), so a group pushes at most 2^9 eight-row subtrees.
   Counter<E, KIND, 10> ctr[4];
@@ -651,9 +653,10 @@ hipError_t reduce_typed(const ReduceArgs& a, hipStream_t s) {
 #undef FRISK_ROWS
   } else if (a.workspace) {
     const ColsSplit sp = cols_split(a.rows, a.cols);
+    const int vec_ok = aligned(a.src, a.ld * kEsz, 4 * kEsz);
     hipLaunchKernelGGL((reduce_cols_blocks_kernel<E, KIND>), dim3(sp.strips, sp.blocks),
                        dim3(tile::kThreads), 0, s, a.src, a.ld, a.rows, a.cols, sp.sps_log2,
-                       sp.b_log2, (float*)a.workspace);
+                       sp.b_log2, (float*)a.workspace, vec_ok);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL((reduce_cols_final_kernel<E, KIND>),

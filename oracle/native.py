@@ -29,6 +29,9 @@ def load():
         lib.oracle_attn_f64.argtypes = [i64, i64, i64, dp, dp, dp, c_int, ctypes.c_double, dp, dp,
                                         c_int]
         lib.oracle_attn_f64.restype = c_int
+        lib.oracle_attn_rows_f64.argtypes = [i64, i64, i64, dp, i64, dp, dp, dp, c_int,
+                                             ctypes.c_double, dp, dp, c_int]
+        lib.oracle_attn_rows_f64.restype = c_int
         lib.oracle_max_threads.restype = c_int
         _lib = lib
     return _lib
@@ -64,6 +67,26 @@ def attn_f64(q, k, v, *, causal=False, scale=None, threads=0):
     lse = np.empty(sq)
     rc = load().oracle_attn_f64(sq, sk, d, _p(q), _p(k), _p(v), int(causal), float(scale), _p(o),
                                 _p(lse), threads)
+    assert rc == 0
+    return o, lse
+
+
+def attn_rows_f64(q, k, v, rows, *, causal=False, scale=None, threads=0):
+    """Rows `rows` of one head: q [sq, d] (all rows), k/v [sk, d] ->
+    (o [len(rows), d], lse [len(rows)]); each row's causal mask follows its
+    index in q."""
+    q = np.ascontiguousarray(q, dtype=np.float64)
+    k = np.ascontiguousarray(k, dtype=np.float64)
+    v = np.ascontiguousarray(v, dtype=np.float64)
+    rows = np.ascontiguousarray(rows, dtype=np.int64)
+    sq, d = q.shape
+    sk = k.shape[0]
+    if scale is None:
+        scale = d ** -0.5
+    o = np.empty((len(rows), d))
+    lse = np.empty(len(rows))
+    rc = load().oracle_attn_rows_f64(sq, sk, d, _p(rows), len(rows), _p(q), _p(k), _p(v),
+                                     int(causal), float(scale), _p(o), _p(lse), threads)
     assert rc == 0
     return o, lse
 

@@ -11,6 +11,7 @@
  *   tail_attention_reference.py:81-114), optional causal mask
  *   (key j visible to query i iff j <= i + sk - sq) and natural-log LSE.
  *   OpenMP over query rows.
+ * oracle_attn_rows_f64: the same for a subset of a head's query rows.
  */
 #include <math.h>
 #include <stdint.h>
@@ -71,6 +72,34 @@ int oracle_gemm_f64(int64_t m, int64_t n, int64_t k, const double* a, int64_t ld
   return 0;
 }
 
+/* Row i of one head (query qi, keys/values [0, end)) into oi / *lse_i; s
+ * is scratch of sk doubles. */
+static void attn_row(const double* qi, const double* k, const double* v, int64_t end, int64_t d,
+                     double scale, double* s, double* oi, double* lse_i) {
+  for (int64_t x = 0; x < d; ++x) oi[x] = 0.0;
+  if (end <= 0) {
+    if (lse_i) *lse_i = -INFINITY;
+    return;
+  }
+  double mx = -INFINITY;
+  for (int64_t j = 0; j < end; ++j) {
+    const double* kj = k + j * d;
+    double acc = 0.0;
+    for (int64_t x = 0; x < d; ++x) acc += qi[x] * kj[x];
+    s[j] = acc * scale;
+    if (s[j] > mx) mx = s[j];
+  }
+  double den = 0.0;
+  for (int64_t j = 0; j < end; ++j) {
+    const double e = exp(s[j] - mx);
+    den += e;
+    const double* vj = v + j * d;
+    for (int64_t x = 0; x < d; ++x) oi[x] += e * vj[x];
+  }
+  for (int64_t x = 0; x < d; ++x) oi[x] /= den;
+  if (lse_i) *lse_i = log(den) + mx;
+}
+
 int oracle_attn_f64(int64_t sq, int64_t sk, int64_t d, const double* q, const double* k,
                     const double* v, int causal, double scale, double* o, double* lse,
                     int threads) {
@@ -82,32 +111,35 @@ int oracle_attn_f64(int64_t sq, int64_t sk, int64_t d, const double* q, const do
     double* s = (double*)malloc(sizeof(double) * (size_t)sk);
 #pragma omp for schedule(dynamic, 16)
     for (int64_t i = 0; i < sq; ++i) {
-      const double* qi = q + i * d;
       int64_t end = sk;
       if (causal) end = i + diag + 1 < sk ? i + diag + 1 : sk;
-      double* oi = o + i * d;
-      for (int64_t x = 0; x < d; ++x) oi[x] = 0.0;
-      if (end <= 0) {
-        if (lse) lse[i] = -INFINITY;
-        continue;
-      }
-      double mx = -INFINITY;
-      for (int64_t j = 0; j < end; ++j) {
-        const double* kj = k + j * d;
-        double acc = 0.0;
-        for (int64_t x = 0; x < d; ++x) acc += qi[x] * kj[x];
-        s[j] = acc * scale;
-        if (s[j] > mx) mx = s[j];
-      }
-      double den = 0.0;
-      for (int64_t j = 0; j < end; ++j) {
-        const double e = exp(s[j] - mx);
-        den += e;
-        const double* vj = v + j * d;
-        for (int64_t x = 0; x < d; ++x) oi[x] += e * vj[x];
-      }
-      for (int64_t x = 0; x < d; ++x) oi[x] /= den;
-      if (lse) lse[i] = log(den) + mx;
+      attn_row(q + i * d, k, v, end, d, scale, s, o + i * d, lse ? lse + i : NULL);
+    }
+    free(s);
+  }
+  return 0;
+}
+
+/* The same arithmetic for a subset of the sq query rows of one head: row
+ * rows[r] (its causal mask from that index) into o[r] / lse[r]; q holds all
+ * sq rows.  A sampled check of a full-size head at a fraction of the cost. */
+int oracle_attn_rows_f64(int64_t sq, int64_t sk, int64_t d, const int64_t* rows, int64_t nrows,
+                         const double* q, const double* k, const double* v, int causal,
+                         double scale, double* o, double* lse, int threads) {
+  if (sq <= 0 || sk <= 0 || d <= 0 || nrows < 0) return -1;
+  for (int64_t r = 0; r < nrows; ++r)
+    if (rows[r] < 0 || rows[r] >= sq) return -1;
+  set_threads(threads);
+  const int64_t diag = sk - sq;
+#pragma omp parallel
+  {
+    double* s = (double*)malloc(sizeof(double) * (size_t)sk);
+#pragma omp for schedule(dynamic, 4)
+    for (int64_t r = 0; r < nrows; ++r) {
+      const int64_t i = rows[r];
+      int64_t end = sk;
+      if (causal) end = i + diag + 1 < sk ? i + diag + 1 : sk;
+      attn_row(q + i * d, k, v, end, d, scale, s, o + r * d, lse ? lse + r : NULL);
     }
     free(s);
   }

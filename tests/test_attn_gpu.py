@@ -12,7 +12,7 @@ import torch
 from frisk_amd import runtime as rt
 from oracle import attention as A
 from oracle import gemm as G
-from tests.gpu_util import Guarded, gen
+from tests.gpu_util import Guarded, gen, sample_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -60,20 +60,28 @@ def test_parity_small(b, h, sq, sk, causal, dt):
 
 
 @pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
-def test_config_c5_full_size_sampled_heads(native_oracle, causal):
-    # b4 h32 s4096 d128 bf16, scale 1/sqrt(128); every head is
-    # computed on the GPU, two heads are checked against the fp64 C oracle.
+def test_config_c5_every_head_sampled_rows(native_oracle, causal):
+    # b4 h32 s4096 d128 bf16, scale 1/sqrt(128).  All 128 (b, h)
+    # heads are checked against the fp64 C oracle on 64 sampled query rows
+    # each (always including the first and last row; under the causal mask
+    # row i sees keys 0..i), output and LSE.
     b, h, s = 4, 32, 4096
     q, k, v = qkv(b, h, s, s, torch.bfloat16, seed=5)
     o, lse = run(q, k, v, causal)
-    for bi, hi in ((0, 0), (3, 31)):
-        ro, rl = native_oracle.attn_f64(q[bi, hi].double().cpu().numpy(),
-                                        k[bi, hi].double().cpu().numpy(),
-                                        v[bi, hi].double().cpu().numpy(), causal=causal,
-                                        scale=SCALE)
-        assert G.row_scaled_error(o[bi, hi].double().cpu().numpy(), ro) <= 1e-2
-        assert np.abs(lse[bi, hi].cpu().numpy() - rl).max() <= LSE_TOL[torch.bfloat16]
-    assert torch.isfinite(o.float()).all()
+    Q, K, V = (t.float().cpu().numpy() for t in (q, k, v))
+    O, L = o.float().cpu().numpy(), lse.cpu().numpy()
+    worst, worst_lse = 0.0, 0.0
+    for bi in range(b):
+        for hi in range(h):
+            rows = sample_rows(s, 64, seed=1000 * bi + hi)
+            ro, rl = native_oracle.attn_rows_f64(Q[bi, hi], K[bi, hi], V[bi, hi], rows,
+                                                 causal=causal, scale=SCALE)
+            err = G.row_scaled_error(O[bi, hi][rows].astype(np.float64), ro)
+            lerr = float(np.abs(L[bi, hi][rows] - rl).max())
+            assert err <= 1e-2, (bi, hi, err)
+            assert lerr <= LSE_TOL[torch.bfloat16], (bi, hi, lerr)
+            worst, worst_lse = max(worst, err), max(worst_lse, lerr)
+    print(f"c5 causal={causal}: worst row-scaled error {worst:.3e}, worst LSE error {worst_lse:.3e}")
 
 
 def test_workgroup_shapes_agree_bitwise():

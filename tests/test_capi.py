@@ -392,3 +392,37 @@ def test_gemm_noalloc_rejects_before_any_device_work():
     assert rc == rt.EUNSUP and "beyond the 67108864-byte scratch" in msg, msg
     assert rt.NOALLOC_SCRATCH_BYTES == 64 << 20
     assert "#define FRISK_GEMM_NOALLOC_SCRATCH_BYTES (64ll << 20)" in HEADER.read_text()
+
+
+def test_last_error_is_per_thread():
+    # Two host threads fail in lockstep with different errors; after both
+    # have failed, each reads back its own message (thread-local
+    # frisk_last_error), across many rounds.
+    import threading
+    rounds = 200
+    barrier = threading.Barrier(2)
+    seen = {0: [], 1: []}
+    bad = {0: dict(m=0), 1: dict(b_type=rt.F16)}
+    prefix = {0: "legacy-gemm-shape", 1: "legacy-gemm-type"}
+
+    def work(t):
+        lib = rt.load()
+        for _ in range(rounds):
+            d = rt.GemmDesc(m=64, n=64, k=64, trans_a=0, trans_b=1, a_type=rt.BF16, b_type=rt.BF16,
+                            c_type=rt.BF16, clear_accum=1, a=16, lda=64, b=16, ldb=64, c=16,
+                            ldc=64, scale_a=1.0, scale_b=1.0)
+            for key, val in bad[t].items():
+                setattr(d, key, val)
+            rc = lib.frisk_gemm(ctypes.byref(d), None)
+            barrier.wait()
+            seen[t].append((rc, lib.frisk_last_error().decode()))
+            barrier.wait()
+
+    ths = [threading.Thread(target=work, args=(t,)) for t in (0, 1)]
+    for th in ths:
+        th.start()
+    for th in ths:
+        th.join(timeout=60)
+    for t in (0, 1):
+        assert len(seen[t]) == rounds
+        assert all(rc == rt.EINVAL and msg.startswith(prefix[t]) for rc, msg in seen[t]), seen[t][:3]

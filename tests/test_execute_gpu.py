@@ -93,3 +93,23 @@ def test_execute_checks_tensors():
         F.execute(s.module, "gemm", [a, a])
     with pytest.raises(ValueError, match="no kernel"):
         F.execute(s.module, "nope", [a, a, a])
+
+
+def test_execute_config_c1_fp32_512():
+    # fp32 C = A.B, M = N = K = 512, row-major A [M, K] and
+    # B [K, N] ~ U[-1, 1] from a fixed seed, built as a Frisk GEMM IR with the
+    # reference's helper API (FriskHelper.create_gemm, python/frisk/common/
+    # utils.py:103-117) and run through execute(); checked against the fp64
+    # oracle and the reference's fp32 rank-1-update oracle
+    # (run_execution.py:58-63).
+    s, _ = P.whole_gemm(512, 512, 512, dtype="fp32", out="fp32")
+    rng = np.random.default_rng(0)
+    a_np = rng.uniform(-1, 1, (512, 512)).astype(np.float32)
+    b_np = rng.uniform(-1, 1, (512, 512)).astype(np.float32)
+    a, b = torch.from_numpy(a_np).cuda(), torch.from_numpy(b_np).cuda()
+    c = torch.full((512, 512), float("nan"), device="cuda")
+    F.execute(s.module, "gemm", [a, b, c])
+    torch.cuda.synchronize()
+    got = c.cpu().numpy().astype(np.float64)
+    assert G.row_scaled_error(got, G.gemm_fp64(a_np, b_np)) <= 1e-5
+    assert G.row_scaled_error(got, G.gemm_fp32_rank1(a_np, b_np)) <= 1e-5

@@ -167,3 +167,19 @@ def test_c_oracle_matches_numpy_oracle(native_oracle, causal):
     co, cl = native_oracle.attn_f64(q[0, 0], k[0, 0], v[0, 0], causal=causal)
     np.testing.assert_allclose(co, o[0, 0], rtol=1e-12, atol=1e-13)
     np.testing.assert_allclose(cl, lse[0, 0], rtol=1e-13)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_c_row_subset_oracle_matches_numpy_oracle(native_oracle, causal):
+    # Selected rows, each with its own causal mask (seq_k > seq_q, so the
+    # mask is offset by seq_k - seq_q), in any order, against the numpy
+    # oracle's rows; row 0 and the last row included.
+    rng = np.random.default_rng(12)
+    q = rng.standard_normal((1, 1, 70, 32))
+    k = rng.standard_normal((1, 1, 90, 32))
+    v = rng.standard_normal((1, 1, 90, 32))
+    o, lse = A.attention_fp64(q, k, v, causal=causal)
+    rows = np.array([69, 0, 17, 5, 40])
+    co, cl = native_oracle.attn_rows_f64(q[0, 0], k[0, 0], v[0, 0], rows, causal=causal)
+    np.testing.assert_allclose(co, o[0, 0][rows], rtol=1e-12, atol=1e-13)
+    np.testing.assert_allclose(cl, lse[0, 0][rows], rtol=1e-13)

@@ -314,3 +314,25 @@ def test_reduce_axis0_two_pass_matches_single_pass_and_oracle(dtype, kind, shape
     assert_same_bits(dtype, bits_of(dtype, two.t), want, "two-pass")
     assert_same_bits(dtype, bits_of(dtype, one), want, "single pass")
     assert two.guards_intact()
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("kind", ["sum", "min"])
+def test_reduce_axis0_two_pass_unaligned_view(dtype, kind):
+    """x[:, 1:] of a row-major tensor: element-aligned but not aligned to
+    four-element vectors, at >= 256 rows so the workspace (two-pass) path
+    runs; its loads fall back to elements and the result is the canonical
+    tree, bit for bit."""
+    rows, cols = 1000, 331
+    src = values(dtype, (rows, cols + 1), seed=seed_of("twopass-unaligned", dtype, kind))
+    full = device_from_bits(dtype, T.to_bits(dtype, src))
+    x = full[:, 1:]
+    assert x.data_ptr() % 16 != 0
+    assert rt.reduce_workspace_bytes(x, torch.empty(cols, dtype=TORCH[dtype], device="cuda"),
+                                     kind, axis=0) > 0
+    out = Guarded((cols,), TORCH[dtype])
+    rt.reduce(x, out.t, kind, axis=0)
+    torch.cuda.synchronize()
+    want = T.to_bits(dtype, T.reduce(src[:, 1:], kind, 0, dtype))
+    assert_same_bits(dtype, bits_of(dtype, out.t), want, "two-pass unaligned")
+    assert out.guards_intact()
