@@ -129,19 +129,22 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_128(const char* __rest
   };
 
   // ---- fragment reads -----------------------------------------------------
-  typename TA::Frag fa[TM];
-  typename TB::Frag fb[TN];
+  // K-major operands share one Frag (tile 0's) across their tiles.
+  typename TA::Frag fa[TA::kSharedFrag ? 1 : TM];
+  typename TB::Frag fb[TB::kSharedFrag ? 1 : TN];
 #pragma unroll
-  for (int t = 0; t < TM; ++t) fa[t] = TA::frag(wm * (32 * TM) + t * 32, lane);
+  for (int t = 0; t < (TA::kSharedFrag ? 1 : TM); ++t) fa[t] = TA::frag(wm * (32 * TM) + t * 32, lane);
 #pragma unroll
-  for (int t = 0; t < TN; ++t) fb[t] = TB::frag(wn * (32 * TN) + t * 32, lane);
+  for (int t = 0; t < (TB::kSharedFrag ? 1 : TN); ++t) fb[t] = TB::frag(wn * (32 * TN) + t * 32, lane);
   using Frag = Frags<TM, TN, kLaneChunks>;
   auto load_frags = [&](int slot, int s, Frag& f) {
     const char* base = smem + slot * kStageBytes;
 #pragma unroll
-    for (int t = 0; t < TM; ++t) TA::read(base, fa[t], s, f.a[t]);
+    for (int t = 0; t < TM; ++t)
+      TA::read(base, fa[TA::kSharedFrag ? 0 : t], s, f.a[t], TA::tile_off(t * 32));
 #pragma unroll
-    for (int t = 0; t < TN; ++t) TB::read(base + kTileBytes, fb[t], s, f.b[t]);
+    for (int t = 0; t < TN; ++t)
+      TB::read(base + kTileBytes, fb[TB::kSharedFrag ? 0 : t], s, f.b[t], TB::tile_off(t * 32));
   };
 
   Acc acc[TM][TN];

@@ -52,6 +52,60 @@ template <> struct Mfma32<Elt::I8> {
   }
 };
 
+// The 16x16 atoms: kBytes = bytes of one operand row consumed by one MFMA;
+// every lane supplies kBytes/4 of them (four lane groups of 16 split the
+// row), so a lane's share is the same 16 B (32 B for fp8) as with 32x32.
+template <Elt E> struct Mfma16x;
+
+template <> struct Mfma16x<Elt::BF16> {
+  static constexpr int kBytes = 64;
+  using Acc = f32x4;
+  __device__ static inline Acc run(const i32x4* a, const i32x4* b, Acc c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a[0]),
+                                                   __builtin_bit_cast(bf16x8, b[0]), c, 0, 0, 0);
+  }
+};
+
+template <> struct Mfma16x<Elt::F16> {
+  static constexpr int kBytes = 64;
+  using Acc = f32x4;
+  __device__ static inline Acc run(const i32x4* a, const i32x4* b, Acc c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a[0]),
+                                                  __builtin_bit_cast(f16x8, b[0]), c, 0, 0, 0);
+  }
+};
+
+template <> struct Mfma16x<Elt::E4M3> {
+  static constexpr int kBytes = 128;
+  using Acc = f32x4;
+  __device__ static inline Acc run(const i32x4* a, const i32x4* b, Acc c) {
+    const i32x8 av = {a[0][0], a[0][1], a[0][2], a[0][3], a[1][0], a[1][1], a[1][2], a[1][3]};
+    const i32x8 bv = {b[0][0], b[0][1], b[0][2], b[0][3], b[1][0], b[1][1], b[1][2], b[1][3]};
+    // Format 0 = fp8 e4m3 for both operands; E8M0 block scales 127 = 2^0.
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, c, 0, 0, 0, 127, 0, 127);
+  }
+};
+
+template <> struct Mfma16x<Elt::I8> {
+  static constexpr int kBytes = 64;
+  using Acc = i32x4;
+  __device__ static inline Acc run(const i32x4* a, const i32x4* b, Acc c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a[0], b[0], c, 0, 0, 0);
+  }
+};
+
+// The MFMA of an ATOM x ATOM output tile (32 or 16).  Lane L of a wave holds
+// operand row L % ATOM and the (L / ATOM)-th of the 64 / ATOM equal K pieces
+// of the instruction; accumulator element r of lane L holds output
+// (acc_row(r, L), L % ATOM).
+template <Elt E, int ATOM> struct MfmaAtom;
+template <Elt E> struct MfmaAtom<E, 32> : Mfma32<E> {
+  __device__ static inline int acc_row(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
+};
+template <Elt E> struct MfmaAtom<E, 16> : Mfma16x<E> {
+  __device__ static inline int acc_row(int r, int lane) { return 4 * (lane >> 4) + r; }
+};
+
 // s_waitcnt with only the vector-memory counter limited to n (gfx9 encoding:
 // vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]).
 #define FRISK_WAIT_VMCNT(n) \

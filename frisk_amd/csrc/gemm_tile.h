@@ -74,9 +74,9 @@ __device__ __forceinline__ i32x2 lds_read_tr8(const char* __restrict__ p) {
   return __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2*)p);
 }
 
-template <Elt IN, bool MN, int BT, int KR>
+template <Elt IN, bool MN, int BT, int KR, int ATOM = 32>
 struct OpTile {
-  using Op = Mfma32<IN>;
+  using Op = MfmaAtom<IN, ATOM>;
   static constexpr int kEsz = EltInfo<IN>::bytes;
   static constexpr int kRB = MN ? BT * kEsz : KR;  // bytes per LDS row
   static constexpr int kRows = MN ? KR / kEsz : BT;
@@ -84,22 +84,32 @@ struct OpTile {
   static constexpr int kChunks = kRB / 16;         // 16 B chunks per LDS row
   static constexpr int kRowsPerBlock = 1024 / kRB; // rows per 1 KiB DMA block
   static constexpr int kBytes = BT * KR;           // the tile, one stage
+  static constexpr int kGroups = 64 / ATOM;        // lane groups sharing one operand row
   static constexpr int kStepChunks = Op::kBytes / 16;
-  static constexpr int kLaneChunks = kStepChunks / 2;
+  static constexpr int kLaneChunks = kStepChunks / kGroups;
+  static constexpr int kLaneK = Op::kBytes / kGroups / kEsz;  // k per lane per MFMA
   static constexpr int kReadsPerChunk = MN ? 2 : 1;  // LDS reads per 16 B of operand
   static_assert(kRows * kRB == kBytes && kRowsPerBlock >= 1, "tile geometry");
   static_assert(!MN || kRB >= 128, "MN-major rows of at least 128 B");
+  static_assert(ATOM == 32 || ATOM == 16, "MFMA atom");
+  static_assert(KR % Op::kBytes == 0, "whole MFMA k-steps per stage");
 
+  // For 16x16 atoms the 32 lanes served together by a transposing read
+  // come from two lane groups, i.e. k-rows e and kLaneK + e (8 + e for
+  // 16-bit types), so the M/N-major swizzles also fold in that row bit.
   __device__ static __forceinline__ int swz(int r) {
     if constexpr (!MN) {
       if constexpr (KR == 128) return (r & 7) ^ ((r >> 3) & 1);
       else return (r >> 2) & 3;  // KR == 64
     } else if constexpr (kEsz == 2) {
-      return (r & 3) << 2;
+      if constexpr (ATOM == 32) return (r & 3) << 2;
+      else return ((r & 3) | (((r >> 3) & 1) << 2)) << 1;
     } else if constexpr (kRB >= 256) {
-      return (r & 7) << 1;
+      if constexpr (ATOM == 32) return (r & 7) << 1;
+      else return (r & 7) | (((r / kLaneK) & 1) << 3);
     } else {
-      return ((r >> 1) & 3) << 1;
+      if constexpr (ATOM == 32) return ((r >> 1) & 3) << 1;
+      else return ((r >> 1) & 3) | (((r / kLaneK) & 1) << 2);
     }
   }
 
@@ -175,35 +185,47 @@ struct OpTile {
   struct Frag {
     int off, sw;
   };
+  // K-major swizzles repeat every 16 rows, so tiles at r0 = 16 i share one
+  // swizzle and differ by the constant r0 * KR: tile_off() adds it, and the
+  // kernels keep one Frag for all K-major tiles.
+  static constexpr bool kSharedFrag = !MN;
+  __device__ static __forceinline__ constexpr int tile_off(int r0) { return MN ? 0 : r0 * KR; }
   __device__ static __forceinline__ Frag frag(int r0, int lane) {
-    const int l32 = lane & 31, half = lane >> 5;
     if constexpr (!MN) {
-      return Frag{(r0 + l32) * KR, swz(r0 + l32) ^ (half * kLaneChunks)};
-    } else if constexpr (kEsz == 2) {
-      // Lane 16G + 4e + q: k-row 8 half + e, columns r0 + 16 (G & 1) + 4q.
-      const int dg = (lane >> 4) & 1, e = (lane >> 2) & 3, q = lane & 3;
-      const int chunk = (r0 >> 3) + 2 * dg + (q >> 1);
-      return Frag{(8 * half + e) * kRB + ((chunk ^ swz(e)) << 4) + 8 * (q & 1), 0};
+      const int row = r0 + lane % ATOM, grp = lane / ATOM;
+      return Frag{row * KR, swz(lane % 16) ^ (grp * kLaneChunks)};
     } else {
-      // Lane 16G + 2e + b: k-row kLaneK half + e, columns r0 + 16 (G & 1) + 8b.
-      constexpr int kLaneK = Op::kBytes / 2;
-      const int dg = (lane >> 4) & 1, e = (lane >> 1) & 7, b = lane & 1;
-      const int chunk = (r0 >> 4) + dg;
-      return Frag{(kLaneK * half + e) * kRB + ((chunk ^ swz(e)) << 4) + 8 * b, 0};
+      // 16-lane group G of the wave covers columns r0 + 16 dg (dg < ATOM/16)
+      // at this lane group's K share kg.
+      const int G = lane >> 4, dg = G % (ATOM / 16), kg = G / (ATOM / 16);
+      if constexpr (kEsz == 2) {
+        // Lane 16G + 4e + q: k-row kLaneK kg + e, columns r0 + 16 dg + 4q.
+        const int e = (lane >> 2) & 3, q = lane & 3;
+        const int row = kLaneK * kg + e;
+        const int chunk = ((r0 + 16 * dg) >> 3) + (q >> 1);
+        return Frag{row * kRB + ((chunk ^ swz(row)) << 4) + 8 * (q & 1), 0};
+      } else {
+        // Lane 16G + 2e + b: k-row kLaneK kg + e, columns r0 + 16 dg + 8b.
+        const int e = (lane >> 1) & 7, b = lane & 1;
+        const int row = kLaneK * kg + e;
+        const int chunk = (r0 + 16 * dg) >> 4;
+        return Frag{row * kRB + ((chunk ^ swz(row)) << 4) + 8 * b, 0};
+      }
     }
   }
-  // The lane's operand of MFMA k-step s (Op::kBytes of K per row).
+  // The lane's operand of MFMA k-step s (Op::kBytes of K per row); `off` is
+  // tile_off() of the tile when f is a shared (tile 0) Frag.
   __device__ static __forceinline__ void read(const char* base, const Frag& f, int s,
-                                              i32x4 (&out)[kLaneChunks]) {
+                                              i32x4 (&out)[kLaneChunks], int off = 0) {
     if constexpr (!MN) {
 #pragma unroll
       for (int j = 0; j < kLaneChunks; ++j) {
         const int chunk = s * kStepChunks + j;
-        out[j] = *(const i32x4*)(base + f.off + ((chunk ^ f.sw) << 4));
+        out[j] = *(const i32x4*)(base + off + f.off + ((chunk ^ f.sw) << 4));
       }
     } else if constexpr (kEsz == 2) {
       static_assert(kLaneChunks == 1, "16-bit operand: 8 k per lane");
-      const char* p = base + f.off + s * 16 * kRB;
+      const char* p = base + f.off + s * (Op::kBytes / 2) * kRB;
       const s16x4 lo = lds_read_tr16(p);
       const s16x4 hi = lds_read_tr16(p + 4 * kRB);
       const i32x2 a = __builtin_bit_cast(i32x2, lo), b = __builtin_bit_cast(i32x2, hi);

@@ -19,9 +19,10 @@
 // two workgroup barriers is 64 MFMAs = 2048 cycles.  A 128-byte row segment
 // is one whole cache line: with 64-byte stages every line is fetched from L2
 // twice (rocprofv3: TCP_TCC_READ_REQ halves from 1.34e8 to 6.7e7 at 8192^3).
-// Two 64 KiB stages fill 128 KiB of the 160 KiB LDS.  With a single wave per
-// SIMD nothing else can fill a stall, so every fragment read and DMA issue
-// is placed between MFMAs explicitly (sched_group_barrier).
+// Five 32 KiB operand-tile slots fill the 160 KiB LDS as a ring (below).
+// With a single wave per SIMD nothing else can fill a stall, so every
+// fragment read and DMA issue is placed between MFMAs explicitly
+// (sched_group_barrier).
 
 #pragma once
 
@@ -32,16 +33,13 @@
 
 namespace frisk {
 
-// Bytes of K per row per stage (64 or 128), LDS stages, and the number of
-// k-steps that issue DMA (0: the default below).
+// Bytes of K per row per stage (64 or 128).
 #ifndef FRISK_G4_KR
 #define FRISK_G4_KR 128
 #endif
-#ifndef FRISK_G4_STAGES
-#define FRISK_G4_STAGES 2
-#endif
-#ifndef FRISK_G4_PARTS
-#define FRISK_G4_PARTS 0
+// MFMA output tile (32: v_mfma_*_32x32x*, 16: v_mfma_*_16x16x*).
+#ifndef FRISK_G4_ATOM
+#define FRISK_G4_ATOM 32
 #endif
 
 namespace g4 {
@@ -49,38 +47,38 @@ namespace g4 {
 constexpr int kBT = 256;
 constexpr int kThreads = 256;
 
-constexpr int lds_bytes(int kr, int stages) { return stages * 2 * kBT * kr; }
+constexpr int kRing = 5;  // operand-tile slots of the LDS ring
+constexpr int lds_bytes(int kr) { return kRing * kBT * kr; }
 
 }  // namespace g4
 
-template <Elt IN, Elt OUT, bool AM, bool BM, int KR, int S>
+template <Elt IN, Elt OUT, bool AM, bool BM, int KR, int ATOM>
 __global__ __launch_bounds__(g4::kThreads) void gemm_w4_kernel(
     const char* __restrict__ A, const char* __restrict__ B, void* __restrict__ C, int M, int N,
     int Kb, int64_t lda_b, int64_t ldb_b, int64_t ldc, float scale, int accumulate, int kb_slice,
     int64_t c_slice_bytes) {
 #if defined(__HIP_DEVICE_COMPILE__)
-  using TA = OpTile<IN, AM, g4::kBT, KR>;
-  using TB = OpTile<IN, BM, g4::kBT, KR>;
+  using TA = OpTile<IN, AM, g4::kBT, KR, ATOM>;
+  using TB = OpTile<IN, BM, g4::kBT, KR, ATOM>;
   A += TA::slice_shift((int64_t)blockIdx.y * kb_slice, lda_b);
   B += TB::slice_shift((int64_t)blockIdx.y * kb_slice, ldb_b);
   Kb = min(Kb - (int)blockIdx.y * kb_slice, kb_slice);
   C = (char*)C + (int64_t)blockIdx.y * c_slice_bytes;
-  using Op = Mfma32<IN>;
+  using Op = MfmaAtom<IN, ATOM>;
   using Acc = typename Op::Acc;
   using AccS = typename std::conditional<IN == Elt::I8, int32_t, float>::type;
   constexpr int BT = g4::kBT;
-  constexpr int TM = 4, TN = 4;                 // 32x32 atoms per wave
+  constexpr int TM = 128 / ATOM, TN = 128 / ATOM;  // atoms per wave (128x128 sub-tile)
+  constexpr int kAccN = sizeof(Acc) / 4;           // accumulator elements per lane
   constexpr int kTileBytes = BT * KR;           // one operand, one stage
-  constexpr int kStageBytes = 2 * kTileBytes;
   constexpr int kLaneChunks = TA::kLaneChunks;  // 16 B pieces per lane per MFMA
   constexpr int kSteps = KR / Op::kBytes;       // MFMA k-steps per stage
   constexpr int kBlocks = kTileBytes / 1024 / 4;  // DMA blocks per wave per operand
-  constexpr int kLoads = 2 * kBlocks;             // DMA loads per lane per stage
   // LDS read instructions per lane per k-step (two per 16 B of an MN-major
   // operand, one of a K-major one).
   constexpr int kFragReads =
       (TM * TA::kReadsPerChunk + TN * TB::kReadsPerChunk) * kLaneChunks;
-  static_assert(S >= 2 && kSteps >= 1, "pipeline shape");
+  static_assert(kSteps >= 1, "pipeline shape");
 
   extern __shared__ __attribute__((aligned(1024))) char smem[];
 
@@ -88,7 +86,6 @@ __global__ __launch_bounds__(g4::kThreads) void gemm_w4_kernel(
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
-  const int l32 = lane & 31, half = lane >> 5;
 
   const int tiles_m = (M + BT - 1) / BT, tiles_n = (N + BT - 1) / BT;
   int tm, tn;
@@ -115,16 +112,6 @@ __global__ __launch_bounds__(g4::kThreads) void gemm_w4_kernel(
   }
   TA::dma_adv(da, lda_b);
   TB::dma_adv(db, ldb_b);
-  // The DMA of a stage goes out in kParts parts, one in each of the first
-  // kParts k-steps of an iteration; part p covers blocks
-  // [p kBlocks / kParts, (p+1) kBlocks / kParts).  With three or more slots
-  // every k-step issues a part.  With two, the stage being loaded is the
-  // very next one, so only the first half of the k-steps issue DMA and the
-  // loads issued last still have two k-steps of MFMAs to land (spreading
-  // over one, two or three k-steps measured within 4% of each other).
-  constexpr int kParts = FRISK_G4_PARTS > 0 ? (FRISK_G4_PARTS < kSteps ? FRISK_G4_PARTS : kSteps)
-                         : (S >= 3 ? kSteps : (kSteps >= 2 ? kSteps / 2 : 1));
-  static_assert(kBlocks >= kParts, "DMA parts");
   // Workgroups start their K walk at a per-XCD offset: stage kt of the loop
   // holds K stage (kt + krot) mod nk.  The workgroups of one XCD share A and
   // B rows through that XCD's L2 and keep one offset, so the sharing is
@@ -133,40 +120,61 @@ __global__ __launch_bounds__(g4::kThreads) void gemm_w4_kernel(
   // Loop stages past the last one stay past it and read nothing.
   const int nk_all = (Kb + KR - 1) / KR;
   const int krot = __builtin_amdgcn_readfirstlane((int)(blockIdx.x % 8) * nk_all / 8);
-  auto issue_part = [&](int stage, int slot, auto part) {
-    constexpr int p = decltype(part)::value;
+  auto phys_of = [&](int stage) {
     int phys = stage + krot;
     if (phys >= nk_all) phys -= nk_all;
-    if (stage >= nk_all) phys = stage;
-    char* dst = smem + slot * kStageBytes + wave * kBlocks * 1024;
+    return stage >= nk_all ? stage : phys;
+  };
+  // The DMA of one operand tile goes out in parts, one per k-step: B in
+  // kBParts parts over the first k-steps of an iteration, A in kAParts parts
+  // over the rest (both in the one k-step of a single-step stage).  Part p
+  // of P covers blocks [p kBlocks / P, (p+1) kBlocks / P).
+  constexpr int kBParts = kSteps >= 2 ? kSteps / 2 : 1;
+  constexpr int kAParts = kSteps >= 2 ? kSteps - kBParts : 1;
+  static_assert(kBlocks >= kBParts && kBlocks >= kAParts, "DMA parts");
+  auto issue = [&](auto op, int stage, int slot, auto part, auto parts) {
+    constexpr int p = decltype(part)::value, np = decltype(parts)::value;
+    constexpr bool is_a = decltype(op)::value;
+    const int phys = phys_of(stage);
+    char* dst = smem + slot * kTileBytes + wave * kBlocks * 1024;
 #pragma unroll
-    for (int i = p * kBlocks / kParts; i < (p + 1) * kBlocks / kParts; ++i) {
-      uint32_t oa = TA::offset(da, i, phys);
-      uint32_t ob = TB::offset(db, i, phys);
-      // Keep the selects as selects: otherwise the backend may turn them
-      // into branches around two copies of each load.
-      asm("" : "+v"(oa));
-      asm("" : "+v"(ob));
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (lds_ptr_t)(dst + i * 1024), 16, oa, 0, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsb, (lds_ptr_t)(dst + kTileBytes + i * 1024), 16, ob,
-                                               0, 0, 0);
+    for (int i = p * kBlocks / np; i < (p + 1) * kBlocks / np; ++i) {
+      uint32_t o = is_a ? TA::offset(da, i, phys) : TB::offset(db, i, phys);
+      // Keep the select a select: otherwise the backend may turn it into a
+      // branch around two copies of the load.
+      asm("" : "+v"(o));
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(is_a ? rsa : rsb, (lds_ptr_t)(dst + i * 1024), 16,
+                                               o, 0, 0, 0);
     }
+  };
+  using OpA = std::true_type;
+  using OpB = std::false_type;
+  // Loads issued by k-step s of an iteration.
+  auto step_loads = [](int s) {
+    if (kSteps == 1) return 2 * kBlocks;
+    if (s < kBParts) return (s + 1) * kBlocks / kBParts - s * kBlocks / kBParts;
+    const int p = s - kBParts;
+    return (p + 1) * kBlocks / kAParts - p * kBlocks / kAParts;
   };
 
   // ---- fragment reads -----------------------------------------------------
-  typename TA::Frag fa[TM];
-  typename TB::Frag fb[TN];
+  // K-major operands share one Frag (tile 0's) across their tiles.
+  typename TA::Frag fa[TA::kSharedFrag ? 1 : TM];
+  typename TB::Frag fb[TB::kSharedFrag ? 1 : TN];
 #pragma unroll
-  for (int t = 0; t < TM; ++t) fa[t] = TA::frag(wm * (32 * TM) + t * 32, lane);
+  for (int t = 0; t < (TA::kSharedFrag ? 1 : TM); ++t) fa[t] = TA::frag(wm * 128 + t * ATOM, lane);
 #pragma unroll
-  for (int t = 0; t < TN; ++t) fb[t] = TB::frag(wn * (32 * TN) + t * 32, lane);
+  for (int t = 0; t < (TB::kSharedFrag ? 1 : TN); ++t) fb[t] = TB::frag(wn * 128 + t * ATOM, lane);
   using Frag = Frags<TM, TN, kLaneChunks>;
-  auto load_frags = [&](int slot, int s, Frag& f) {
-    const char* base = smem + slot * kStageBytes;
+  auto load_frags = [&](int aslot, int bslot, int s, Frag& f) {
+    const char* abase = smem + aslot * kTileBytes;
+    const char* bbase = smem + bslot * kTileBytes;
 #pragma unroll
-    for (int t = 0; t < TM; ++t) TA::read(base, fa[t], s, f.a[t]);
+    for (int t = 0; t < TM; ++t)
+      TA::read(abase, fa[TA::kSharedFrag ? 0 : t], s, f.a[t], TA::tile_off(t * ATOM));
 #pragma unroll
-    for (int t = 0; t < TN; ++t) TB::read(base + kTileBytes, fb[t], s, f.b[t]);
+    for (int t = 0; t < TN; ++t)
+      TB::read(bbase, fb[TB::kSharedFrag ? 0 : t], s, f.b[t], TB::tile_off(t * ATOM));
   };
 
   Acc acc[TM][TN];
@@ -182,84 +190,88 @@ __global__ __launch_bounds__(g4::kThreads) void gemm_w4_kernel(
   };
 
   // ---- pipeline -----------------------------------------------------------
-  // Stage kt lives in slot kt % S.  In the last k-step of stage kt, after
-  // half of its MFMAs, each wave waits for its own loads of stage kt+1 and
-  // for its LDS reads; a workgroup barrier then publishes stage kt+1 and
-  // proves that every wave is done with slot kt % S.  That slot receives
-  // stage kt+S, whose DMA is spread over the first kParts k-steps of
-  // iteration kt+1.  Stage kt+1 is issued during iteration kt+2-S and S-2
-  // newer stages may be in flight at the wait.  Every iteration issues
-  // exactly kLoads loads (past the last stage they are zero-reads without
-  // memory traffic), so the vmcnt bookkeeping is static.
+  // LDS ring of five operand-tile slots: tile t (A of stage t/2 when t is
+  // even, B of stage (t-1)/2 when odd) lives in slot t % 5.  Iteration kt
+  // reads A(kt) and B(kt) and issues B(kt+1), then A(kt+2); their slots
+  // held A(kt-1) and B(kt-1), which every wave finished reading before the
+  // barrier that ended iteration kt-1.  In the last k-step, after half of
+  // its MFMAs, each wave waits for its LDS reads and for all but its newest
+  // kBlocks loads (A(kt+2)), which leaves A(kt+1) (issued an iteration
+  // earlier) and B(kt+1) landed; the workgroup barrier then publishes them.
+  // Every k-step issues DMA, so no k-step carries a burst of issues, and
+  // every iteration issues the same loads (past the last stage they are
+  // zero-reads without memory traffic), so the vmcnt bookkeeping is static.
+  // Measured against two 64 KiB stages written whole per iteration
+  // (4096^3 bf16 / 4096x8192x8192 fp8 / 8192^3 bf16): +2% / +7% / +4%.
   const int nk = (Kb + KR - 1) / KR;
-#pragma unroll
-  for (int st = 0; st < S - 1; ++st)
-    static_for<0, kParts>([&](auto p) { issue_part(st, st, p); });
-  FRISK_WAIT_VMCNT(kLoads * (S - 2));
+  static_for<0, kAParts>([&](auto p) { issue(OpA{}, 0, 0, p, std::integral_constant<int, kAParts>{}); });
+  static_for<0, kBParts>([&](auto p) { issue(OpB{}, 0, 1, p, std::integral_constant<int, kBParts>{}); });
+  static_for<0, kAParts>([&](auto p) { issue(OpA{}, 1, 2, p, std::integral_constant<int, kAParts>{}); });
+  FRISK_WAIT_VMCNT(kBlocks);
   __builtin_amdgcn_s_barrier();
 
   Frag fr[2];
-  load_frags(0, 0, fr[0]);
+  load_frags(0, 1, 0, fr[0]);
   // Drain every LGKM operation issued so far (these fragment reads and the
   // scalar loads of the epilogue's kernel arguments): with scalar loads
   // pending at the loop entry the LGKM counter is unordered, and the
   // compiler would then wait for lgkmcnt(0) at the top of every iteration.
   __builtin_amdgcn_s_waitcnt(0xC07F);
-  int slot = 0, fslot = S - 1;  // slots of stage kt and of stage kt+S-1
+  int a_rd = 0, b_rd = 1, b_wr = 3, a_wr = 4;  // slots of A(kt), B(kt), B(kt+1), A(kt+2)
+  auto adv = [](int x) { return x >= 3 ? x - 3 : x + 2; };  // (x + 2) mod 5
   constexpr int kMf = TM * TN;
   constexpr int kHalf = kMf / 2;
   for (int kt = 0; kt < nk; ++kt) {
     static_for<0, kSteps>([&](auto step) {
       constexpr int s = decltype(step)::value;
       constexpr int cur = s & 1, nxt = cur ^ 1;
-      constexpr bool dma = s < kParts;
-      constexpr int nload = dma ? 2 * ((s + 1) * kBlocks / kParts - s * kBlocks / kParts) : 0;
+      constexpr int nload = step_loads(s);
+      auto issue_step = [&]() {
+        if constexpr (kSteps == 1) {
+          issue(OpB{}, kt + 1, b_wr, std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{});
+          issue(OpA{}, kt + 2, a_wr, std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{});
+        } else if constexpr (s < kBParts) {
+          issue(OpB{}, kt + 1, b_wr, std::integral_constant<int, s>{},
+                std::integral_constant<int, kBParts>{});
+        } else {
+          issue(OpA{}, kt + 2, a_wr, std::integral_constant<int, s - kBParts>{},
+                std::integral_constant<int, kAParts>{});
+        }
+      };
       if constexpr (s + 1 < kSteps) {
         // Program order: fragment reads, then DMA (the compiler keeps LDS
         // reads and LDS-DMA writes in order, as it cannot tell slots apart).
-        load_frags(slot, s + 1, fr[nxt]);
-        if constexpr (dma) issue_part(kt + S - 1, fslot, step);
+        // Fragment reads go under the first half of the MFMAs, DMA under
+        // the second half.
+        load_frags(a_rd, b_rd, s + 1, fr[nxt]);
+        issue_step();
         mfma_rows(fr[cur], 0, TM);
-        if constexpr (dma) {
-          // Fragment reads under the first half of the MFMAs, DMA under the
-          // second half.
-          constexpr int kDsG = kFragReads < kHalf ? kFragReads : kHalf;
-          constexpr int kDsPer = (kFragReads + kDsG - 1) / kDsG;
-          constexpr int kVmPer = (nload + (kMf - kDsG) - 1) / (kMf - kDsG);
-          static_for<0, kDsG>([&](auto) {
-            __builtin_amdgcn_sched_group_barrier(0x100, kDsPer, 0);  // DS read
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);       // MFMA
-          });
-          static_for<0, (nload + kVmPer - 1) / kVmPer>([&](auto) {
-            __builtin_amdgcn_sched_group_barrier(0x010, kVmPer, 0);  // VMEM (LDS-DMA)
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);       // MFMA
-          });
-        } else {
-          static_for<0, kFragReads>([&](auto) {
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-          });
-        }
+        constexpr int kDsG = kFragReads < kHalf ? kFragReads : kHalf;
+        constexpr int kDsPer = (kFragReads + kDsG - 1) / kDsG;
+        constexpr int kVmPer = (nload + (kMf - kDsG) - 1) / (kMf - kDsG);
+        static_for<0, kDsG>([&](auto) {
+          __builtin_amdgcn_sched_group_barrier(0x100, kDsPer, 0);  // DS read
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);       // MFMA
+        });
+        static_for<0, (nload + kVmPer - 1) / kVmPer>([&](auto) {
+          __builtin_amdgcn_sched_group_barrier(0x010, kVmPer, 0);  // VMEM (LDS-DMA)
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);       // MFMA
+        });
         __builtin_amdgcn_sched_barrier(0);
       } else {
-        if constexpr (dma) {
-          issue_part(kt + S - 1, fslot, step);
-          mfma_rows(fr[cur], 0, TM / 2);
-          constexpr int kVmPer = (nload + kHalf - 1) / kHalf;
-          static_for<0, (nload + kVmPer - 1) / kVmPer>([&](auto) {
-            __builtin_amdgcn_sched_group_barrier(0x010, kVmPer, 0);  // VMEM (LDS-DMA)
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);       // MFMA
-          });
-        } else {
-          mfma_rows(fr[cur], 0, TM / 2);
-        }
+        issue_step();
+        mfma_rows(fr[cur], 0, TM / 2);
+        constexpr int kVmPer = (nload + kHalf - 1) / kHalf;
+        static_for<0, (nload + kVmPer - 1) / kVmPer>([&](auto) {
+          __builtin_amdgcn_sched_group_barrier(0x010, kVmPer, 0);  // VMEM (LDS-DMA)
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);       // MFMA
+        });
         __builtin_amdgcn_sched_barrier(0);
-        // vmcnt <= kLoads (S-2) and lgkmcnt = 0.
-        __builtin_amdgcn_s_waitcnt((((kLoads * (S - 2)) & 15) | (((kLoads * (S - 2)) >> 4) << 14) |
-                                    (7 << 4)));
+        // vmcnt <= kBlocks (this wave's A(kt+2) loads) and lgkmcnt = 0.
+        __builtin_amdgcn_s_waitcnt(((kBlocks & 15) | ((kBlocks >> 4) << 14) | (7 << 4)));
         __builtin_amdgcn_s_barrier();
-        const int nslot = slot + 1 == S ? 0 : slot + 1;
-        load_frags(nslot, 0, fr[kSteps & 1 ? nxt : 0]);
+        const int na = adv(a_rd), nb = adv(b_rd);
+        load_frags(na, nb, 0, fr[kSteps & 1 ? nxt : 0]);
         mfma_rows(fr[cur], TM / 2, TM);
         constexpr int kDsPer = (kFragReads + kHalf - 1) / kHalf;
         static_for<0, kHalf>([&](auto) {
@@ -267,8 +279,10 @@ __global__ __launch_bounds__(g4::kThreads) void gemm_w4_kernel(
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);       // MFMA
         });
         __builtin_amdgcn_sched_barrier(0);
-        fslot = slot;
-        slot = nslot;
+        a_rd = na;
+        b_rd = nb;
+        b_wr = adv(b_wr);
+        a_wr = adv(a_wr);
       }
     });
     if constexpr (kSteps == 1) fr[0] = fr[1];
@@ -277,30 +291,28 @@ __global__ __launch_bounds__(g4::kThreads) void gemm_w4_kernel(
   FRISK_WAIT_VMCNT(0);
   __syncthreads();
 
-  // Epilogue: per wave, stage a 32 x 128 slice (one accumulator row block)
-  // as 32-bit values, then each lane stores 8 consecutive columns.  The
-  // 32x32 accumulator holds D[8*(r/4) + 4*(lane/32) + r%4][lane%32] in
-  // element r.
-  constexpr int kPitch = 32 * TN + 4;
-  static_assert(4 * 32 * kPitch * 4 <= g4::lds_bytes(KR, S), "epilogue staging fits in LDS");
-  AccS* stage = (AccS*)(smem + wave * (32 * kPitch * 4));
-  constexpr int kGroups = 32 * TN / 8;  // 8-column groups per staged row
+  // Epilogue: per wave, stage an ATOM x 128 slice (one accumulator row
+  // block) as 32-bit values, then each lane stores 8 consecutive columns
+  // (the ragged last group of a row one element at a time).  Accumulator
+  // element r of lane L holds output (Op::acc_row(r, L), L % ATOM).
+  constexpr int kPitch = 128 + 4;
+  static_assert(4 * ATOM * kPitch * 4 <= g4::lds_bytes(KR), "epilogue staging fits in LDS");
+  AccS* stage = (AccS*)(smem + wave * (ATOM * kPitch * 4));
+  constexpr int kGroups = 128 / 8;  // 8-column groups per staged row
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
 #pragma unroll
     for (int j = 0; j < TN; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int rr = 8 * (r >> 2) + 4 * half + (r & 3);
-        stage[rr * kPitch + j * 32 + l32] = acc[i][j][r];
-      }
+      for (int r = 0; r < kAccN; ++r)
+        stage[Op::acc_row(r, lane) * kPitch + j * ATOM + lane % ATOM] = acc[i][j][r];
     __syncthreads();
 #pragma unroll
-    for (int it = 0; it < 32 * kGroups / 64; ++it) {
+    for (int it = 0; it < ATOM * kGroups / 64; ++it) {
       const int q = it * 64 + lane;
       const int rr = q / kGroups, g = q % kGroups;
-      const int gr = row0 + wm * (32 * TM) + i * 32 + rr;
-      const int gc = col0 + wn * (32 * TN) + g * 8;
+      const int gr = row0 + wm * 128 + i * ATOM + rr;
+      const int gc = col0 + wn * 128 + g * 8;
       if (gr < M && gc < N) {
         AccS v[8];
         *(i32x4*)&v[0] = *(const i32x4*)&stage[rr * kPitch + g * 8];
@@ -316,11 +328,11 @@ __global__ __launch_bounds__(g4::kThreads) void gemm_w4_kernel(
 
 template <Elt IN, Elt OUT, bool AM, bool BM>
 static hipError_t launch_w4(const GemmArgs& g, hipStream_t stream) {
-  constexpr int KR = FRISK_G4_KR, S = FRISK_G4_STAGES;
+  constexpr int KR = FRISK_G4_KR;
   constexpr int kEsz = EltInfo<IN>::bytes;
-  constexpr int kLds = g4::lds_bytes(KR, S);
+  constexpr int kLds = g4::lds_bytes(KR);
   static_assert(kLds <= 160 * 1024, "LDS budget of one CU");
-  auto kern = gemm_w4_kernel<IN, OUT, AM, BM, KR, S>;
+  auto kern = gemm_w4_kernel<IN, OUT, AM, BM, KR, FRISK_G4_ATOM>;
   // Thread-safe one-time opt-in to more than 64 KiB of dynamic LDS.
   static const hipError_t attr =
       hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
@@ -338,10 +350,10 @@ static hipError_t launch_w4(const GemmArgs& g, hipStream_t stream) {
 template <Elt IN, bool AM, bool BM>
 static hipError_t launch_w4_split(const GemmArgs& g, int slices, int64_t kb_slice, float* partial,
                                   hipStream_t stream) {
-  constexpr int KR = FRISK_G4_KR, S = FRISK_G4_STAGES;
+  constexpr int KR = FRISK_G4_KR;
   constexpr int kEsz = EltInfo<IN>::bytes;
-  constexpr int kLds = g4::lds_bytes(KR, S);
-  auto kern = gemm_w4_kernel<IN, Elt::F32, AM, BM, KR, S>;
+  constexpr int kLds = g4::lds_bytes(KR);
+  auto kern = gemm_w4_kernel<IN, Elt::F32, AM, BM, KR, FRISK_G4_ATOM>;
   static const hipError_t attr =
       hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
   if (attr != hipSuccess) return attr;
