@@ -52,12 +52,18 @@ __device__ __host__ inline float e4m3_to_f32(uint8_t x) {
   return s ? -mag : mag;
 }
 
-// Round-to-nearest-even f32 -> bf16 bit pattern (NaN stays a quiet NaN).
-__device__ inline uint16_t f32_to_bf16_bits(float f) {
-  uint32_t u = __builtin_bit_cast(uint32_t, f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
+// Round-to-nearest-even f32 -> bf16 bit pattern (NaN stays a quiet NaN):
+// gfx950's v_cvt_pk_bf16_f32.  (Written out in integer arithmetic, the NaN
+// test compiled to exec-masked branches around every conversion, which made
+// the GEMM epilogue a sixth of the 4096^3 kernel.)
+__device__ inline uint16_t f32_to_bf16_bits(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
+
+// Two f32 values as one packed pair of bf16 (lo in bits 0-15), one
+// v_cvt_pk_bf16_f32.
+__device__ inline uint32_t f32x2_to_bf16x2_bits(float lo, float hi) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
 }
 
 __device__ inline float bf16_bits_to_f32(uint16_t b) {

@@ -123,6 +123,13 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
+// Stores 8 consecutive outputs (scaled, optionally added to what C holds)
+// at C[idx ..].  16-bit outputs go out as one nontemporal 16 B store per
+// lane, whole 128-byte lines per 8 lanes: with every tile's epilogue landing
+// at once, streaming them past the caches measured 2-3% faster end to end
+// (bf16 4096^3, 8192^3).  32-bit outputs take two 16 B stores per lane,
+// each covering half of every 32-byte sector; as nontemporal stores those
+// cost a quarter of the int8 4096^3 throughput, so they stay ordinary.
 template <Elt OUT, typename AccS>
 __device__ inline void store8(void* c, int64_t idx, const AccS* v, bool accumulate, float scale) {
   if constexpr (OUT == Elt::I32) {
@@ -159,13 +166,18 @@ __device__ inline void store8(void* c, int64_t idx, const AccS* v, bool accumula
         else f[i] += (float)__builtin_bit_cast(_Float16, o[i]);
       }
     }
-    uint16_t r[8];
+    i32x4 r;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      if constexpr (OUT == Elt::BF16) r[i] = f32_to_bf16_bits(f[i]);
-      else r[i] = __builtin_bit_cast(uint16_t, (_Float16)f[i]);
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (OUT == Elt::BF16) {
+        r[i] = (int)f32x2_to_bf16x2_bits(f[2 * i], f[2 * i + 1]);
+      } else {
+        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+        const h2 h = {(_Float16)f[2 * i], (_Float16)f[2 * i + 1]};
+        r[i] = __builtin_bit_cast(int, h);
+      }
     }
-    *(i32x4*)p = *(const i32x4*)r;
+    __builtin_nontemporal_store(r, (i32x4*)p);
   }
 }
 
