@@ -123,6 +123,20 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
+// Two f32 values as a packed pair of 16-bit outputs (lo in bits 0-15): one
+// v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32, round to nearest even.
+template <Elt OUT>
+__device__ inline uint32_t pack_f32x2(float lo, float hi) {
+  static_assert(OUT == Elt::BF16 || OUT == Elt::F16, "16-bit output");
+  if constexpr (OUT == Elt::BF16) {
+    return f32x2_to_bf16x2_bits(lo, hi);
+  } else {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const h2 h = {(_Float16)lo, (_Float16)hi};
+    return __builtin_bit_cast(uint32_t, h);
+  }
+}
+
 // Stores 8 consecutive outputs (scaled, optionally added to what C holds)
 // at C[idx ..].  16-bit outputs go out as one nontemporal 16 B store per
 // lane, whole 128-byte lines per 8 lanes: with every tile's epilogue landing
@@ -168,16 +182,39 @@ __device__ inline void store8(void* c, int64_t idx, const AccS* v, bool accumula
     }
     i32x4 r;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if constexpr (OUT == Elt::BF16) {
-        r[i] = (int)f32x2_to_bf16x2_bits(f[2 * i], f[2 * i + 1]);
-      } else {
-        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-        const h2 h = {(_Float16)f[2 * i], (_Float16)f[2 * i + 1]};
-        r[i] = __builtin_bit_cast(int, h);
-      }
-    }
+    for (int i = 0; i < 4; ++i) r[i] = (int)pack_f32x2<OUT>(f[2 * i], f[2 * i + 1]);
     __builtin_nontemporal_store(r, (i32x4*)p);
+  }
+}
+
+// Stores 4 consecutive outputs (scaled, optionally added to what C holds)
+// at C[idx ..]: one 16-byte store of a 32-bit output, one 8-byte store of a
+// 16-bit one.
+template <Elt OUT, typename AccS>
+__device__ inline void store4(void* c, int64_t idx, const AccS* v, bool accumulate, float scale) {
+  if constexpr (OUT == Elt::I32) {
+    int32_t* p = (int32_t*)c + idx;
+    i32x4 r = {(int)v[0], (int)v[1], (int)v[2], (int)v[3]};
+    if (accumulate) r += *(const i32x4*)p;
+    *(i32x4*)p = r;
+  } else if constexpr (OUT == Elt::F32) {
+    float* p = (float*)c + idx;
+    f32x4 r = {v[0] * scale, v[1] * scale, v[2] * scale, v[3] * scale};
+    if (accumulate) r += *(const f32x4*)p;
+    *(f32x4*)p = r;
+  } else {
+    uint16_t* p = (uint16_t*)c + idx;
+    float f[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) f[i] = v[i] * scale;
+    if (accumulate) {
+      const i32x2 old = *(const i32x2*)p;
+      const uint16_t* o = (const uint16_t*)&old;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) f[i] += load_as_f32<OUT>(o, i);
+    }
+    const i32x2 r = {(int)pack_f32x2<OUT>(f[0], f[1]), (int)pack_f32x2<OUT>(f[2], f[3])};
+    *(i32x2*)p = r;
   }
 }
 

@@ -186,7 +186,7 @@ __global__ __launch_bounds__(g4::kThreads) void gemm_w4_kernel(
 #pragma unroll
     for (int i = i0; i < i1; ++i)
 #pragma unroll
-      for (int j = 0; j < TN; ++j) acc[i][j] = Op::run(f.a[i], f.b[j], acc[i][j]);
+      for (int j = 0; j < TN; ++j) acc[i][j] = Op::run(f.b[j], f.a[i], acc[i][j]);
   };
 
   // ---- pipeline -----------------------------------------------------------
@@ -291,37 +291,70 @@ __global__ __launch_bounds__(g4::kThreads) void gemm_w4_kernel(
   FRISK_WAIT_VMCNT(0);
   __syncthreads();
 
-  // Epilogue: per wave, stage an ATOM x 128 slice (one accumulator row
-  // block) as 32-bit values, then each lane stores 8 consecutive columns
-  // (the ragged last group of a row one element at a time).  Accumulator
-  // element r of lane L holds output (Op::acc_row(r, L), L % ATOM).
-  constexpr int kPitch = 128 + 4;
-  static_assert(4 * ATOM * kPitch * 4 <= g4::lds_bytes(KR), "epilogue staging fits in LDS");
-  AccS* stage = (AccS*)(smem + wave * (ATOM * kPitch * 4));
-  constexpr int kGroups = 128 / 8;  // 8-column groups per staged row
+  // Epilogue.  The MFMAs take the B fragment as their first operand, so
+  // accumulator element r of lane L in atom (i, j) is output row
+  // i ATOM + L % ATOM, column j ATOM + Op::acc_row(r, L) of the wave's
+  // 128x128 sub-tile, and elements 4q .. 4q+3 are four consecutive columns.
+  // Each wave stages half of its sub-tile at a time in LDS by rows, one
+  // 16-byte write of four accumulators straight from the AGPRs per column
+  // group, then stores row pieces, consecutive lanes on consecutive pieces:
+  // 8 outputs (16 bytes) per lane for 16-bit outputs through store8, 4 (16
+  // bytes) for 32-bit ones through store4; both scale, accumulate and
+  // convert.  Staged row R keeps 16-byte chunk c at c ^ (R & 15) ^ (c >> 4):
+  // the writes of 16 lanes (16 rows, one column group) and each read of 16
+  // lanes (one row; chunks 2g or 2g+1, or g) touch every bank once.
+  {
+    constexpr int kOut = EltInfo<OUT>::bytes == 2 ? 8 : 4;  // outputs per lane per store
+    constexpr int kPPR = 128 / kOut;         // pieces per staged row
+    constexpr int kPassTM = TM / 2;          // atom rows per pass
+    constexpr int kRows = kPassTM * ATOM;
+    constexpr int kPitch = 128 * 4;
+    static_assert(4 * kRows * kPitch <= g4::lds_bytes(KR), "epilogue staging fits in LDS");
+    static_assert(kRows * kPPR % 64 == 0, "whole store rounds");
+    char* stage = smem + wave * (kRows * kPitch);
+    auto chunk_at = [](int R, int c) { return R * kPitch + ((c ^ (R & 15) ^ (c >> 4)) << 4); };
 #pragma unroll
-  for (int i = 0; i < TM; ++i) {
+    for (int ps = 0; ps < TM / kPassTM; ++ps) {
 #pragma unroll
-    for (int j = 0; j < TN; ++j)
+      for (int ii = 0; ii < kPassTM; ++ii) {
+        const int i = ps * kPassTM + ii;
 #pragma unroll
-      for (int r = 0; r < kAccN; ++r)
-        stage[Op::acc_row(r, lane) * kPitch + j * ATOM + lane % ATOM] = acc[i][j][r];
-    __syncthreads();
-#pragma unroll
-    for (int it = 0; it < ATOM * kGroups / 64; ++it) {
-      const int q = it * 64 + lane;
-      const int rr = q / kGroups, g = q % kGroups;
-      const int gr = row0 + wm * 128 + i * ATOM + rr;
-      const int gc = col0 + wn * 128 + g * 8;
-      if (gr < M && gc < N) {
-        AccS v[8];
-        *(i32x4*)&v[0] = *(const i32x4*)&stage[rr * kPitch + g * 8];
-        *(i32x4*)&v[4] = *(const i32x4*)&stage[rr * kPitch + g * 8 + 4];
-        if (gc + 8 <= N) store8<OUT>(C, (int64_t)gr * ldc + gc, v, accumulate != 0, scale);
-        else store_n<OUT>(C, (int64_t)gr * ldc + gc, v, N - gc, accumulate != 0, scale);
+        for (int j = 0; j < TN; ++j)
+          static_for<0, kAccN / 4>([&](auto qc) {
+            constexpr int q = decltype(qc)::value;
+            const int R = ii * ATOM + lane % ATOM;
+            const int col = j * ATOM + Op::acc_row(4 * q, lane);
+            // Elements 4q .. 4q+3 as one 4-vector, a subregister of the
+            // accumulator tuple.  (Assembled element by element, the
+            // backend copied element 4q into all four lanes of the vector.)
+            const auto a4 = __builtin_shufflevector(acc[i][j], acc[i][j], 4 * q, 4 * q + 1, 4 * q + 2,
+                                                    4 * q + 3);
+            *(i32x4*)(stage + chunk_at(R, col / 4)) = __builtin_bit_cast(i32x4, a4);
+          });
       }
+      __syncthreads();
+#pragma unroll
+      for (int it = 0; it < kRows * kPPR / 64; ++it) {
+        const int qq = it * 64 + lane;
+        const int rr = qq / kPPR, g = qq % kPPR;
+        const int gr = row0 + wm * 128 + ps * kRows + rr;
+        const int gc = col0 + wn * 128 + g * kOut;
+        AccS e[kOut];
+#pragma unroll
+        for (int h = 0; h < kOut / 4; ++h)
+          *(i32x4*)&e[4 * h] = *(const i32x4*)(stage + chunk_at(rr, g * (kOut / 4) + h));
+        if (gr < M && gc < N) {
+          const int64_t idx = (int64_t)gr * ldc + gc;
+          if (gc + kOut <= N) {
+            if constexpr (kOut == 8) store8<OUT>(C, idx, e, accumulate != 0, scale);
+            else store4<OUT>(C, idx, e, accumulate != 0, scale);
+          } else {
+            store_n<OUT>(C, idx, e, N - gc, accumulate != 0, scale);
+          }
+        }
+      }
+      __syncthreads();
     }
-    __syncthreads();
   }
 #endif  // __HIP_DEVICE_COMPILE__
 }
