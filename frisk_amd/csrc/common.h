@@ -6,6 +6,7 @@
 #include <stdint.h>
 
 #include <atomic>
+#include <type_traits>
 
 namespace frisk {
 
@@ -51,6 +52,16 @@ __device__ __host__ inline float e4m3_to_f32(uint8_t x) {
     mag = __builtin_ldexpf(1.0f + (float)m * 0.125f, (int)e - 7);
   }
   return s ? -mag : mag;
+}
+
+// Calls f(std::integral_constant<int, i>) for i = I .. N-1, so that the body
+// can use i in constant expressions (builtin arguments, array bounds).
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
+  }
 }
 
 // Round-to-nearest-even f32 -> bf16 bit pattern (NaN stays a quiet NaN):

@@ -113,16 +113,6 @@ template <Elt E> struct MfmaAtom<E, 16> : Mfma16x<E> {
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-// Calls f(std::integral_constant<int, i>) for i = I .. N-1, so that the body
-// can use i in constant expressions (builtin arguments, array bounds).
-template <int I, int N, typename F>
-__device__ __forceinline__ void static_for(F&& f) {
-  if constexpr (I < N) {
-    f(std::integral_constant<int, I>{});
-    static_for<I + 1, N>(f);
-  }
-}
-
 // Two f32 values as a packed pair of 16-bit outputs (lo in bits 0-15): one
 // v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32, round to nearest even.
 template <Elt OUT>
