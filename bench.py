@@ -38,6 +38,7 @@ sys.path.insert(0, str(ROOT))
 PEAK = {"bf16": 2500.0, "f16": 2500.0, "fp8": 5000.0, "int8": 5000.0}  # dense TFLOP/s (TOP/s)
 REF_FIXED_TILE_US = {"single": 21.584, "graph": 6.5386}  # the reference's published H100 figures
 HBM_PEAK_GBS = 8000.0
+PEAK_MHZ = 2400.0  # shader clock of the published MFMA peaks
 SETTLE_S = 0.25  # untimed load before each workload's warm-up, see time_launches
 
 
@@ -206,6 +207,75 @@ def launch_percentiles(torch, fn, n=50):
     return {"p10": round(pick(0.1), 6), "p50": round(pick(0.5), 6), "p90": round(pick(0.9), 6)}
 
 
+def _sclk_paths():
+    import glob
+    return sorted(glob.glob("/sys/class/drm/card*/device/pp_dpm_sclk"))
+
+
+def read_sclk_mhz():
+    """Current shader clock from the amdgpu driver's DPM table (the level
+    marked '*'), or None where the file is not readable."""
+    for path in _sclk_paths():
+        try:
+            for line in open(path).read().splitlines():
+                if line.rstrip().endswith("*"):
+                    return int(line.split(":")[1].strip().lower().split("mhz")[0])
+        except (OSError, ValueError, IndexError):
+            continue
+    return None
+
+
+def sustained_clock(torch, fn, seconds=0.4):
+    """Median shader clock (MHz) sampled every 20 ms while fn runs back to
+    back for `seconds` (the clock a sustained workload sees; MI355X's
+    published peaks are quoted at 2400 MHz)."""
+    import threading
+    samples, stop = [], threading.Event()
+
+    def sample():
+        while not stop.is_set():
+            v = read_sclk_mhz()
+            if v is not None:
+                samples.append(v)
+            time.sleep(0.02)
+
+    th = threading.Thread(target=sample, daemon=True)
+    th.start()
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(8):
+            fn()
+        torch.cuda.synchronize()
+    stop.set()
+    th.join()
+    if not samples:
+        return None
+    samples.sort()
+    return samples[len(samples) // 2]
+
+
+def provenance(torch):
+    """What was measured: hashes of the kernel sources and of the built
+    library, the git commit recorded at build time, and the GPU."""
+    import hashlib
+    from frisk_amd.build import source_digest
+    lib = ROOT / "frisk_amd" / "libfrisk_hip.so"
+    info = {}
+    bi = ROOT / "frisk_amd" / "BUILD_INFO.json"
+    if bi.exists():
+        info = json.loads(bi.read_text())
+    props = torch.cuda.get_device_properties(0)
+    gpu = {"name": props.name, "arch": getattr(props, "gcnArchName", None),
+           "cus": props.multi_processor_count, "mem_gib": round(props.total_memory / 2 ** 30, 1)}
+    uuid = getattr(props, "uuid", None)
+    if uuid is not None:
+        gpu["uuid"] = str(uuid)
+    return {"source_sha256_16": source_digest(),
+            "library_sha256_16": hashlib.sha256(lib.read_bytes()).hexdigest()[:16] if lib.exists() else None,
+            "git_commit": info.get("git_commit"), "built_source_sha256_16": info.get("source_sha256_16"),
+            "gpu": gpu, "torch": torch.__version__, "hip": torch.version.hip}
+
+
 def projection_sweep(torch, rt, steps, warmup, settle_s):
     """configs[2]: Y[M, N] = X[M, K] . W[N, K]^T in bf16 for (N, K) in
     {(4096, 4096), (14336, 4096), (4096, 14336)} and M in {16, 128, 1024,
@@ -307,12 +377,28 @@ def fixed_tile_latency(torch, rt):
                                      "graph": round(REF_FIXED_TILE_US["graph"] / replays[len(replays) // 2], 2)}}
 
 
+def _repeat(fn, min_seconds, max_reps):
+    """Runs fn until min_seconds of wall time have passed (at most max_reps
+    times); returns (repetitions, seconds)."""
+    reps = 0
+    t0 = time.perf_counter()
+    while reps < max_reps:
+        fn()
+        reps += 1
+        if time.perf_counter() - t0 >= min_seconds:
+            break
+    return reps, time.perf_counter() - t0
+
+
 def cpu_baseline(torch, min_seconds=10.0, max_passes=8):
-    """fp64 C oracle (oracle/oracle.c) on a bounded sample of the headline
-    workload: the bf16 4096^3 GEMM (inputs decoded exactly from bf16) in
-    blocks of 512 output rows, whole passes over the 4096 rows repeated until
-    at least `min_seconds` of wall time (at most `max_passes`), on all CPU
-    threads of this process."""
+    """fp64 C oracle (oracle/oracle.c) on bounded samples of the headline
+    workloads, on this host's cores.  Top level: the bf16 4096^3 GEMM
+    (inputs decoded exactly from bf16) in blocks of 512 output rows, whole
+    passes over the 4096 rows repeated until at least `min_seconds` of wall
+    time (at most `max_passes`), on all CPU threads of this process.  `legs`:
+    the same GEMM on one core (64 output rows), and the attention forward of
+    configs[4] (b4 h32 s4096 d128) for 128 query rows of one head on all
+    threads and 16 rows on one core (4 * rows * s * d FLOPs: QK^T and PV)."""
     import numpy as np
     from oracle import native
     native.load()
@@ -323,19 +409,37 @@ def cpu_baseline(torch, min_seconds=10.0, max_passes=8):
     a = torch.randn(m, k, generator=g).to(torch.bfloat16).double().numpy()
     b = torch.randn(n, k, generator=g).to(torch.bfloat16).double().numpy()
     native.gemm_f64(a[:8], b, trans_b=True, threads=threads)  # warm up threads
-    rows = 0
-    t0 = time.perf_counter()
-    for _ in range(max_passes):
+
+    def gemm_pass():
         for r0 in range(0, m, blk):
             native.gemm_f64(a[r0:r0 + blk], b, trans_b=True, threads=threads)
-            rows += blk
-        if time.perf_counter() - t0 >= min_seconds:
-            break
-    dt = time.perf_counter() - t0
-    return {"value": round(2.0 * rows * n * k / dt / 1e12, 6), "unit": "TFLOP/s",
-            "cores": threads, "kind": "port",
-            "sample": f"{rows // m} full pass(es) over the 4096^3 GEMM in 512-row blocks "
-                      f"(fp64 oracle/oracle.c, {dt:.1f} s wall)"}
+
+    passes, dt = _repeat(gemm_pass, min_seconds, max_passes)
+    rows = passes * m
+    out = {"value": round(2.0 * rows * n * k / dt / 1e12, 6), "unit": "TFLOP/s",
+           "cores": threads, "kind": "port",
+           "sample": f"{passes} full pass(es) over the 4096^3 GEMM in 512-row blocks "
+                     f"(fp64 oracle/oracle.c, {dt:.1f} s wall)"}
+    legs = {}
+    reps, dt = _repeat(lambda: native.gemm_f64(a[:64], b, trans_b=True, threads=1), 2.0, 50)
+    legs["gemm_bf16_4096_single_core"] = {
+        "value": round(2.0 * 64 * reps * n * k / dt / 1e12, 6), "unit": "TFLOP/s", "cores": 1,
+        "kind": "port", "sample": f"{reps} x 64 output rows of the 4096^3 GEMM ({dt:.1f} s)"}
+    s_len, d = 4096, 128
+    q = torch.randn(s_len, d, generator=g).to(torch.bfloat16).double().numpy()
+    kk = torch.randn(s_len, d, generator=g).to(torch.bfloat16).double().numpy()
+    v = torch.randn(s_len, d, generator=g).to(torch.bfloat16).double().numpy()
+    for name, nrows, nthreads, secs in (("fa_fwd_b4h32s4096d128", 128, threads, 4.0),
+                                        ("fa_fwd_b4h32s4096d128_single_core", 16, 1, 2.0)):
+        rows_idx = np.arange(0, s_len, s_len // nrows, dtype=np.int64)[:nrows]
+        reps, dt = _repeat(lambda: native.attn_rows_f64(q, kk, v, rows_idx, scale=d ** -0.5,
+                                                         threads=nthreads), secs, 100000)
+        legs[name] = {"value": round(4.0 * nrows * reps * s_len * d / dt / 1e12, 6),
+                      "unit": "TFLOP/s", "cores": nthreads, "kind": "port",
+                      "sample": f"{reps} x {nrows} query rows of one head, s=4096 d=128, "
+                                f"non-causal (fp64 oracle_attn_rows_f64, {dt:.1f} s)"}
+    out["legs"] = legs
+    return out
 
 
 def traffic_from_profile(name):
@@ -390,8 +494,11 @@ def main():
                              "traffic": traffic_from_profile(name)}
         else:
             tf = flops / ms / 1e9
+            mhz = sustained_clock(torch, fn)
             results[name] = {"dtype": label, "ms": round(ms, 6), "tflops": round(tf, 2),
                              "frac_peak": round(tf / PEAK[label], 4),
+                             "sclk_mhz": mhz,
+                             "frac_peak_at_sclk": round(tf / (PEAK[label] * mhz / PEAK_MHZ), 4) if mhz else None,
                              "launch_ms": launch_percentiles(torch, fn),
                              "traffic": traffic_from_profile(name)}
         del fn
@@ -419,7 +526,9 @@ def main():
                    "m": 4096, "n": 4096, "k": 4096, "layout": "NT"},
         "roofline": {"bound": "mfma", "achieved": head["tflops"], "peak": PEAK["bf16"],
                      "unit": "TFLOP/s", "frac": round(head["tflops"] / PEAK["bf16"], 4),
-                     "traffic": traffic},
+                     "traffic": traffic, "sclk_mhz": head["sclk_mhz"],
+                     "frac_at_sclk": head["frac_peak_at_sclk"]},
+        "provenance": provenance(torch),
         "workloads": results,
         "projection_sweep": projection_sweep(torch, rt, args.steps, args.warmup, 0.1),
         "fixed_tile_64x16": fixed_tile_latency(torch, rt),

@@ -72,7 +72,45 @@ def build(verbose: bool = False, extra: list[str] | None = None) -> Path:
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
     os.replace(tmp, LIB)
+    write_build_info()
     return LIB
+
+
+def source_digest() -> str:
+    """sha256 (first 16 hex digits) over the kernel sources and the C-ABI
+    header, in name order: the same digest bench.py reports."""
+    import hashlib
+    h = hashlib.sha256()
+    files = sorted(list(CSRC.glob("*")) + list((HERE.parent / "include").glob("*.h")))
+    for f in sorted(files, key=lambda f: f.name):
+        if f.is_file():
+            h.update(f.name.encode())
+            h.update(f.read_bytes())
+    return h.hexdigest()[:16]
+
+
+def write_build_info() -> None:
+    """frisk_amd/BUILD_INFO.json: the git commit the library was built from
+    (with a '+dirty' mark for uncommitted changes) and the source digest,
+    so that a run on a machine without the repository history can name
+    what it measured."""
+    import json
+    commit = None
+    try:
+        root = HERE.parent
+        r = subprocess.run(["git", "-C", str(root), "rev-parse", "HEAD"], capture_output=True,
+                           text=True, timeout=10)
+        if r.returncode == 0:
+            commit = r.stdout.strip()
+            d = subprocess.run(["git", "-C", str(root), "status", "--porcelain", "--",
+                                "frisk_amd/csrc", "include"], capture_output=True, text=True,
+                               timeout=10)
+            if d.returncode == 0 and d.stdout.strip():
+                commit += "+dirty"
+    except (OSError, subprocess.SubprocessError):
+        commit = None
+    (HERE / "BUILD_INFO.json").write_text(
+        json.dumps({"git_commit": commit, "source_sha256_16": source_digest()}) + "\n")
 
 
 def build_ffi(verbose: bool = False) -> Path:
