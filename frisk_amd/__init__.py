@@ -9,6 +9,8 @@ create_session.  On top of that:
 execute  -- run a GEMM / attention tile program on the GPU (C-ABI)
 execute_packet / plan_packet -- run an execution packet written by
             frisk.export_execution (after frisk.infer_layouts)
+variants -- the compiled GEMM kernel variants and the MMA contracts they
+            execute
 parse_module -- read textual tile IR (the printed form, or MLIR's generic
             operation form) back into a module; `python -m frisk_amd.opt`
             is the frisk-opt-like driver over it

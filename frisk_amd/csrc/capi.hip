@@ -212,6 +212,31 @@ int check_gemm(const frisk_gemm_desc* d, const char* fn, bool ptrs, frisk::GemmA
   if (mfma_type && nt && vec_ok && offsets_ok && frisk::gemm_skinny_supported(g)) route = GemmRoute::Skinny;
   else if (mfma_type && vec_ok && offsets_ok) route = GemmRoute::Mfma;
   else route = GemmRoute::Generic;
+
+  // A requested kernel variant: the named tile and wave grid, unsplit.
+  if (d->tile || d->wave_m || d->wave_n || d->variant_flags) {
+    const int wm = d->wave_m ? d->wave_m : 2, wn = d->wave_n ? d->wave_n : 2;
+    const bool grid_pair = (d->wave_m == 0) == (d->wave_n == 0);
+    const bool ok256 = d->tile == 256 && wm == 2 && wn == 2;
+    const bool ok128 = d->tile == 128 && ((wm == 2 && wn == 2) || (wm == 4 && wn == 1) ||
+                                          (wm == 1 && wn == 4) || (wm == 2 && wn == 1) ||
+                                          (wm == 1 && wn == 2));
+    if (d->variant_flags != 0 || !grid_pair || !(ok256 || ok128))
+      return fail(FRISK_EINVAL,
+                  "%s: no kernel variant tile=%d wave grid %dx%d (flags %d): 256 with 2x2, or 128 "
+                  "with 2x2, 4x1, 1x4, 2x1 or 1x2",
+                  fn, (int)d->tile, (int)d->wave_m, (int)d->wave_n, (int)d->variant_flags);
+    if (!(mfma_type && vec_ok && offsets_ok))
+      return fail(FRISK_EUNSUP,
+                  "%s: the %dx%d-tile variant runs on the matrix cores only: bf16/f16/e4m3/int8, "
+                  "16-byte aligned operands and row pitches, whole 16-byte pieces of K in a "
+                  "K-contiguous operand, operand reach below 2^31 bytes",
+                  fn, (int)d->tile, (int)d->tile);
+    route = GemmRoute::Mfma;
+    g.tile = d->tile;
+    g.wave_m = wm;
+    g.wave_n = wn;
+  }
   return 0;
 }
 
@@ -227,8 +252,19 @@ int64_t gemm_workspace(const frisk::GemmArgs& g, GemmRoute route) {
     if (g.m > kSkinnySplitMaxM) return frisk::gemm_split_plan(g, cus).workspace_bytes;
     return frisk::gemm_skinny_plan(g, cus, true).workspace_bytes;
   }
-  if (route == GemmRoute::Mfma) return frisk::gemm_split_plan(g, cus).workspace_bytes;
+  if (route == GemmRoute::Mfma) return g.tile ? 0 : frisk::gemm_split_plan(g, cus).workspace_bytes;
   return 0;
+}
+
+// K bytes per lane row of one MFMA atom (the atom's k times the element size).
+int atom_k_bytes(frisk::Elt in) {
+  switch (in) {
+    case frisk::Elt::BF16:
+    case frisk::Elt::F16: return 32;  // 32x32x16
+    case frisk::Elt::E4M3: return 64;  // 32x32x64
+    case frisk::Elt::I8: return 32;  // 32x32x32
+    default: return 0;
+  }
 }
 
 const char* mfma_atom(frisk::Elt in) {
@@ -305,14 +341,24 @@ int frisk_gemm_plan(const frisk_gemm_desc* d, char* buf, int64_t len) {
   } else {
     const frisk::MfmaChoice c = frisk::gemm_mfma_choice(g, cus, ws);
     const int tile = c.big ? 256 : 128;
+    const int wm = c.big || !g.tile ? 2 : g.wave_m, wn = c.big || !g.tile ? 2 : g.wave_n;
+    const int stage = c.big ? 128 : 64;
+    // The workgroup tile's instruction contract in the solver's syntax
+    // (#frisk.mma_contract): the 256x256 kernel feeds the B fragment as the
+    // MFMA's first operand (swapped), the 128x128 kernel does not.
+    const char* policy = wm == wn ? "Square" : wn == 1 ? "FullRow" : "FullCol";
     n = snprintf(buf, (size_t)len,
                  "{\"kernel\": \"%s\", \"tile_m\": %d, \"tile_n\": %d, \"atom\": \"%s\", "
-                 "\"waves\": [2, 2], \"wave_tile\": [%d, %d], \"stage_bytes\": %d, "
+                 "\"waves\": [%d, %d], \"wave_tile\": [%d, %d], \"stage_bytes\": %d, "
                  "\"a_major\": \"%s\", \"b_major\": \"%s\", \"lds_read_a\": \"%s\", "
-                 "\"lds_read_b\": \"%s\", \"slices\": %d, \"workspace_bytes\": %lld}",
-                 c.big ? "gemm_w4" : "gemm_128", tile, tile, mfma_atom(g.in), tile / 2, tile / 2,
-                 c.big ? 128 : 64, a_major, b_major, lds_read(g.trans_a), lds_read(!g.trans_b),
-                 c.slices, (long long)(c.slices > 1 ? need : 0));
+                 "\"lds_read_b\": \"%s\", \"slices\": %d, \"workspace_bytes\": %lld, "
+                 "\"requested\": %s, \"mma_contract\": \"{atom = \\\"%s\\\", wave_grid = [%d, %d], "
+                 "repeats = [%d, %d, %d], policy = \\\"%s\\\", swapped = %s}\"}",
+                 c.big ? "gemm_w4" : "gemm_128", tile, tile, mfma_atom(g.in), wm, wn, tile / wm,
+                 tile / wn, stage, a_major, b_major, lds_read(g.trans_a), lds_read(!g.trans_b),
+                 c.slices, (long long)(c.slices > 1 ? need : 0), g.tile ? "true" : "false",
+                 mfma_atom(g.in), wm, wn, tile / wm / 32, tile / wn / 32,
+                 stage / atom_k_bytes(g.in), policy, c.big ? "true" : "false");
   }
   if (n < 0 || n >= len)
     return fail(FRISK_EINVAL, "frisk_gemm_plan: buffer of %lld bytes is too small", (long long)len);

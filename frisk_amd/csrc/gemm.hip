@@ -179,6 +179,8 @@ SplitPlan gemm_split_plan(const GemmArgs& g, int cus) {
 }
 
 MfmaChoice gemm_mfma_choice(const GemmArgs& g, int cus, bool workspace) {
+  // A requested variant runs unsplit on the tile it names.
+  if (g.tile) return MfmaChoice{g.tile == 256, 1, g.k * elt_bytes(g.in)};
   const SplitPlan p = gemm_split_plan(g, cus);
   if (workspace && p.slices > 1) return MfmaChoice{p.big, p.slices, p.kb_slice};
   // 256x256 tiles (4 waves of 128x128, one workgroup per CU) when there are
@@ -201,6 +203,7 @@ hipError_t run_layout(const GemmArgs& g, hipStream_t s, const MfmaChoice& c, flo
     return gemm_128_split_layout<AM, BM>(g, c.slices, c.kb_slice, partial, s);
   }
   if (c.big) return gemm_w4_layout<AM, BM>(g, s);
+  if (g.tile == 128) return gemm_128_grid_layout<AM, BM>(g, s);
   return gemm_128_layout<AM, BM>(g, s);
 }
 
@@ -208,7 +211,7 @@ hipError_t run_layout(const GemmArgs& g, hipStream_t s, const MfmaChoice& c, flo
 
 hipError_t gemm_mfma(const GemmArgs& g, hipStream_t s, void* workspace, int64_t workspace_bytes) {
   const int cus = device_cus();
-  const bool ws = workspace && workspace_bytes >= gemm_split_plan(g, cus).workspace_bytes;
+  const bool ws = !g.tile && workspace && workspace_bytes >= gemm_split_plan(g, cus).workspace_bytes;
   const MfmaChoice c = gemm_mfma_choice(g, cus, ws);
   float* partial = c.slices > 1 ? (float*)workspace : nullptr;
   switch ((g.trans_a ? 2 : 0) | (g.trans_b ? 0 : 1)) {

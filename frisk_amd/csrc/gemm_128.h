@@ -45,7 +45,14 @@ constexpr int kRow = 64;  // bytes of K per row per stage
 constexpr int kStages = FRISK_GEMM_STAGES;
 // LDS bytes of a BT x BT tile pipeline: kStages stages of (A, B) tiles.
 constexpr int lds_bytes(int bt) { return kStages * 2 * bt * kRow; }
-static_assert(2 * lds_bytes(128) <= 160 * 1024, "two 128x128 workgroups per CU");
+// LDS bytes of one workgroup with a WM x WN wave grid: the pipeline, or the
+// epilogue's staging (each wave 32 rows of 32 TN + 4 32-bit values) when
+// that is larger (the 4x1 grid).
+constexpr int lds_bytes_grid(int bt, int wm, int wn) {
+  const int epi = wm * wn * 32 * (bt / wn + 4) * 4;
+  return lds_bytes(bt) > epi ? lds_bytes(bt) : epi;
+}
+static_assert(2 * lds_bytes_grid(128, 4, 1) <= 160 * 1024, "two 128x128 workgroups per CU");
 
 }  // namespace g128
 
@@ -79,7 +86,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_128(const char* __rest
   constexpr int kBM = BT, kBN = BT;
   constexpr int kTileBytes = BT * kRow;  // one operand, one stage
   constexpr int kStageBytes = 2 * kTileBytes;
-  constexpr int kLdsBytes = g128::lds_bytes(BT);
+  constexpr int kLdsBytes = g128::lds_bytes_grid(BT, WM, WN);
   constexpr int TM = kBM / WM / 32, TN = kBN / WN / 32;
   constexpr int kLaneChunks = TA::kLaneChunks;         // 16 B pieces per lane per MFMA
   constexpr int kSteps = kRow / Op::kBytes;            // MFMA k-steps per stage (2 or 1)
@@ -260,18 +267,18 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_128(const char* __rest
 #endif  // __HIP_DEVICE_COMPILE__
 }
 
-template <Elt IN, Elt OUT, bool AM, bool BM>
+template <Elt IN, Elt OUT, bool AM, bool BM, int WM = 2, int WN = 2>
 static hipError_t launch_128(const GemmArgs& g, hipStream_t stream) {
   constexpr int kEsz = EltInfo<IN>::bytes;
-  constexpr int kLds = g128::lds_bytes(128);
-  auto kern = gemm_mfma_128<IN, OUT, AM, BM, 128, 2, 2>;
+  constexpr int kLds = g128::lds_bytes_grid(128, WM, WN);
+  auto kern = gemm_mfma_128<IN, OUT, AM, BM, 128, WM, WN>;
   // Thread-safe one-time opt-in to more than 64 KiB of dynamic LDS.
   static const hipError_t attr =
       hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
   if (attr != hipSuccess) return attr;
   const int tiles = (int)(((g.m + 127) / 128) * ((g.n + 127) / 128));
   const int kb = (int)(g.k * kEsz);
-  hipLaunchKernelGGL(kern, dim3(tiles), dim3(256), kLds, stream, (const char*)g.a,
+  hipLaunchKernelGGL(kern, dim3(tiles), dim3(64 * WM * WN), kLds, stream, (const char*)g.a,
                      (const char*)g.b, g.c, (int)g.m, (int)g.n, kb, g.lda * kEsz, g.ldb * kEsz,
                      g.ldc, g.scale, g.accumulate, kb, (int64_t)0);
   return hipGetLastError();
@@ -284,7 +291,7 @@ template <Elt IN, bool AM, bool BM>
 static hipError_t launch_128_split(const GemmArgs& g, int slices, int64_t kb_slice, float* partial,
                                    hipStream_t stream) {
   constexpr int kEsz = EltInfo<IN>::bytes;
-  constexpr int kLds = g128::lds_bytes(128);
+  constexpr int kLds = g128::lds_bytes_grid(128, 2, 2);
   auto kern = gemm_mfma_128<IN, Elt::F32, AM, BM, 128, 2, 2>;
   static const hipError_t attr =
       hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
@@ -322,6 +329,32 @@ hipError_t gemm_128_layout(const GemmArgs& g, hipStream_t s) {
     case FRISK_PAIR(Elt::I8, Elt::I32): return launch_128<Elt::I8, Elt::I32, AM, BM>(g, s);
     default: return hipErrorInvalidValue;
   }
+}
+
+template <bool AM, bool BM, int WM, int WN>
+static hipError_t gemm_128_typed(const GemmArgs& g, hipStream_t s) {
+  switch (FRISK_PAIR(g.in, g.out)) {
+    case FRISK_PAIR(Elt::BF16, Elt::BF16): return launch_128<Elt::BF16, Elt::BF16, AM, BM, WM, WN>(g, s);
+    case FRISK_PAIR(Elt::BF16, Elt::F32): return launch_128<Elt::BF16, Elt::F32, AM, BM, WM, WN>(g, s);
+    case FRISK_PAIR(Elt::F16, Elt::F16): return launch_128<Elt::F16, Elt::F16, AM, BM, WM, WN>(g, s);
+    case FRISK_PAIR(Elt::F16, Elt::F32): return launch_128<Elt::F16, Elt::F32, AM, BM, WM, WN>(g, s);
+    case FRISK_PAIR(Elt::E4M3, Elt::BF16): return launch_128<Elt::E4M3, Elt::BF16, AM, BM, WM, WN>(g, s);
+    case FRISK_PAIR(Elt::E4M3, Elt::F16): return launch_128<Elt::E4M3, Elt::F16, AM, BM, WM, WN>(g, s);
+    case FRISK_PAIR(Elt::E4M3, Elt::F32): return launch_128<Elt::E4M3, Elt::F32, AM, BM, WM, WN>(g, s);
+    case FRISK_PAIR(Elt::I8, Elt::I32): return launch_128<Elt::I8, Elt::I32, AM, BM, WM, WN>(g, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <bool AM, bool BM>
+hipError_t gemm_128_grid_layout(const GemmArgs& g, hipStream_t s) {
+  const int wm = g.wave_m ? g.wave_m : 2, wn = g.wave_n ? g.wave_n : 2;
+  if (wm == 2 && wn == 2) return gemm_128_typed<AM, BM, 2, 2>(g, s);
+  if (wm == 4 && wn == 1) return gemm_128_typed<AM, BM, 4, 1>(g, s);
+  if (wm == 1 && wn == 4) return gemm_128_typed<AM, BM, 1, 4>(g, s);
+  if (wm == 2 && wn == 1) return gemm_128_typed<AM, BM, 2, 1>(g, s);
+  if (wm == 1 && wn == 2) return gemm_128_typed<AM, BM, 1, 2>(g, s);
+  return hipErrorInvalidValue;
 }
 
 #undef FRISK_PAIR

@@ -4,6 +4,7 @@
 
 namespace frisk {
 template hipError_t gemm_128_layout<false, true>(const GemmArgs&, hipStream_t);
+template hipError_t gemm_128_grid_layout<false, true>(const GemmArgs&, hipStream_t);
 template hipError_t gemm_128_split_layout<false, true>(const GemmArgs&, int, int64_t, float*,
                                                    hipStream_t);
 }  // namespace frisk

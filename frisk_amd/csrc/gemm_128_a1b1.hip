@@ -4,6 +4,7 @@
 
 namespace frisk {
 template hipError_t gemm_128_layout<true, false>(const GemmArgs&, hipStream_t);
+template hipError_t gemm_128_grid_layout<true, false>(const GemmArgs&, hipStream_t);
 template hipError_t gemm_128_split_layout<true, false>(const GemmArgs&, int, int64_t, float*,
                                                    hipStream_t);
 }  // namespace frisk

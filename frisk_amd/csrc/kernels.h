@@ -22,6 +22,9 @@ struct GemmArgs {
   int64_t ldc;
   float scale;  // scale_a * scale_b
   int accumulate;
+  // Requested kernel variant (0: the library chooses): 256 or 128 tiles,
+  // and the 128x128 kernel's wave grid.
+  int tile = 0, wave_m = 0, wave_n = 0;
 };
 
 // Split-K plan of the LDS-staged MFMA kernels (bf16/f16): `slices` slices
@@ -61,6 +64,9 @@ template <bool AM, bool BM>
 hipError_t gemm_w4_split_layout(const GemmArgs& g, int slices, int64_t kb_slice, float* partial,
                                 hipStream_t s);
 template <bool AM, bool BM> hipError_t gemm_128_layout(const GemmArgs& g, hipStream_t s);
+// The 128x128 kernel with the wave grid g.wave_m x g.wave_n (2x2, 4x1, 1x4,
+// 2x1 or 1x2).
+template <bool AM, bool BM> hipError_t gemm_128_grid_layout(const GemmArgs& g, hipStream_t s);
 template <bool AM, bool BM>
 hipError_t gemm_128_split_layout(const GemmArgs& g, int slices, int64_t kb_slice, float* partial,
                                  hipStream_t s);

@@ -29,9 +29,15 @@ whole-tensor operation, and launches the MI355X kernel for it:
   for them are allowed in the loop.  `sm_scale` (default 1/sqrt(D)) and
   `causal` are arguments of execute().
 
-The tile sizes and thread counts of a program describe the computation, not
-the launch: the MI355X kernels choose their own tiling.  Anything else raises
-ValueError naming the first mismatch.  There is no CPU fallback.
+A tiled GEMM program also names its workgroup tile (BM x BN) and thread
+count.  `plan()` runs layout inference (frisk_amd/ir/infer.cpp) on a copy of
+the program and reads the instruction contract of its tile product (MFMA
+atom and wave grid, `#frisk.mma_contract`); when a compiled kernel executes
+exactly that workgroup product (frisk_amd/variants.py) `execute()` runs that
+variant (`frisk_gemm_desc.tile / wave_m / wave_n`), and `plan().layouts_match`
+is True.  Otherwise the library's own tiling runs and `mismatch` says why.
+The attention kernel keeps its own tiling.  Anything else raises ValueError
+naming the first mismatch.  There is no CPU fallback.
 """
 from __future__ import annotations
 
@@ -39,7 +45,7 @@ import math
 from dataclasses import dataclass
 from typing import Optional, Sequence
 
-from . import _ir, tileprog
+from . import _ir, tileprog, variants
 
 ir = _ir()
 fr = ir.frisk
@@ -56,6 +62,12 @@ class GemmPlan:
     m: int
     n: int
     k: int
+    # The tile product's instruction contract from layout inference, the
+    # kernel variant (tile, wave_m, wave_n) that executes it, or why none does.
+    contract: Optional[str] = None
+    variant: Optional[tuple] = None
+    layouts_match: bool = False
+    mismatch: str = ""
 
 
 @dataclass
@@ -291,7 +303,11 @@ def _gemm_tiled(ops, entry) -> GemmPlan:
               f"A{a_shape} B{b_shape} C{c_shape} exactly")
     if _elem(a_t) != _elem(a_src) or _elem(b_t) != _elem(b_src):
         _fail("A/B tiles must keep the input dtype")
-    return GemmPlan(ia, ib, ic, ta, tb, True, M, N, K)
+    p = GemmPlan(ia, ib, ic, ta, tb, True, M, N, K)
+    policy = gop.get_attr("policy")
+    names = {"f16": "fp16", "bf16": "bf16", "f8E4M3FN": "e4m3fn", "i8": "int8", "f32": "fp32"}
+    p._tile = (bm, bn, bk, names.get(_elem(a_t), _elem(a_t)), policy, par.get_thread_num())
+    return p
 
 
 # ---------------------------------------------------------------------------
@@ -416,9 +432,64 @@ def _attention(ops, entry) -> AttnPlan:
 
 
 # ---------------------------------------------------------------------------
+_CONTRACTS: dict = {}
+
+
+def tile_contract(bm: int, bn: int, bk: int, dtype: str, trans_a: bool, trans_b: bool,
+                  threads: int, policy=None):
+    """(contract, reason) of the workgroup tile product C[bm, bn] += op(A).op(B)
+    (A, B tiles in Shared memory, f32 accumulator, `threads` lanes, warp
+    `policy`): the `#frisk.mma_contract` layout inference binds for it, or
+    (None, reason) when inference finds none."""
+    key = (bm, bn, bk, dtype, bool(trans_a), bool(trans_b), threads, str(policy))
+    if key not in _CONTRACTS:
+        try:
+            from .common import utils
+            s = utils.create_session()
+            S = ir.MemorySpace.SHARED
+            acc_t = "int32" if dtype == "int8" else "fp32"
+            _, entry = s.new_kernel("tile", [
+                s.memref_type([bk, bm] if trans_a else [bm, bk], dtype, space=S),
+                s.memref_type([bn, bk] if trans_b else [bk, bn], dtype, space=S),
+                s.memref_type([bm, bn], acc_t)])
+            acc = s.alloc_buffer([bm, bn], acc_t)
+            g = s.create_gemm(entry.get_argument(0), entry.get_argument(1), acc, trans_a=trans_a,
+                              trans_b=trans_b, clear_accum=True, legacy_semantics="tensor_v1")
+            if policy is not None:
+                g.set_attr("policy", s.builder.get_gemm_warp_policy_attr(policy))
+            g.set_attr("frisk.execution_threads", s.builder.get_int64_attr(threads))
+            s.builder.create_copy_op(acc, entry.get_argument(2), [], [])
+            fr.normalize_layout_ir(s.module, "gfx950")
+            rep = fr.infer_layouts(s.module)
+            if rep.get("status") != "materialized":
+                raise ValueError(f"layout inference {rep.get('status')}: {rep.get('failure', '')}")
+            found = [a for a in rep["assignments"] if a.startswith("mma#")]
+            _CONTRACTS[key] = (found[0].split(": ", 1)[1], "")
+        except Exception as e:  # reported as the reason; the GEMM still runs
+            _CONTRACTS[key] = (None, f"no instruction contract: {e}")
+    return _CONTRACTS[key]
+
+
+def _bind_variant(p: "GemmPlan", tile) -> "GemmPlan":
+    """Fill p.contract / variant / layouts_match / mismatch for the
+    workgroup tile `tile` = (bm, bn, bk, dtype, policy, threads), or record
+    that the program names none."""
+    if tile is None:
+        p.mismatch = "whole-matrix program: it names no workgroup tile, the library tiles it"
+        return p
+    bm, bn, bk, dtype, policy, threads = tile
+    p.contract, why = tile_contract(bm, bn, bk, dtype, p.trans_a, p.trans_b, threads, policy)
+    if p.contract is not None:
+        p.variant, why = variants.variant_for(p.contract, bm, bn, threads)
+    p.layouts_match = p.variant is not None
+    p.mismatch = why
+    return p
+
+
 def plan(module, kernel: str):
     """Recognise kernel `kernel` of `module`: a GemmPlan, an AttnPlan or a
-    tileprog.OpsPlan (fill / copy / reduce programs)."""
+    tileprog.OpsPlan (fill / copy / reduce programs).  A GemmPlan carries the
+    tile product's instruction contract and the kernel variant it selects."""
     k = module.get_kernel(kernel)
     if k is None:
         raise ValueError(f"execute: module has no kernel @{kernel}")
@@ -430,7 +501,8 @@ def plan(module, kernel: str):
     for recognise in (_gemm_whole, _gemm_tiled, _attention, tileprog.plan_whole,
                       tileprog.plan_tiled):
         try:
-            return recognise(ops, entry)
+            p = recognise(ops, entry)
+            return _bind_variant(p, getattr(p, "_tile", None)) if isinstance(p, GemmPlan) else p
         except (_Reject, tileprog.Reject) as e:
             reasons.append(f"{recognise.__name__.lstrip('_')}: {e}")
     raise ValueError(f"execute: kernel @{kernel} is not a recognised GEMM, attention or tile-op "
@@ -469,7 +541,8 @@ def execute(module, kernel: str, tensors: Sequence, *, stream=None, causal: bool
         return tileprog.run(p, tensors, stream=stream)
     if isinstance(p, GemmPlan):
         return rt.gemm(tensors[p.a], tensors[p.b], tensors[p.c], trans_a=p.trans_a, trans_b=p.trans_b,
-                       clear_accum=p.clear_accum, scale_a=scale_a, scale_b=scale_b, stream=stream)
+                       clear_accum=p.clear_accum, scale_a=scale_a, scale_b=scale_b, stream=stream,
+                       variant=p.variant)
     q, kk, v, o = (tensors[i] for i in (p.q, p.k, p.v, p.o))
     if p.k_transposed:
         kk = kk.transpose(-1, -2)  # [B, H, S, D] view; the C-ABI needs unit D stride

@@ -826,6 +826,9 @@ void bindBuilder(py::module_& m) {
       })
       // Extensions for building tensor-form IR directly (the form
       // frisk.normalize_layout_ir produces and layout inference consumes).
+      .def("get_gemm_warp_policy_attr", [](PyBuilder&, GemmWarpPolicy p) {
+        return PyAttr{Attribute::gemmPolicy(p)};
+      })
       .def("get_i64_array_attr", [](PyBuilder&, std::vector<int64_t> v) {
         return PyAttr{Attribute::denseI64(std::move(v))};
       })
@@ -1278,9 +1281,9 @@ void bindFrisk(py::module_& m) {
     return d;
   });
   m.def("mma_bindings", [](int64_t mm, int64_t n, int64_t k, const PyType& in, const PyType& acc,
-                           int64_t threads) {
+                           int64_t threads, GemmWarpPolicy policy) {
     py::list out;
-    for (const MmaBinding& b : cdna4MmaBindings(mm, n, k, in.t, acc.t, threads)) {
+    for (const MmaBinding& b : cdna4MmaBindings(mm, n, k, in.t, acc.t, threads, policy)) {
       py::dict d;
       d["atom"] = std::string(b.hw.atom.name);
       d["wave_grid"] = std::vector<int64_t>{b.hw.gM, b.hw.gN};
@@ -1294,7 +1297,7 @@ void bindFrisk(py::module_& m) {
     }
     return out;
   }, py::arg("m"), py::arg("n"), py::arg("k"), py::arg("in_type"), py::arg("acc_type"),
-     py::arg("threads") = 256);
+     py::arg("threads") = 256, py::arg("policy") = GemmWarpPolicy::Auto);
 
   bindLayout(m);
 }

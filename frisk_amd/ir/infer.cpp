@@ -266,7 +266,7 @@ std::string MmaBinding::str() const {
 }
 
 std::vector<MmaBinding> cdna4MmaBindings(int64_t m, int64_t n, int64_t k, Type in, Type acc,
-                                         int64_t threads) {
+                                         int64_t threads, GemmWarpPolicy policy) {
   std::vector<MmaBinding> out;
   auto kind = mfmaInputOf(in);
   if (!kind || threads < 64 || threads > 1024 || !isPow2(threads)) return out;
@@ -288,6 +288,18 @@ std::vector<MmaBinding> cdna4MmaBindings(int64_t m, int64_t n, int64_t k, Type i
         if (!dup) out.push_back(MmaBinding{*g, p, swapped});
       }
     }
+  }
+  if (policy != GemmWarpPolicy::Auto) {
+    // Keep the bindings whose logical wave grid (the hardware grid, turned
+    // around when the operands are swapped) is the policy's grid for that
+    // atom on the logical (m, n).
+    std::vector<MmaBinding> kept;
+    for (const MmaBinding& b : out) {
+      auto want = geometryWithAtom(m, n, k, b.hw.atom, threads, policy);
+      const int64_t lm = b.swapped ? b.hw.gN : b.hw.gM, ln = b.swapped ? b.hw.gM : b.hw.gN;
+      if (want && want->gM == lm && want->gN == ln) kept.push_back(b);
+    }
+    out = std::move(kept);
   }
   return out;
 }
@@ -724,7 +736,10 @@ class Inference {
       s.in = op->operand(0).type().elementType();
       s.acc = op->result(0).type().elementType();
       s.threads = threadsOf_.count(op) ? threadsOf_[op] : 128;
-      s.bindings = cdna4MmaBindings(s.m, s.n, s.k, s.in, s.acc, s.threads);
+      // frisk.mma's policy defaults to Square (FriskLayoutOps.td:42-43).
+      const GemmWarpPolicy policy = op->hasAttr("policy") ? (GemmWarpPolicy)op->intAttr("policy")
+                                                          : GemmWarpPolicy::Square;
+      s.bindings = cdna4MmaBindings(s.m, s.n, s.k, s.in, s.acc, s.threads, policy);
       if (s.bindings.empty())
         fail(op, "instruction-contract: no MFMA binding for this shape, type and thread count");
       for (const MmaBinding& b : s.bindings)

@@ -84,8 +84,15 @@ struct MmaBinding {
   int64_t mfmaPerWave() const { return hw.mRepeat * hw.nRepeat * hw.kRepeat; }
   std::string str() const;
 };
+// The MFMA bindings of an (m, n, k) product on `threads` lanes.  With the
+// Auto policy every wave grid is a candidate (the solver chooses); Square,
+// FullRow and FullCol fix the logical wave grid to the one that policy
+// gives (SM90MmaLayoutProof.cpp:25-62: a non-Auto policy yields one
+// geometry), leaving the MFMA atom and the operand orientation to the
+// solver.
 std::vector<MmaBinding> cdna4MmaBindings(int64_t m, int64_t n, int64_t k, Type in, Type acc,
-                                         int64_t threads);
+                                         int64_t threads,
+                                         GemmWarpPolicy policy = GemmWarpPolicy::Auto);
 
 // ---- cost model ---------------------------------------------------------------
 // Named features in issue cycles per wave (or bytes / barriers), weighted

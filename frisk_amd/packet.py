@@ -34,6 +34,8 @@ import json
 import re
 from typing import Any
 
+from . import variants
+
 __all__ = ["plan_packet", "execute_packet"]
 
 _TRANSPARENT = {"memref.alloc", "frisk.layout_view", "frisk.copy", "arith.constant",
@@ -118,13 +120,18 @@ def plan_packet(packet) -> dict:
         init = producer.get(mma["operands"][2])
         if not init or init["name"] != "arith.constant" or _splat(init["attrs"].get("value")) != 0.0:
             raise ValueError("execution packet: GEMM accumulator must start from a zero constant")
+        # The packet is one workgroup tile product: the compiled kernel that
+        # executes its contract (MFMA atom and wave grid) runs it.
+        m, n = mma["attrs"]["m"], mma["attrs"]["n"]
+        threads = int(mma["attrs"].get("frisk.execution_threads", 0))
+        variant, why = variants.variant_for(contract(mma), m, n, threads)
         return {"kind": "gemm", "a": source_arg(mma["operands"][0]), "b": source_arg(mma["operands"][1]),
                 "c": source_arg(store["operands"][1]),
                 "trans_a": bool(mma["attrs"].get("trans_a", False)),
                 "trans_b": bool(mma["attrs"].get("trans_b", False)),
-                "m": mma["attrs"]["m"], "n": mma["attrs"]["n"], "k": mma["attrs"]["k"],
-                "contract": contract(mma), "layouts_match": True,
-                "arg_types": [types[a] for a in args]}
+                "m": m, "n": n, "k": mma["attrs"]["k"], "threads": threads,
+                "contract": contract(mma), "variant": variant, "layouts_match": variant is not None,
+                "mismatch": why, "arg_types": [types[a] for a in args]}
     if names == _ATTENTION:
         qk, mul, rmax, bmax, sub, ex, rsum, bsum, div, trunc, pv, store = body
         chain = [(mul, 0, qk), (rmax, 0, mul), (bmax, 0, rmax), (sub, 0, mul), (sub, 1, bmax),
@@ -146,13 +153,19 @@ def plan_packet(packet) -> dict:
         if not scale_op or scale_op["name"] != "arith.constant":
             raise ValueError("execution packet: the score scale must be a constant")
         head_dim = qk["attrs"]["k"]
+        # The attention kernel computes S^T = K.Q^T with the 32x32x16 atom
+        # (queries on lanes, whole query rows per wave) and needs head_dim
+        # >= 32 for its O^T tiles.
         kernel_layout = "swapped = true" in contract(qk) and "32x32x16" in contract(qk)
+        why = "" if kernel_layout and head_dim >= 32 else (
+            "the attention kernel computes S^T = K.Q^T with 32x32x16 MFMAs and head_dim >= 32; "
+            f"this packet's QK contract is {contract(qk)} at head_dim {head_dim}")
         return {"kind": "attention", "q": source_arg(qk["operands"][0]), "k": source_arg(qk["operands"][1]),
                 "v": source_arg(pv["operands"][1]), "o": source_arg(store["operands"][1]),
                 "scale": _splat(scale_op["attrs"].get("value")), "seq_q": qk["attrs"]["m"],
                 "seq_k": qk["attrs"]["n"], "head_dim": head_dim,
                 "contract": contract(qk), "layouts_match": bool(kernel_layout and head_dim >= 32),
-                "arg_types": [types[a] for a in args]}
+                "mismatch": why, "arg_types": [types[a] for a in args]}
     values = {v["id"]: v for v in pk["values"]}
     if names in (["frisk.tile_load", "frisk.reduce_tensor", "frisk.tile_store"],
                  ["frisk.tile_load", "frisk.reduce_tensor", "arith.addf", "frisk.tile_store"],
@@ -245,11 +258,23 @@ def _plan_reduce(body, producer, values, source_arg, types, args, root):
             "leaf_order": order, "arg_types": [types[a] for a in args]}
 
 
-def execute_packet(packet, tensors, *, stream=None) -> dict:
+def execute_packet(packet, tensors, *, stream=None, allow_layout_mismatch=False) -> dict:
     """Run the packet on the GPU with `tensors` bound to the kernel's
-    arguments (in order).  Returns the plan that was executed."""
+    arguments (in order).  Returns the plan that was executed.
+
+    A GEMM packet runs on the kernel variant its MMA contract selects, an
+    attention packet on the attention kernel.  When no kernel executes the
+    packet's contract (`plan_packet(...)["layouts_match"]` is False) this
+    raises ValueError with the reason, unless `allow_layout_mismatch`, which
+    runs the library's own kernel on the same tensors (same mathematics,
+    other register layouts)."""
     from . import runtime as rt
     plan = plan_packet(packet)
+    if plan["kind"] in ("gemm", "attention") and not plan["layouts_match"] and \
+            not allow_layout_mismatch:
+        raise ValueError(f"execution packet: no kernel executes this {plan['kind']} packet's "
+                         f"instruction contract ({plan['mismatch']}); pass "
+                         "allow_layout_mismatch=True to run the library's own kernel")
     tensors = list(tensors)
     if len(tensors) != len(plan["arg_types"]):
         raise ValueError(f"execution packet: kernel takes {len(plan['arg_types'])} arguments, "
@@ -261,7 +286,7 @@ def execute_packet(packet, tensors, *, stream=None) -> dict:
                              f"{tuple(t.shape)}")
     if plan["kind"] == "gemm":
         rt.gemm(tensors[plan["a"]], tensors[plan["b"]], tensors[plan["c"]], trans_a=plan["trans_a"],
-                trans_b=plan["trans_b"], stream=stream)
+                trans_b=plan["trans_b"], stream=stream, variant=plan["variant"])
     elif plan["kind"] == "reduce":
         dst = tensors[plan["dst"]]
         if plan["init"] is not None:

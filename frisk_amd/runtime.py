@@ -26,7 +26,7 @@ EXPORTS = ("frisk_gemm", "frisk_gemm_workspace_size", "frisk_gemm_plan", "frisk_
            "frisk_copy", "frisk_fill",
            "frisk_last_error", "frisk_abi_version", "frisk_probe_mfma_layout",
            "frisk_probe_lds_transpose")
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 REDUCE_SUM, REDUCE_MAX, REDUCE_MIN = 0, 1, 2
 REDUCE_KINDS = {"sum": REDUCE_SUM, "add": REDUCE_SUM, "max": REDUCE_MAX, "min": REDUCE_MIN}
@@ -43,6 +43,8 @@ class GemmDesc(ctypes.Structure):
         ("c", ctypes.c_void_p), ("ldc", ctypes.c_int64),
         ("scale_a", ctypes.c_float), ("scale_b", ctypes.c_float),
         ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_int64),
+        ("tile", ctypes.c_int32), ("wave_m", ctypes.c_int32), ("wave_n", ctypes.c_int32),
+        ("variant_flags", ctypes.c_int32),
     ]
 
 
@@ -182,8 +184,9 @@ def _row_major(t, name: str) -> int:
 
 
 def gemm_desc(a, b, c, *, trans_a=False, trans_b=False, clear_accum=True,
-              scale_a=1.0, scale_b=1.0) -> GemmDesc:
-    """Describe C (+)= op(A).op(B) for row-major device tensors (see frisk_hip.h)."""
+              scale_a=1.0, scale_b=1.0, variant=None) -> GemmDesc:
+    """Describe C (+)= op(A).op(B) for row-major device tensors (see frisk_hip.h).
+    `variant` = (tile, wave_m, wave_n) requests a kernel variant (frisk_gemm_desc.tile)."""
     lda, ldb, ldc = _row_major(a, "A"), _row_major(b, "B"), _row_major(c, "C")
     m = a.shape[1] if trans_a else a.shape[0]
     k = a.shape[0] if trans_a else a.shape[1]
@@ -195,7 +198,8 @@ def gemm_desc(a, b, c, *, trans_a=False, trans_b=False, clear_accum=True,
     return GemmDesc(m, n, k, int(bool(trans_a)), int(bool(trans_b)),
                     torch_dtype_code(a.dtype), torch_dtype_code(b.dtype), torch_dtype_code(c.dtype),
                     int(bool(clear_accum)), a.data_ptr(), lda, b.data_ptr(), ldb,
-                    c.data_ptr(), ldc, float(scale_a), float(scale_b), None, 0)
+                    c.data_ptr(), ldc, float(scale_a), float(scale_b), None, 0,
+                    *(tuple(variant) if variant else (0, 0, 0)), 0)
 
 
 def gemm_workspace_bytes(a, b, c, *, trans_a=False, trans_b=False) -> int:
@@ -214,10 +218,11 @@ def plan_of(desc: GemmDesc) -> dict:
     return json.loads(buf.value.decode())
 
 
-def gemm_plan(a, b, c, *, trans_a=False, trans_b=False, workspace=True) -> dict:
-    """The launch gemm(a, b, c, ..., workspace=workspace) makes (frisk_gemm_plan):
-    kernel, tiles, MFMA atom, operand storage order and LDS reads, split-K."""
-    d = gemm_desc(a, b, c, trans_a=trans_a, trans_b=trans_b)
+def gemm_plan(a, b, c, *, trans_a=False, trans_b=False, workspace=True, variant=None) -> dict:
+    """The launch gemm(a, b, c, ..., workspace=workspace, variant=variant) makes
+    (frisk_gemm_plan): kernel, tiles, MFMA atom, wave grid, operand storage
+    order and LDS reads, split-K, and the kernel's instruction contract."""
+    d = gemm_desc(a, b, c, trans_a=trans_a, trans_b=trans_b, variant=variant)
     if workspace is not False:
         need = int(load().frisk_gemm_workspace_size(ctypes.byref(d)))
         _check(need if need < 0 else OK, "frisk_gemm_workspace_size")
@@ -226,14 +231,16 @@ def gemm_plan(a, b, c, *, trans_a=False, trans_b=False, workspace=True) -> dict:
 
 
 def gemm(a, b, c, *, trans_a=False, trans_b=False, clear_accum=True,
-         scale_a=1.0, scale_b=1.0, workspace=True, stream=None):
+         scale_a=1.0, scale_b=1.0, workspace=True, stream=None, variant=None):
     """C = op(A).op(B) (or C += ... with clear_accum=False) on the GPU.
 
     `workspace`: True allocates the scratch frisk_gemm_workspace_size asks
     for (torch's caching allocator), a device tensor supplies it, False runs
-    the unsplit kernels."""
+    the unsplit kernels.  `variant` = (tile, wave_m, wave_n) runs that kernel
+    variant (unsplit): (256, 2, 2), or (128, gm, gn) with the wave grid
+    2x2, 4x1, 1x4, 2x1 or 1x2."""
     d = gemm_desc(a, b, c, trans_a=trans_a, trans_b=trans_b, clear_accum=clear_accum,
-                  scale_a=scale_a, scale_b=scale_b)
+                  scale_a=scale_a, scale_b=scale_b, variant=variant)
     ws = None
     if workspace is not False:
         need = load().frisk_gemm_workspace_size(ctypes.byref(d))

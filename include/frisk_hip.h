@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define FRISK_ABI_VERSION 5
+#define FRISK_ABI_VERSION 6
 
 /* Element types (the dtype strings of ffi/ir.cpp:399-411 plus bf16/i8/i32). */
 typedef enum frisk_dtype {
@@ -105,6 +105,16 @@ typedef struct frisk_gemm_desc {
   float scale_a, scale_b;
   void* workspace; /* optional, may be NULL */
   int64_t workspace_bytes;
+  /* Optional kernel variant; all zero: the library chooses.  tile = 256:
+   * the 256x256 kernel (four waves in a 2x2 grid); tile = 128: the 128x128
+   * kernel with a wave_m x wave_n wave grid, one of 2x2, 4x1, 1x4 (256
+   * threads) or 2x1, 1x2 (128 threads), 0x0 meaning 2x2.  A requested
+   * variant runs unsplit (the workspace is not used), and returns
+   * FRISK_EUNSUP when the descriptor does not meet the matrix-core
+   * conditions below.  variant_flags must be 0.  This is how a tile
+   * program's instruction contract (its #frisk.mma_contract: MFMA atom and
+   * wave grid of the workgroup tile) selects the kernel that executes it. */
+  int32_t tile, wave_m, wave_n, variant_flags;
 } frisk_gemm_desc;
 
 int frisk_gemm(const frisk_gemm_desc* desc, void* stream);

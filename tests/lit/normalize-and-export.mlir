@@ -28,7 +28,11 @@
 // LAYOUT: module attributes {{{.*}}frisk.layout_cost_model = "cdna4-layout-v1"
 // LAYOUT: frisk.mma
 // LAYOUT-SAME: form = "ss"
-// LAYOUT-SAME: atom = "v_mfma_f32_32x32x16_f16"
+// The builder's GEMM carries policy Square, which fixes the wave grid (a
+// non-Auto policy gives one geometry, SM90MmaLayoutProof.cpp:25-62): two
+// waves over 64x64 as 1x2; the MFMA atom is the solver's choice.
+// LAYOUT-SAME: atom = "v_mfma_f32_{{32x32x16|16x16x32}}_f16", wave_grid = [1, 2]
+// LAYOUT-SAME: policy = "Square"
 // LAYOUT: frisk.reduce_tensor
 // LAYOUT-SAME: frisk.reduction_contract = #frisk.reduction_contract<
 

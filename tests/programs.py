@@ -161,9 +161,13 @@ def attention_tensor_form(M=64, N=64, D=16, dtype="fp16", threads=128, scale=0.2
                                       {"value": b.get_dense_splat_attr(ty, x)}).get_result(0)
     op = lambda n, ins, ty, attrs=None: b.create_op(n, ins, [ty], attrs or {}).get_result(0)
     zero = const(t2(M, N, f32), 0.0)
+    # Waves along the queries (FullRow): every wave owns whole query rows of
+    # S and of O, the layout of the attention kernel (frisk_amd/csrc/attn.h).
+    # Without the attribute frisk.mma's policy is Square.
+    full_row = b.get_gemm_warp_policy_attr(F.GemmWarpPolicy.FullRow)
     scores = op("frisk.mma", [qv, kv, zero], t2(M, N, f32),
                 {"m": i64(M), "n": i64(N), "k": i64(D), "trans_a": b.get_bool_attr(False),
-                 "trans_b": b.get_bool_attr(True)})
+                 "trans_b": b.get_bool_attr(True), "policy": full_row})
     scaled = op("arith.mulf", [scores, const(t2(M, N, f32), scale)], t2(M, N, f32))
     mx = op("frisk.reduce_tensor", [scaled], t1(M, f32), {"kind": b.get_str_attr("max"), "dim": i64(1)})
     e0 = op("tensor.empty", [], t2(M, N, f32))
@@ -178,7 +182,7 @@ def attention_tensor_form(M=64, N=64, D=16, dtype="fp16", threads=128, scale=0.2
     ozero = const(t2(M, D, f32), 0.0)
     result = op("frisk.mma", [p, vv, ozero], t2(M, D, f32),
                 {"m": i64(M), "n": i64(D), "k": i64(N), "trans_a": b.get_bool_attr(False),
-                 "trans_b": b.get_bool_attr(False)})
+                 "trans_b": b.get_bool_attr(False), "policy": full_row})
     b.create_op("frisk.tile_store", [result, view(o, mo)], [])
     return s, kernel
 

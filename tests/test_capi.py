@@ -360,6 +360,42 @@ def test_gemm_plan_generic_cases():
         plan(m=0)
 
 
+def test_gemm_variant_requests():
+    # frisk_gemm_desc.tile / wave_m / wave_n name the kernel that runs; the
+    # plan reports it with its instruction contract in the solver's syntax.
+    p = plan(tile=128, wave_m=4, wave_n=1)
+    assert p["kernel"] == "gemm_128" and p["requested"] and p["waves"] == [4, 1]
+    assert p["wave_tile"] == [32, 128] and p["slices"] == 1
+    assert p["mma_contract"] == ('{atom = "v_mfma_f32_32x32x16_bf16", wave_grid = [4, 1], '
+                                 'repeats = [1, 4, 2], policy = "FullRow", swapped = false}')
+    p = plan(tile=256)
+    assert p["kernel"] == "gemm_w4" and p["requested"] and "swapped = true" in p["mma_contract"]
+    assert plan(tile=128)["waves"] == [2, 2]
+    # The library's own choice is reported unrequested, with its contract.
+    p = plan()
+    assert not p["requested"] and 'repeats = [4, 4, 4], policy = "Square"' in p["mma_contract"]
+    # A requested variant runs unsplit: no workspace is asked for.
+    d = rt.GemmDesc(m=128, n=4096, k=4096, trans_a=0, trans_b=0, a_type=rt.BF16, b_type=rt.BF16,
+                    c_type=rt.BF16, clear_accum=1, a=16, lda=4096, b=16, ldb=4096, c=16,
+                    ldc=4096, scale_a=1.0, scale_b=1.0, tile=128)
+    assert rt.load().frisk_gemm_workspace_size(ctypes.byref(d)) == 0
+    d.tile = 0
+    assert rt.load().frisk_gemm_workspace_size(ctypes.byref(d)) > 0
+    # Small M requested on 128x128 tiles runs there, not on the small-M kernel.
+    assert plan(m=16, tile=128, wave_m=2, wave_n=1)["kernel"] == "gemm_128"
+    for bad in (dict(tile=128, wave_m=3, wave_n=1), dict(tile=256, wave_m=4, wave_n=1),
+                dict(tile=64), dict(wave_m=2, wave_n=2), dict(tile=128, wave_m=2),
+                dict(tile=128, variant_flags=1)):
+        with pytest.raises(ValueError, match="no kernel variant"):
+            plan(**bad)
+    # Valid variant, but the request is not matrix-core work.
+    for bad in (dict(a_type=rt.F32, b_type=rt.F32, c_type=rt.F32), dict(lda=4100)):
+        with pytest.raises(ValueError, match="runs on the matrix cores only"):
+            plan(tile=128, **bad)
+    rc, msg = gemm_call(tile=256, lda=4100)
+    assert rc == rt.EUNSUP and "256x256-tile variant" in msg, msg
+
+
 def test_attn_rejects_kv_rows_beyond_32bit_offsets():
     # 32 heads x 128 dims viewed [b, s, h, d] -> [b, h, s, d]: a key row is
     # 8 KiB apart, so key 2^18 (the 2^18 + 1st) starts at 2 GiB.

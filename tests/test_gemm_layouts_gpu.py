@@ -186,3 +186,49 @@ def test_sentinel_guards_every_layout(ta, tb):
         run(a, b, gc.t, ta, tb, sa, sb)
         assert gc.guards_intact()
         assert torch.equal(a, a0) and torch.equal(b, b0)
+
+
+VARIANTS = [(256, 2, 2), (128, 2, 2), (128, 4, 1), (128, 1, 4), (128, 2, 1), (128, 1, 2)]
+
+
+@pytest.mark.parametrize("variant", VARIANTS, ids=[f"t{t}w{a}x{b}" for t, a, b in VARIANTS])
+@pytest.mark.parametrize("in_dt,out_dt", [(torch.bfloat16, torch.bfloat16), (FP8, torch.float32),
+                                          (torch.int8, torch.int32)], ids=["bf16", "fp8", "i8"])
+@pytest.mark.parametrize("ta,tb", LAYOUTS, ids=LAYOUT_IDS)
+def test_requested_kernel_variants(variant, in_dt, out_dt, ta, tb):
+    # frisk_gemm_desc.tile / wave_m / wave_n: the tile and wave grid a tile
+    # program's instruction contract names.  The plan reports exactly that
+    # variant, and the result matches the oracle like the library's own choice.
+    m, n, k = 304, 528, 784
+    tile, wm, wn = variant
+    print(f"case variant {variant} ta={ta} tb={tb} {in_dt}", flush=True)
+    a, b, sa, sb = make_operands(m, n, k, in_dt, ta, tb, seed=tile + 7 * wm + 3 * wn)
+    c = torch.empty(m, n, dtype=out_dt, device="cuda")
+    p = rt.gemm_plan(a, b, c, trans_a=ta, trans_b=tb, variant=variant)
+    assert p["requested"] and p["tile_m"] == tile and p["waves"] == [wm, wn], p
+    assert p["kernel"] == ("gemm_w4" if tile == 256 else "gemm_128") and p["slices"] == 1
+    assert f"wave_grid = [{wm}, {wn}]" in p["mma_contract"]
+    rt.gemm(a, b, c, trans_a=ta, trans_b=tb, scale_a=sa, scale_b=sb, variant=variant)
+    torch.cuda.synchronize()
+    if in_dt == torch.int8:
+        A = a.cpu().numpy().astype(np.float64)
+        B = b.cpu().numpy().astype(np.float64)
+        assert np.array_equal(c.cpu().numpy().astype(np.float64), (A.T if ta else A) @ (B.T if tb else B))
+    else:
+        check(decode(c), reference(a, b, ta, tb, sa, sb), in_dt, out_dt)
+
+
+def test_variants_agree_bitwise_on_one_grid():
+    # Every 128x128 wave grid sums each output over the same k order, so the
+    # grids give identical bits (only the placement of work differs).
+    m, n, k = 512, 640, 1024
+    a, b, _, _ = make_operands(m, n, k, torch.bfloat16, False, True, seed=5)
+    outs = []
+    for v in VARIANTS[1:]:
+        c = torch.empty(m, n, dtype=torch.float32, device="cuda")
+        rt.gemm(a, b, c, trans_b=True, variant=v)
+        outs.append(c)
+    torch.cuda.synchronize()
+    for c in outs[1:]:
+        assert torch.equal(c, outs[0])
+

@@ -611,13 +611,35 @@ def test_sm90_swizzle_form():
 # ---------------------------------------------------------------------------
 def test_plan_recognises_tiled_gemm():
     from frisk_amd.executor import GemmPlan, plan
+    key = lambda p: (p.a, p.b, p.c, p.trans_a, p.trans_b, p.clear_accum, p.m, p.n, p.k)
     for ta, tb in itertools.product([False, True], repeat=2):
         s, _ = P.tiled_gemm(512, 256, 1024, trans_a=ta, trans_b=tb)
-        assert plan(s.module, "matmul") == GemmPlan(0, 1, 2, ta, tb, True, 512, 256, 1024)
+        p = plan(s.module, "matmul")
+        assert key(p) == key(GemmPlan(0, 1, 2, ta, tb, True, 512, 256, 1024))
+        # 128x128 tiles on 256 threads (the builder's Square policy): the
+        # 2x2 wave grid of the 128x128 kernel executes the tile's contract.
+        assert p.variant == (128, 2, 2) and p.layouts_match and p.mismatch == ""
+        assert 'wave_grid = [2, 2]' in p.contract and 'policy = "Square"' in p.contract
     s, _ = P.tiled_gemm(256, 256, 256, k_scale=32)
     assert plan(s.module, "matmul").k == 256
     s, _ = P.whole_gemm(64, 32, 16, clear=False)
-    assert plan(s.module, "gemm") == GemmPlan(0, 1, 2, False, False, False, 64, 32, 16)
+    p = plan(s.module, "gemm")
+    assert key(p) == key(GemmPlan(0, 1, 2, False, False, False, 64, 32, 16))
+    assert p.variant is None and not p.layouts_match and "whole-matrix" in p.mismatch
+
+
+@pytest.mark.parametrize("bm,threads,variant", [(256, 256, (256, 2, 2)), (128, 128, (128, 1, 2)),
+                                                (64, 128, None)])
+def test_plan_takes_the_kernel_variant_from_the_contract(bm, threads, variant):
+    # The solver's contract for the program's workgroup tile product picks
+    # the compiled kernel that executes it; a tile no kernel computes keeps
+    # the library's own tiling and says why.
+    from frisk_amd.executor import plan
+    s, _ = P.tiled_gemm(512, 512, 256, BM=bm, BN=bm, BK=64, threads=threads)
+    p = plan(s.module, "matmul")
+    assert p.variant == variant and p.layouts_match == (variant is not None)
+    if variant is None:
+        assert "no kernel computes a 64x64 workgroup tile" in p.mismatch
 
 
 def test_plan_recognises_attention():

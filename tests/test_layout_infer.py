@@ -17,6 +17,7 @@ import re
 import pytest
 
 import frisk_amd as F
+from frisk_amd import variants as V
 from tests import programs as P
 
 
@@ -303,6 +304,43 @@ def test_plan_packet_attention_and_gemm():
     g = F.plan_packet(_packet(_gemm_module()))
     assert g["kind"] == "gemm" and (g["a"], g["b"], g["c"]) == (0, 1, 2)
     assert (g["m"], g["n"], g["k"]) == (64, 64, 16) and not g["trans_a"] and not g["trans_b"]
+    # A 64x64 tile on the default 128 threads: no compiled kernel executes it.
+    assert g["threads"] == 128 and g["variant"] is None and g["layouts_match"] is False
+    assert "no kernel computes a 64x64 workgroup tile" in g["mismatch"]
+
+
+@pytest.mark.parametrize("m,threads,variant", [(128, 256, (128, 2, 2)), (128, 128, (128, 1, 2)),
+                                               (256, 256, (256, 2, 2))])
+def test_plan_packet_gemm_variant_from_contract(m, threads, variant):
+    g = F.plan_packet(_packet(_gemm_module(m, m, 64, threads=threads)))
+    assert g["threads"] == threads and g["variant"] == variant and g["layouts_match"] is True
+    assert g["mismatch"] == ""
+    assert V.logical_grid(V.parse_contract(g["contract"])) == variant[1:]
+
+
+def test_execute_packet_refuses_a_contract_no_kernel_executes():
+    with pytest.raises(ValueError, match="allow_layout_mismatch"):
+        F.execute_packet(_packet(_gemm_module()), [None, None, None])
+    with pytest.raises(ValueError, match="head_dim >= 32"):
+        F.execute_packet(_packet(_attention(64, 64, 16, 128, dtype="fp16")), [None] * 4)
+
+
+def test_variant_for_reasons():
+    c = ('atom = "v_mfma_f32_32x32x16_bf16", wave_grid = [2, 2], repeats = [2, 2, 4], '
+         'policy = "Square", swapped = false')
+    assert V.variant_for(c, 128, 128, 256) == ((128, 2, 2), "")
+    assert V.variant_for(c, 256, 256, 256) == ((256, 2, 2), "")
+    assert "threads do not form" in V.variant_for(c, 128, 128, 128)[1]
+    assert "64x128" in V.variant_for(c, 64, 128, 256)[1]
+    c16 = c.replace("32x32x16", "16x16x32")
+    assert "32x32 MFMA atoms" in V.variant_for(c16, 128, 128, 256)[1]
+    # A swapped contract runs the transposed product: hardware grid [1, 2]
+    # is the logical 2x1 grid.
+    cs = c.replace("wave_grid = [2, 2]", "wave_grid = [1, 2]").replace("false", "true")
+    assert V.variant_for(cs, 128, 128, 128) == ((128, 2, 1), "")
+    fp8 = c.replace("v_mfma_f32_32x32x16_bf16", "v_mfma_scale_f32_32x32x64_f8f6f4")
+    assert V.variant_for(fp8, 128, 128, 256) == ((128, 2, 2), "")
+    assert V.variant_for("", 128, 128, 256)[0] is None
 
 
 def test_plan_packet_rejects_other_programs():

@@ -34,9 +34,13 @@ def test_attention_packet(M, N, D, dtype, threads):
     g.manual_seed(M + N + D)
     q, k, v = ((torch.rand(n, D, generator=g, device="cuda") * 2 - 1).to(tdt) for n in (M, N, N))
     o = torch.full((M, D), float("nan"), dtype=torch.float32, device="cuda")
-    plan = F.execute_packet(_packet(M, N, D, dtype, threads), [q, k, v, o])
+    # head_dim 16: the packet's contract is not the kernel's (it pads V);
+    # the kernel runs the same mathematics on the packet's tensors.
+    plan = F.execute_packet(_packet(M, N, D, dtype, threads), [q, k, v, o],
+                            allow_layout_mismatch=D < 32)
     torch.cuda.synchronize()
     assert plan["kind"] == "attention" and plan["scale"] == 0.25
+    assert plan["layouts_match"] == (D >= 32)
     qd, kd, vd = decode(q), decode(k), decode(v)
     ref = A.attention_fp64(qd[None, None], kd[None, None], vd[None, None], scale=0.25)[0][0, 0]
     err = np.abs(decode(o) - ref)
@@ -53,24 +57,35 @@ def test_attention_packet(M, N, D, dtype, threads):
         assert np.all(err <= 2.0 ** -7 * (w @ np.abs(vd)) + 1e-6), err.max()
 
 
-def test_gemm_packet():
+@pytest.mark.parametrize("m,k,threads,dtype,variant", [(128, 64, 256, "bf16", (128, 2, 2)),
+                                                       (128, 128, 128, "fp16", (128, 1, 2)),
+                                                       (256, 64, 256, "bf16", (256, 2, 2)),
+                                                       (64, 32, 128, "bf16", None)])
+def test_gemm_packet(m, k, threads, dtype, variant):
+    print(f"case packet gemm {m}x{m}x{k} threads={threads} {dtype}", flush=True)
     s = F.create_session()
     S = F.MemorySpace.SHARED
-    _, entry = s.new_kernel("gemm", [s.memref_type([64, 32], "bf16", space=S),
-                                     s.memref_type([32, 64], "bf16", space=S),
-                                     s.memref_type([64, 64], "fp32")])
-    c = s.alloc_buffer([64, 64], "fp32")
-    s.create_gemm(entry.get_argument(0), entry.get_argument(1), c, clear_accum=True,
-                  legacy_semantics="tensor_v1")
+    _, entry = s.new_kernel("gemm", [s.memref_type([m, k], dtype, space=S),
+                                     s.memref_type([k, m], dtype, space=S),
+                                     s.memref_type([m, m], "fp32")])
+    c = s.alloc_buffer([m, m], "fp32")
+    g = s.create_gemm(entry.get_argument(0), entry.get_argument(1), c, clear_accum=True,
+                      legacy_semantics="tensor_v1")
+    g.set_attr("frisk.execution_threads", s.builder.get_int64_attr(threads))
     s.builder.create_copy_op(c, entry.get_argument(2), [], [])
     F.frisk.normalize_layout_ir(s.module, "gfx950")
     F.frisk.infer_layouts(s.module)
-    a = randn((64, 32), 1).to(torch.bfloat16)
-    b = randn((32, 64), 2).to(torch.bfloat16)
-    out = torch.full((64, 64), float("nan"), dtype=torch.float32, device="cuda")
-    plan = F.execute_packet(F.frisk.export_execution(s.module), [a, b, out])
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float16
+    a = randn((m, k), 1).to(tdt)
+    b = randn((k, m), 2).to(tdt)
+    out = torch.full((m, m), float("nan"), dtype=torch.float32, device="cuda")
+    # The 64x64 tile on 128 threads has no kernel of its own: it runs on the
+    # library's tiling only when the caller allows it.
+    plan = F.execute_packet(F.frisk.export_execution(s.module), [a, b, out],
+                            allow_layout_mismatch=variant is None)
     torch.cuda.synchronize()
-    assert plan["kind"] == "gemm"
+    assert plan["kind"] == "gemm" and plan["variant"] == variant
+    assert plan["layouts_match"] == (variant is not None)
     ref = decode(a) @ decode(b)
     assert G.row_scaled_error(decode(out), ref) <= 1e-5
 

@@ -81,7 +81,8 @@ def test_frisk_opt_packet_executes(tmp_path):
     g.manual_seed(7)
     q, k, v = ((torch.rand(64, 16, generator=g, device="cuda") * 2 - 1).half() for _ in range(3))
     o = torch.full((64, 16), float("nan"), dtype=torch.float32, device="cuda")
-    plan = F.execute_packet(packet, [q, k, v, o])
+    # head_dim 16 is not the attention kernel's contract (the kernel pads V).
+    plan = F.execute_packet(packet, [q, k, v, o], allow_layout_mismatch=True)
     torch.cuda.synchronize()
     assert plan["kind"] == "attention"
     qd, kd, vd = decode(q), decode(k), decode(v)
