@@ -207,53 +207,6 @@ def launch_percentiles(torch, fn, n=50):
     return {"p10": round(pick(0.1), 6), "p50": round(pick(0.5), 6), "p90": round(pick(0.9), 6)}
 
 
-def _sclk_paths():
-    import glob
-    return sorted(glob.glob("/sys/class/drm/card*/device/pp_dpm_sclk"))
-
-
-def read_sclk_mhz():
-    """Current shader clock from the amdgpu driver's DPM table (the level
-    marked '*'), or None where the file is not readable."""
-    for path in _sclk_paths():
-        try:
-            for line in open(path).read().splitlines():
-                if line.rstrip().endswith("*"):
-                    return int(line.split(":")[1].strip().lower().split("mhz")[0])
-        except (OSError, ValueError, IndexError):
-            continue
-    return None
-
-
-def sustained_clock(torch, fn, seconds=0.4):
-    """Median shader clock (MHz) sampled every 20 ms while fn runs back to
-    back for `seconds` (the clock a sustained workload sees; MI355X's
-    published peaks are quoted at 2400 MHz)."""
-    import threading
-    samples, stop = [], threading.Event()
-
-    def sample():
-        while not stop.is_set():
-            v = read_sclk_mhz()
-            if v is not None:
-                samples.append(v)
-            time.sleep(0.02)
-
-    th = threading.Thread(target=sample, daemon=True)
-    th.start()
-    t0 = time.perf_counter()
-    while time.perf_counter() - t0 < seconds:
-        for _ in range(8):
-            fn()
-        torch.cuda.synchronize()
-    stop.set()
-    th.join()
-    if not samples:
-        return None
-    samples.sort()
-    return samples[len(samples) // 2]
-
-
 def provenance(torch):
     """What was measured: hashes of the kernel sources and of the built
     library, the git commit recorded at build time, and the GPU."""
@@ -466,6 +419,7 @@ def main():
         sys.exit(2)
     import torch
     from frisk_amd import runtime as rt
+    from frisk_amd.clock import sustained_clock
     rt.load()
     torch.cuda.set_device(0)
     work = make_workloads(torch, rt)

@@ -1278,6 +1278,7 @@ void bindFrisk(py::module_& m) {
     py::dict d;
     d["id"] = p.id;
     d["weights"] = p.weights;
+    d["simd_share"] = p.simdShare;
     return d;
   });
   m.def("mma_bindings", [](int64_t mm, int64_t n, int64_t k, const PyType& in, const PyType& acc,

@@ -321,6 +321,12 @@ const std::vector<std::string>& CostProfile::featureNames() {
   return names;
 }
 
+const std::vector<std::string>& CostProfile::perWaveFeatures() {
+  static const std::vector<std::string> names = {"mfma_cycles", "valu_issues", "trans_issues",
+                                                 "reduction_shuffles"};
+  return names;
+}
+
 CostProfile CostProfile::defaults() {
   // Cycles per unit on MI355X.  MFMA cycles count 1:1.  LDS cycles are
   // modelled phases (16 lanes x 16 B at 64 banks of 4 B).  A 128-byte global
@@ -372,6 +378,41 @@ struct JsonCursor {
     i = end;
     return v;
   }
+  bool boolean() {
+    ws();
+    for (const char* w : {"true", "false"})
+      if (s.compare(i, strlen(w), w) == 0) {
+        i += strlen(w);
+        return w[0] == 't';
+      }
+    throw InvalidArgument("cost-profile: expected true or false");
+  }
+  // Reads past one value of any kind (provenance records).
+  void skip() {
+    ws();
+    if (i >= s.size()) throw InvalidArgument("cost-profile: truncated");
+    if (s[i] == '"') {
+      str();
+    } else if (s[i] == '{' || s[i] == '[') {
+      const char close = s[i] == '{' ? '}' : ']';
+      ++i;
+      if (eat(close)) return;
+      do {
+        if (close == '}') {
+          str();
+          expect(':');
+        }
+        skip();
+      } while (eat(','));
+      expect(close);
+    } else if (s[i] == 't' || s[i] == 'f') {
+      boolean();
+    } else if (s.compare(i, 4, "null") == 0) {
+      i += 4;
+    } else {
+      num();
+    }
+  }
 };
 }  // namespace
 
@@ -401,6 +442,10 @@ CostProfile CostProfile::fromJson(const std::string& text) {
         } while (c.eat(','));
         c.expect('}');
       }
+    } else if (key == "simd_share") {
+      p.simdShare = c.boolean();
+    } else if (key == "provenance") {
+      c.skip();
     } else {
       throw InvalidArgument("cost-profile: unknown key '" + key + "'");
     }
@@ -1110,10 +1155,19 @@ class Inference {
       }
       complete &= ok;
     }
+    double share = 1.0;
+    if (opts_.profile.simdShare) {
+      int64_t threads = 0;
+      for (auto& kv : threadsOf_) threads = std::max(threads, kv.second);
+      share = (threads > 0 ? threads : 128) / 64.0 / 4.0;
+    }
+    const auto& perWave = CostProfile::perWaveFeatures();
     double total = 0;
     for (auto& kv : f) {
       auto w = opts_.profile.weights.find(kv.first);
-      total += (w == opts_.profile.weights.end() ? 0.0 : w->second) * kv.second;
+      const double scale =
+          std::find(perWave.begin(), perWave.end(), kv.first) != perWave.end() ? share : 1.0;
+      total += (w == opts_.profile.weights.end() ? 0.0 : w->second) * kv.second * scale;
     }
     return total;
   }

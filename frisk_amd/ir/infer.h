@@ -100,11 +100,18 @@ std::vector<MmaBinding> cdna4MmaBindings(int64_t m, int64_t n, int64_t k, Type i
 struct CostProfile {
   std::string id = "cdna4-layout-v1";
   std::map<std::string, double> weights;
+  // Per-wave features (MFMA, VALU, transcendental and cross-lane issue) are
+  // scaled by waves / 4 before weighting: the share of a CU's four SIMDs the
+  // workgroup's waves occupy, so the cost is in CU cycles per workgroup (the
+  // unit a profile fitted to kernel throughput is in).
+  bool simdShare = false;
   static CostProfile defaults();
-  // {"id": "...", "weights": {"feature": number, ...}}; unknown features are
-  // rejected (InvalidArgument).
+  // {"id": "...", "weights": {"feature": number, ...}, "simd_share": bool,
+  // "provenance": {...}}; unknown features or keys are rejected
+  // (InvalidArgument), "provenance" is read past.
   static CostProfile fromJson(const std::string& text);
   static const std::vector<std::string>& featureNames();
+  static const std::vector<std::string>& perWaveFeatures();
 };
 
 struct InferOptions {

@@ -7,7 +7,7 @@ same passes of this package, with their names and options:
 
   --frisk-normalize-layout-ir[='target=gfx950']
   --frisk-infer-layouts[='analysis-only dump-analysis exact-combination-limit=N
-                          beam-width=N max-expanded-states=N cost-profile=FILE
+                          beam-width=N max-expanded-states=N cost-profile=FILE|NAME
                           target=gfx950']
   --frisk-export-execution[='output=FILE minify']
 
@@ -15,7 +15,9 @@ Passes run in command-line order on the module read from the input file (or
 stdin, `-`).  The module is printed to stdout (or -o FILE) afterwards, as
 mlir-opt does; --frisk-export-execution without output= writes the packet to
 stdout instead of the module.  dump-analysis writes the constraint listing to
-stderr.  -verify-each verifies the module after every pass.  Errors go to
+stderr.  cost-profile= takes a profile file or the name of one shipped in
+frisk_amd/cost_profiles (e.g. cdna4-calibrated-v1, fitted to kernel times by
+frisk_amd/calibrate.py).  -verify-each verifies the module after every pass.  Errors go to
 stderr as `<file>:<line>:<col>: error: ...` (parse) or `error: ...` (passes)
 and the exit status is 1.
 
@@ -74,8 +76,8 @@ def run_pass(name: str, opts: dict, module, streams) -> bool:
         if name == "frisk-infer-layouts":
             profile = None
             if opts.get("cost-profile"):
-                with open(opts["cost-profile"]) as f:
-                    profile = f.read()
+                from .calibrate import load_profile
+                profile = load_profile(opts["cost-profile"])
             report = fr.infer_layouts(
                 module, opts.get("target"),
                 exact_combination_limit=_int(opts, "exact-combination-limit", 256),

@@ -1,0 +1,126 @@
+"""The calibrated cost profile (frisk_amd/calibrate.py) and the profile
+semantics layout inference gives it.
+
+The reference's calibrated SM90 model loads frozen coefficients from a
+profile file and names the model after the profile's SHA-256
+(lib/Dialect/Frisk/Target/SM90/SM90CalibratedCostModel.cpp:26-35,276-292);
+here the shipped profile is re-derived from the committed sweep of measured
+kernel times, so a change to the solver's features or to the fit shows up
+as a mismatch."""
+import json
+import subprocess
+import sys
+from pathlib import Path
+
+import pytest
+
+from frisk_amd import calibrate as C
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def _profile():
+    return json.loads(C.PROFILE_FILE.read_text())
+
+
+def test_shipped_profile_loads_by_name_id_and_path():
+    text = C.PROFILE_FILE.read_text()
+    pid = _profile()["id"]
+    assert pid.startswith("cdna4-calibrated-v1-")
+    for key in ("cdna4-calibrated-v1", "cdna4-calibrated-v1.json", pid, str(C.PROFILE_FILE)):
+        assert C.load_profile(key) == text
+    with pytest.raises(FileNotFoundError):
+        C.load_profile("no-such-profile")
+    r = C.staged_tile_report(128, 128, 64, "bf16", False, False, 256, None, text)
+    assert r["cost_model"] == pid and r["status"] == "materialized"
+
+
+def test_refit_reproduces_the_shipped_profile():
+    sweep = json.loads(C.SWEEP_FILE.read_text())
+    profile, report = C.fit(sweep, with_decisions=False)
+    shipped = _profile()
+    assert profile["weights"] == shipped["weights"]
+    assert profile["id"] == shipped["id"] and profile["simd_share"] is True
+    assert profile["provenance"] == shipped["provenance"]
+    # The id is the SHA-256 of the canonical weights.
+    import hashlib
+    digest = hashlib.sha256(C.canonical_weights(shipped["weights"]).encode()).hexdigest()
+    assert shipped["id"].endswith(digest[:16])
+    # The calibrated model predicts the measured CU cycles per workgroup far
+    # better than the hardware-rate profile does even at its best scale.
+    rms = lambda v: (sum(x * x for x in v) / len(v)) ** 0.5
+    assert rms(report["rel"]) < 0.2 and rms(report["rel"]) < 0.5 * rms(report["default_rel"])
+    assert rms(report["loo"]) < 0.2
+
+
+def test_sweep_rows_cover_every_variant_type_and_order():
+    rows = json.loads(C.SWEEP_FILE.read_text())["rows"]
+    gemm = {(r["dtype"], r["trans_a"], r["trans_b"], tuple(r["variant"])) for r in rows
+            if r["kind"] == "gemm"}
+    assert len(gemm) == len(C.GEMM_DTYPES) * len(C.ORDERS) * len(C.GEMM_VARIANTS)
+    assert {r["kernel"] for r in rows if r["kind"] == "gemm"} == {"gemm_w4", "gemm_128"}
+    attn = [r for r in rows if r["kind"] == "attention"]
+    assert len(attn) == len(C.ATTN_CASES) and any(r["causal"] for r in attn)
+    assert all(r["sclk_mhz"] and r["ms"] > 0 and r["pass_spread"] < 0.1 for r in rows)
+
+
+def test_simd_share_scales_per_wave_features():
+    only_mfma = {"mfma_cycles": 1.0, "lds_read_cycles": 0, "lds_write_cycles": 0,
+                 "global_lines": 0, "barriers": 0, "conversion_bytes": 0}
+    for threads in (128, 256):
+        plain = C.staged_tile_report(128, 128, 64, "bf16", False, False, threads, "Square",
+                                     json.dumps({"id": "p", "weights": only_mfma}))
+        share = C.staged_tile_report(128, 128, 64, "bf16", False, False, threads, "Square",
+                                     json.dumps({"id": "s", "weights": only_mfma,
+                                                 "simd_share": True,
+                                                 "provenance": {"a": [1, "x", {"b": None}],
+                                                                "c": False}}))
+        mfma = plain["features"]["mfma_cycles"]
+        assert plain["cost"] == mfma
+        assert share["cost"] == mfma * threads / 64 / 4
+        # Reported features stay per wave.
+        assert share["features"] == plain["features"]
+
+
+@pytest.mark.parametrize("text,match", [('{"simd_share": 1}', "true or false"),
+                                        ('{"extra": 1}', "unknown key"),
+                                        ('{"provenance": {"a": }}', "expected a number"),
+                                        ('{"weights": {"mfma_cycles": -1}}', ">= 0")])
+def test_profile_parse_errors(text, match):
+    with pytest.raises(ValueError, match=match):
+        C.staged_tile_report(128, 128, 64, "bf16", False, False, 256, None, text)
+
+
+def test_gemm_row_features_check_the_variant():
+    f, contract = C.gemm_row_features((128, 2, 1), "bf16", True, True, 64, 4096)
+    assert "wave_grid" in contract and f["mfma_cycles"] == 64 * 1024
+    # Per stage the tile streams A and B (2 x 128 x 64 bf16 = 256 lines) and
+    # the epilogue stores the f32 tile once (512 lines).
+    assert f["global_lines"] == 64 * 256 + 512
+
+
+@pytest.mark.parametrize("b,h,s,causal,waves", [(4, 32, 4096, False, 8), (8, 8, 1024, False, 8),
+                                                (2, 32, 1025, False, 4), (1, 16, 2048, False, 4),
+                                                (4, 32, 4096, True, 4)])
+def test_attention_shape_follows_the_launch_rule(b, h, s, causal, waves):
+    # The launch rule's own measured cases (b4 h32 s4096 and b8 h8 s1024
+    # keep 8 waves; b2 h32 s1025 and b1 h16 s2048 take 4).
+    w, wgs, blocks = C.attention_shape(b, h, s, causal)
+    assert w == waves and wgs == b * h * -(-s // (32 * w))
+    if causal:
+        assert blocks == pytest.approx(sum(2 * (i + 1) for i in range(s // 128)) / (s // 128))
+    else:
+        assert blocks == -(-s // 64)
+
+
+def test_opt_driver_takes_a_shipped_profile(tmp_path):
+    src = ROOT / "tests" / "lit" / "normalize-and-export.mlir"
+    text = "\n".join(l for l in src.read_text().splitlines() if not l.startswith("//"))
+    inp = tmp_path / "in.mlir"
+    inp.write_text(text)
+    r = subprocess.run([sys.executable, "-m", "frisk_amd.opt", str(inp),
+                        "--frisk-normalize-layout-ir=target=gfx950",
+                        "--frisk-infer-layouts=target=gfx950 cost-profile=cdna4-calibrated-v1"],
+                       cwd=ROOT, capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    assert f'frisk.layout_cost_model = "{_profile()["id"]}"' in r.stdout
