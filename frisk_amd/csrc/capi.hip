@@ -342,7 +342,11 @@ int frisk_gemm_plan(const frisk_gemm_desc* d, char* buf, int64_t len) {
     const frisk::MfmaChoice c = frisk::gemm_mfma_choice(g, cus, ws);
     const int tile = c.big ? 256 : 128;
     const int wm = c.big || !g.tile ? 2 : g.wave_m, wn = c.big || !g.tile ? 2 : g.wave_n;
-    const int stage = c.big ? 128 : 64;
+    const int64_t tiles128 = ((g.m + 127) / 128) * ((g.n + 127) / 128);
+    const int stage = c.big ? 128
+                      : g.tile ? 64
+                      : c.slices > 1 ? (tiles128 * c.slices <= cus && c.kb_slice % 128 == 0 ? 128 : 64)
+                                     : frisk::gemm_128_stage_bytes(g, cus);
     // The workgroup tile's instruction contract in the solver's syntax
     // (#frisk.mma_contract): the 256x256 kernel feeds the B fragment as the
     // MFMA's first operand (swapped), the 128x128 kernel does not.

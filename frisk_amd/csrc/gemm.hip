@@ -124,21 +124,28 @@ SplitPlan gemm_split_plan(const GemmArgs& g, int cus) {
   if (tiles256 >= cus / 2) return p;
   const int64_t tiles = ((g.m + 127) / 128) * ((g.n + 127) / 128);
   const int64_t kb = g.k * 2;
-  // 128x128 tiles.  Split only grids that leave CUs without a tile: slices
-  // until two workgroups per CU, each slice at least 8 stages (8 x 64 B of
-  // K), and the f32 partials at most a quarter of the bytes of A and B
-  // (their second pass then costs little).  Measured on the projection
-  // sweep: M = 128 runs 1.6-4.8x faster than on the unsplit small-M kernel
-  // (17.0 us at N = K = 4096 with 4 slices, against 24.0 with 16); M = 1024,
-  // N = 4096 (256 tiles) runs 1.3x slower split in two.
+  // 128x128 tiles.  Split only grids that leave CUs without a tile, each
+  // slice at least 8 stages, and the f32 partials at most a quarter of the
+  // bytes of A and B (their second pass then costs little).  Grids of at
+  // most half as many tiles as CUs take slices up to one workgroup per CU,
+  // on 128-byte stages (the launch picks them when slices fit one
+  // workgroup per CU); larger grids take slices up to two workgroups per
+  // CU on 64-byte stages.  Measured on the projection sweep: M = 128 runs
+  // 1.6-4.8x faster than on the unsplit small-M kernel; with operands from
+  // HBM, 128 x 4096 x 14336 323 -> 416 TFLOP/s and 128 x 14336 x 4096
+  // 334 -> 373 on 128-byte stages (one workgroup per CU) against 64-byte
+  // ones (two); M = 1024, N = 4096 (256 tiles) runs 1.3x slower split in
+  // two.
   if (tiles < cus) {
-    int64_t slices = (2 * (int64_t)cus + tiles - 1) / tiles;
-    slices = std::min<int64_t>(slices, kb / (8 * kRow));
+    const bool deep = 2 * tiles <= cus;
+    const int64_t row = deep ? 128 : kRow;  // bytes of K per stage
+    int64_t slices = deep ? cus / tiles : (2 * (int64_t)cus + tiles - 1) / tiles;
+    slices = std::min<int64_t>(slices, kb / (8 * row));
     slices = std::min<int64_t>(slices, (g.m + g.n) * kb / (16 * g.m * g.n));
     slices = std::min<int64_t>(slices, 64);
     if (slices >= 2) {
-      const int64_t chunks = (kb + kRow - 1) / kRow;  // slices start on stage boundaries
-      p.kb_slice = ((chunks + slices - 1) / slices) * kRow;
+      const int64_t chunks = (kb + row - 1) / row;  // slices start on stage boundaries
+      p.kb_slice = ((chunks + slices - 1) / slices) * row;
       p.slices = (int)((kb + p.kb_slice - 1) / p.kb_slice);
       if (p.slices < 2) p = SplitPlan{1, kb, 0, false};
     }

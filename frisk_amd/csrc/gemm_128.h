@@ -10,9 +10,15 @@
 //  * 128x128 output tile per 256-thread workgroup (4 waves, 2x2), each wave
 //    owning a 64x64 sub-tile as 2x2 v_mfma 32x32 accumulators; two
 //    workgroups share a CU.
-//  * K is consumed in stages of 64 bytes per row (32 bf16/f16, 64 fp8/i8),
-//    loaded by LDS-DMA (buffer_load_dwordx4 ... lds: no VGPRs stage the
-//    data) into kStages rotating LDS slots, one barrier per stage.
+//  * K is consumed in stages of KROW bytes per row, loaded by LDS-DMA
+//    (buffer_load_dwordx4 ... lds: no VGPRs stage the data) into kStages
+//    rotating LDS slots, one barrier per stage.  KROW = 64 (32 bf16/f16,
+//    64 fp8/i8; 64 KiB of LDS, two workgroups per CU) or 128 (one whole
+//    128-byte line per row segment, 128 KiB, one workgroup per CU).  A row
+//    segment of 64 bytes is half a cache line, whose other half the next
+//    stage fetches again; with operands streamed from HBM that costs the
+//    single-workgroup grids most (1024 x 4096 x 4096 bf16, operands not in
+//    any cache: 668 -> 846 TFLOP/s with 128-byte stages).
 //  * Operand tiles, their XOR swizzles and the fragment reads for either
 //    storage order of A and B (template flags AM / BM, MN-major when set)
 //    are those of gemm_tile.h.  For the K-major 64 B rows the swizzle is
@@ -38,21 +44,22 @@ namespace frisk {
 
 namespace g128 {
 
-constexpr int kRow = 64;  // bytes of K per row per stage
 #ifndef FRISK_GEMM_STAGES
 #define FRISK_GEMM_STAGES 4
 #endif
 constexpr int kStages = FRISK_GEMM_STAGES;
-// LDS bytes of a BT x BT tile pipeline: kStages stages of (A, B) tiles.
-constexpr int lds_bytes(int bt) { return kStages * 2 * bt * kRow; }
+// LDS bytes of a BT x BT tile pipeline: kStages stages of (A, B) tiles of
+// krow bytes of K per row.
+constexpr int lds_bytes(int bt, int krow) { return kStages * 2 * bt * krow; }
 // LDS bytes of one workgroup with a WM x WN wave grid: the pipeline, or the
 // epilogue's staging (each wave 32 rows of 32 TN + 4 32-bit values) when
 // that is larger (the 4x1 grid).
-constexpr int lds_bytes_grid(int bt, int wm, int wn) {
+constexpr int lds_bytes_grid(int bt, int wm, int wn, int krow) {
   const int epi = wm * wn * 32 * (bt / wn + 4) * 4;
-  return lds_bytes(bt) > epi ? lds_bytes(bt) : epi;
+  return lds_bytes(bt, krow) > epi ? lds_bytes(bt, krow) : epi;
 }
-static_assert(2 * lds_bytes_grid(128, 4, 1) <= 160 * 1024, "two 128x128 workgroups per CU");
+static_assert(2 * lds_bytes_grid(128, 4, 1, 64) <= 160 * 1024, "two 128x128 workgroups per CU");
+static_assert(lds_bytes_grid(128, 4, 1, 128) <= 160 * 1024, "one 128x128 workgroup per CU");
 
 }  // namespace g128
 
@@ -62,7 +69,7 @@ static_assert(2 * lds_bytes_grid(128, 4, 1) <= 160 * 1024, "two 128x128 workgrou
 // Split-K: blockIdx.y is a K slice of kb_slice bytes; the slice's A and B
 // start kb_slice bytes of K further per slice, and its output is the tile
 // of C c_slice_bytes * y bytes further (the f32 partial of that slice).
-template <Elt IN, Elt OUT, bool AM, bool BM, int BT, int WM, int WN>
+template <Elt IN, Elt OUT, bool AM, bool BM, int BT, int WM, int WN, int KROW>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_128(const char* __restrict__ A,
                                                               const char* __restrict__ B,
                                                               void* __restrict__ C, int M, int N,
@@ -72,7 +79,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_128(const char* __rest
                                                               int64_t c_slice_bytes) {
   // The body is device code only; the host pass just needs the kernel stub.
 #if defined(__HIP_DEVICE_COMPILE__)
-  constexpr int kRow = g128::kRow, kStages = g128::kStages;
+  constexpr int kRow = KROW, kStages = g128::kStages;
   using TA = OpTile<IN, AM, BT, kRow>;
   using TB = OpTile<IN, BM, BT, kRow>;
   A += TA::slice_shift((int64_t)blockIdx.y * kb_slice, lda_b);
@@ -86,10 +93,10 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_128(const char* __rest
   constexpr int kBM = BT, kBN = BT;
   constexpr int kTileBytes = BT * kRow;  // one operand, one stage
   constexpr int kStageBytes = 2 * kTileBytes;
-  constexpr int kLdsBytes = g128::lds_bytes_grid(BT, WM, WN);
+  constexpr int kLdsBytes = g128::lds_bytes_grid(BT, WM, WN, KROW);
   constexpr int TM = kBM / WM / 32, TN = kBN / WN / 32;
   constexpr int kLaneChunks = TA::kLaneChunks;         // 16 B pieces per lane per MFMA
-  constexpr int kSteps = kRow / Op::kBytes;            // MFMA k-steps per stage (2 or 1)
+  constexpr int kSteps = kRow / Op::kBytes;            // MFMA k-steps per stage (1 to 4)
   constexpr int kBlocks = kTileBytes / 1024 / kWaves;  // 1 KiB DMA blocks per wave per operand
   constexpr int kLoads = 2 * kBlocks;                  // DMA loads per lane per stage
   constexpr int kFragReads =                           // LDS reads per lane per k-step
@@ -267,11 +274,11 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_128(const char* __rest
 #endif  // __HIP_DEVICE_COMPILE__
 }
 
-template <Elt IN, Elt OUT, bool AM, bool BM, int WM = 2, int WN = 2>
+template <Elt IN, Elt OUT, bool AM, bool BM, int WM = 2, int WN = 2, int KROW = 64>
 static hipError_t launch_128(const GemmArgs& g, hipStream_t stream) {
   constexpr int kEsz = EltInfo<IN>::bytes;
-  constexpr int kLds = g128::lds_bytes_grid(128, WM, WN);
-  auto kern = gemm_mfma_128<IN, OUT, AM, BM, 128, WM, WN>;
+  constexpr int kLds = g128::lds_bytes_grid(128, WM, WN, KROW);
+  auto kern = gemm_mfma_128<IN, OUT, AM, BM, 128, WM, WN, KROW>;
   // Thread-safe one-time opt-in to more than 64 KiB of dynamic LDS.
   static const hipError_t attr =
       hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
@@ -287,12 +294,12 @@ static hipError_t launch_128(const GemmArgs& g, hipStream_t stream) {
 // Split-K on 128x128 tiles: f32 partial tiles of each K slice into
 // `partial` ([slices][M][N]), then their sum in slice order into C
 // (bf16 / f16 inputs, scale 1).
-template <Elt IN, bool AM, bool BM>
-static hipError_t launch_128_split(const GemmArgs& g, int slices, int64_t kb_slice, float* partial,
-                                   hipStream_t stream) {
+template <Elt IN, bool AM, bool BM, int KROW>
+static hipError_t launch_128_split_k(const GemmArgs& g, int slices, int64_t kb_slice,
+                                     float* partial, hipStream_t stream) {
   constexpr int kEsz = EltInfo<IN>::bytes;
-  constexpr int kLds = g128::lds_bytes_grid(128, 2, 2);
-  auto kern = gemm_mfma_128<IN, Elt::F32, AM, BM, 128, 2, 2>;
+  constexpr int kLds = g128::lds_bytes_grid(128, 2, 2, KROW);
+  auto kern = gemm_mfma_128<IN, Elt::F32, AM, BM, 128, 2, 2, KROW>;
   static const hipError_t attr =
       hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
   if (attr != hipSuccess) return attr;
@@ -306,6 +313,17 @@ static hipError_t launch_128_split(const GemmArgs& g, int slices, int64_t kb_sli
   return gemm_splitk_sum(partial, slices, g, stream);
 }
 
+// 128-byte stages when the slices are at most one workgroup per CU (the
+// split plan then cuts K on 128-byte boundaries), else 64-byte stages.
+template <Elt IN, bool AM, bool BM>
+static hipError_t launch_128_split(const GemmArgs& g, int slices, int64_t kb_slice, float* partial,
+                                   hipStream_t stream) {
+  const int64_t tiles = ((g.m + 127) / 128) * ((g.n + 127) / 128);
+  if (tiles * slices <= device_cus() && kb_slice % 128 == 0)
+    return launch_128_split_k<IN, AM, BM, 128>(g, slices, kb_slice, partial, stream);
+  return launch_128_split_k<IN, AM, BM, 64>(g, slices, kb_slice, partial, stream);
+}
+
 template <bool AM, bool BM>
 hipError_t gemm_128_split_layout(const GemmArgs& g, int slices, int64_t kb_slice, float* partial,
                                  hipStream_t s) {
@@ -316,19 +334,28 @@ hipError_t gemm_128_split_layout(const GemmArgs& g, int slices, int64_t kb_slice
 
 #define FRISK_PAIR(i, o) (((int)(i) << 8) | (int)(o))
 
-template <bool AM, bool BM>
-hipError_t gemm_128_layout(const GemmArgs& g, hipStream_t s) {
+template <bool AM, bool BM, int KROW>
+static hipError_t gemm_128_pairs(const GemmArgs& g, hipStream_t s) {
   switch (FRISK_PAIR(g.in, g.out)) {
-    case FRISK_PAIR(Elt::BF16, Elt::BF16): return launch_128<Elt::BF16, Elt::BF16, AM, BM>(g, s);
-    case FRISK_PAIR(Elt::BF16, Elt::F32): return launch_128<Elt::BF16, Elt::F32, AM, BM>(g, s);
-    case FRISK_PAIR(Elt::F16, Elt::F16): return launch_128<Elt::F16, Elt::F16, AM, BM>(g, s);
-    case FRISK_PAIR(Elt::F16, Elt::F32): return launch_128<Elt::F16, Elt::F32, AM, BM>(g, s);
-    case FRISK_PAIR(Elt::E4M3, Elt::BF16): return launch_128<Elt::E4M3, Elt::BF16, AM, BM>(g, s);
-    case FRISK_PAIR(Elt::E4M3, Elt::F16): return launch_128<Elt::E4M3, Elt::F16, AM, BM>(g, s);
-    case FRISK_PAIR(Elt::E4M3, Elt::F32): return launch_128<Elt::E4M3, Elt::F32, AM, BM>(g, s);
-    case FRISK_PAIR(Elt::I8, Elt::I32): return launch_128<Elt::I8, Elt::I32, AM, BM>(g, s);
+    case FRISK_PAIR(Elt::BF16, Elt::BF16): return launch_128<Elt::BF16, Elt::BF16, AM, BM, 2, 2, KROW>(g, s);
+    case FRISK_PAIR(Elt::BF16, Elt::F32): return launch_128<Elt::BF16, Elt::F32, AM, BM, 2, 2, KROW>(g, s);
+    case FRISK_PAIR(Elt::F16, Elt::F16): return launch_128<Elt::F16, Elt::F16, AM, BM, 2, 2, KROW>(g, s);
+    case FRISK_PAIR(Elt::F16, Elt::F32): return launch_128<Elt::F16, Elt::F32, AM, BM, 2, 2, KROW>(g, s);
+    case FRISK_PAIR(Elt::E4M3, Elt::BF16): return launch_128<Elt::E4M3, Elt::BF16, AM, BM, 2, 2, KROW>(g, s);
+    case FRISK_PAIR(Elt::E4M3, Elt::F16): return launch_128<Elt::E4M3, Elt::F16, AM, BM, 2, 2, KROW>(g, s);
+    case FRISK_PAIR(Elt::E4M3, Elt::F32): return launch_128<Elt::E4M3, Elt::F32, AM, BM, 2, 2, KROW>(g, s);
+    case FRISK_PAIR(Elt::I8, Elt::I32): return launch_128<Elt::I8, Elt::I32, AM, BM, 2, 2, KROW>(g, s);
     default: return hipErrorInvalidValue;
   }
+}
+
+// The library's own 128x128 launch: 128-byte stages when the grid is at
+// most one workgroup per CU, 64-byte stages (two workgroups per CU)
+// otherwise.  Both sum K in the same order, so the choice changes no bit.
+template <bool AM, bool BM>
+hipError_t gemm_128_layout(const GemmArgs& g, hipStream_t s) {
+  if (gemm_128_stage_bytes(g, device_cus()) == 128) return gemm_128_pairs<AM, BM, 128>(g, s);
+  return gemm_128_pairs<AM, BM, 64>(g, s);
 }
 
 template <bool AM, bool BM, int WM, int WN>

@@ -64,8 +64,15 @@ template <bool AM, bool BM>
 hipError_t gemm_w4_split_layout(const GemmArgs& g, int slices, int64_t kb_slice, float* partial,
                                 hipStream_t s);
 template <bool AM, bool BM> hipError_t gemm_128_layout(const GemmArgs& g, hipStream_t s);
+// Bytes of K per row per pipeline stage of gemm_128_layout's launch: 128
+// when its grid of 128x128 tiles is at most one workgroup per CU, else 64
+// (two workgroups per CU fit in LDS).
+inline int gemm_128_stage_bytes(const GemmArgs& g, int cus) {
+  const int64_t tiles = ((g.m + 127) / 128) * ((g.n + 127) / 128);
+  return tiles <= cus ? 128 : 64;
+}
 // The 128x128 kernel with the wave grid g.wave_m x g.wave_n (2x2, 4x1, 1x4,
-// 2x1 or 1x2).
+// 2x1 or 1x2), 64-byte stages.
 template <bool AM, bool BM> hipError_t gemm_128_grid_layout(const GemmArgs& g, hipStream_t s);
 template <bool AM, bool BM>
 hipError_t gemm_128_split_layout(const GemmArgs& g, int slices, int64_t kb_slice, float* partial,

@@ -39,20 +39,24 @@ def run(a, b, c, ta, tb, sa=1.0, sb=1.0, kernel=None, **kw):
     return p
 
 
-# (m, n, k, kernel): 256x256 tiles (at least 128 of them) with ragged edges
-# in M and N and a K tail inside the last stage; 128x128 tiles likewise.
+# (m, n, k, kernel, stage bytes): 256x256 tiles (at least 128 of them) with
+# ragged edges in M and N and a K tail inside the last stage; 128x128 tiles
+# likewise, on a grid of at most one workgroup per CU (128-byte stages) and
+# on a larger one (299 tiles: 64-byte stages, two workgroups per CU).
 # Every extent keeps 16 B row pitches for 8-bit M/N-major storage.
-SHAPES = [(2064, 4000, 1008, "gemm_w4"), (304, 528, 784, "gemm_128")]
+SHAPES = [(2064, 4000, 1008, "gemm_w4", 128), (304, 528, 784, "gemm_128", 128),
+          (1552, 2832, 528, "gemm_128", 64)]
 
 
 @pytest.mark.parametrize("in_dt,out_dt", MFMA_PAIRS, ids=PAIR_IDS)
 @pytest.mark.parametrize("ta,tb", LAYOUTS, ids=LAYOUT_IDS)
-@pytest.mark.parametrize("m,n,k,kernel", SHAPES, ids=["w4", "t128"])
-def test_every_layout_and_type_on_mfma(m, n, k, kernel, in_dt, out_dt, ta, tb):
+@pytest.mark.parametrize("m,n,k,kernel,stage", SHAPES, ids=["w4", "t128", "t128s64"])
+def test_every_layout_and_type_on_mfma(m, n, k, kernel, stage, in_dt, out_dt, ta, tb):
     print(f"case layout ta={ta} tb={tb} {in_dt}->{out_dt} m={m} n={n} k={k}", flush=True)
     a, b, sa, sb = make_operands(m, n, k, in_dt, ta, tb, seed=m + n + 3 * ta + 5 * tb)
     c = torch.empty(m, n, dtype=out_dt, device="cuda")
     p = run(a, b, c, ta, tb, sa, sb, kernel=kernel, workspace=False)
+    assert p["stage_bytes"] == stage, p
     assert p["a_major"] == ("m" if ta else "k") and p["b_major"] == ("k" if tb else "n")
     r = sample_rows(m, 48, seed=k) if kernel == "gemm_w4" else None
     ref = reference(a, b, ta, tb, sa, sb, rows=r)
@@ -220,13 +224,18 @@ def test_requested_kernel_variants(variant, in_dt, out_dt, ta, tb):
 
 def test_variants_agree_bitwise_on_one_grid():
     # Every 128x128 wave grid sums each output over the same k order, so the
-    # grids give identical bits (only the placement of work differs).
+    # grids give identical bits (only the placement of work differs); so does
+    # the library's own launch of this grid (20 tiles: 128-byte stages, where
+    # the requested variants run 64-byte stages).
     m, n, k = 512, 640, 1024
     a, b, _, _ = make_operands(m, n, k, torch.bfloat16, False, True, seed=5)
     outs = []
-    for v in VARIANTS[1:]:
+    for v in VARIANTS[1:] + [None]:
         c = torch.empty(m, n, dtype=torch.float32, device="cuda")
-        rt.gemm(a, b, c, trans_b=True, variant=v)
+        if v is None:
+            p = rt.gemm_plan(a, b, c, trans_b=True, workspace=False)
+            assert p["kernel"] == "gemm_128" and p["stage_bytes"] == 128, p
+        rt.gemm(a, b, c, trans_b=True, variant=v, workspace=False)
         outs.append(c)
     torch.cuda.synchronize()
     for c in outs[1:]:
