@@ -13,6 +13,12 @@
 //    per load instruction.  Batches of U k-steps are double-buffered: batch
 //    b+1 is loaded while batch b is multiplied (operands from HBM:
 //    64x4096x4096 33.0 -> 24.5 us, 16x4096x4096 13.9 -> 11.9 us).
+//  * A batch of kSkinnyWaves * U k-steps gives wave w the k-step pairs
+//    (2w, 2w+1), (2w+8, 2w+9), ...: the two 64 B halves of each 128 B line
+//    are loaded by one wave back to back (the per-workgroup rotation is
+//    even, so pairs stay aligned).  Operands from HBM, TFLOP/s, against
+//    interleaving single k-steps over the waves: 16x4096x4096 45.4 -> 47.8,
+//    16x14336x4096 65.4 -> 68.0, 16x4096x14336 60.3 -> 61.7.
 //  * W rows and the K tail are bounds-checked by raw buffer loads (offsets
 //    past num_records read zeros); X rows past M are clamped (their outputs
 //    are not stored).
@@ -100,16 +106,17 @@ __global__ __launch_bounds__(64 * kSkinnyWaves) void gemm_skinny_kernel(
   const int all_steps = (Kb + 63) / 64;
   const int s_begin = blockIdx.z * steps_per_slice;
   const int nsteps = min(all_steps - s_begin, steps_per_slice);
-  const int rot = (int)(((unsigned)blockIdx.x * 5u + (unsigned)blockIdx.y * 3u) % (unsigned)nsteps);
+  const int rot = (int)(((unsigned)blockIdx.x * 5u + (unsigned)blockIdx.y * 3u) % (unsigned)nsteps) & ~1;
   const int kmax = Kb - quad * 16;    // this lane's 16 B chunk is live while kb < kmax
   // Batches of U k-steps, double-buffered: the loads of batch b+1 are in
   // flight while batch b is multiplied, so a workgroup pays one memory
   // latency per slice instead of one per batch.  Batches past the end load
   // nothing (zero reads) and add zero products.
-  auto load = [&](int s0, i32x4 (&av)[U][TM], i32x4 (&bv)[U][TN]) {
+  static_assert(U % 2 == 0, "k-step pairs");
+  auto load = [&](int b0, i32x4 (&av)[U][TM], i32x4 (&bv)[U][TN]) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int st = s0 + kSkinnyWaves * u;
+      const int st = b0 + 2 * wave + (u & 1) + 2 * kSkinnyWaves * (u >> 1);
       int sr = st + rot;
       if (sr >= nsteps) sr -= nsteps;
       const int kb = (s_begin + sr) * 64;
@@ -134,8 +141,8 @@ __global__ __launch_bounds__(64 * kSkinnyWaves) void gemm_skinny_kernel(
   };
   constexpr int kBatch = kSkinnyWaves * U;
   i32x4 a0[U][TM], b0[U][TN], a1[U][TM], b1[U][TN];
-  load(wave, a0, b0);
-  for (int s0 = wave; s0 < nsteps; s0 += 2 * kBatch) {
+  load(0, a0, b0);
+  for (int s0 = 0; s0 < nsteps; s0 += 2 * kBatch) {
     load(s0 + kBatch, a1, b1);
     mul(a0, b0);
     if (s0 + kBatch >= nsteps) break;
