@@ -55,7 +55,6 @@ from __future__ import annotations
 import argparse
 import hashlib
 import json
-import math
 import sys
 import time
 from pathlib import Path
@@ -255,10 +254,10 @@ def attention_shape(b: int, h: int, s: int, causal: bool, cus: int = 256) -> Tup
 
 
 def row_features(row: dict) -> dict:
+    """The solver's features of one workgroup of a sweep row."""
     if row["kind"] == "gemm":
-        f, contract = gemm_row_features(tuple(row["variant"]), row["dtype"], row["trans_a"],
-                                        row["trans_b"], row["bk"], row["k"])
-        return f
+        return gemm_row_features(tuple(row["variant"]), row["dtype"], row["trans_a"],
+                                 row["trans_b"], row["bk"], row["k"])[0]
     return attention_row_features(row["d"], row["dtype"], row["waves"], row["key_blocks"])
 
 

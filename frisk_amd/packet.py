@@ -32,7 +32,6 @@ from __future__ import annotations
 
 import json
 import re
-from typing import Any
 
 from . import variants
 
