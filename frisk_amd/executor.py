@@ -42,7 +42,8 @@ naming the first mismatch.  There is no CPU fallback.
 from __future__ import annotations
 
 import math
-from dataclasses import dataclass
+from dataclasses import dataclass, field
+from functools import lru_cache
 from typing import Optional, Sequence
 
 from . import _ir, tileprog, variants
@@ -68,6 +69,9 @@ class GemmPlan:
     variant: Optional[tuple] = None
     layouts_match: bool = False
     mismatch: str = ""
+    # The program's workgroup tile (bm, bn, bk, dtype, policy, threads), or
+    # None for a whole-matrix program.
+    tile: Optional[tuple] = field(default=None, repr=False)
 
 
 @dataclass
@@ -303,11 +307,10 @@ def _gemm_tiled(ops, entry) -> GemmPlan:
               f"A{a_shape} B{b_shape} C{c_shape} exactly")
     if _elem(a_t) != _elem(a_src) or _elem(b_t) != _elem(b_src):
         _fail("A/B tiles must keep the input dtype")
-    p = GemmPlan(ia, ib, ic, ta, tb, True, M, N, K)
-    policy = gop.get_attr("policy")
     names = {"f16": "fp16", "bf16": "bf16", "f8E4M3FN": "e4m3fn", "i8": "int8", "f32": "fp32"}
-    p._tile = (bm, bn, bk, names.get(_elem(a_t), _elem(a_t)), policy, par.get_thread_num())
-    return p
+    tile = (bm, bn, bk, names.get(_elem(a_t), _elem(a_t)), gop.get_attr("policy"),
+            par.get_thread_num())
+    return GemmPlan(ia, ib, ic, ta, tb, True, M, N, K, tile=tile)
 
 
 # ---------------------------------------------------------------------------
@@ -432,42 +435,42 @@ def _attention(ops, entry) -> AttnPlan:
 
 
 # ---------------------------------------------------------------------------
-_CONTRACTS: dict = {}
-
-
 def tile_contract(bm: int, bn: int, bk: int, dtype: str, trans_a: bool, trans_b: bool,
                   threads: int, policy=None):
     """(contract, reason) of the workgroup tile product C[bm, bn] += op(A).op(B)
     (A, B tiles in Shared memory, f32 accumulator, `threads` lanes, warp
     `policy`): the `#frisk.mma_contract` layout inference binds for it, or
     (None, reason) when inference finds none."""
-    key = (bm, bn, bk, dtype, bool(trans_a), bool(trans_b), threads, str(policy))
-    if key not in _CONTRACTS:
-        try:
-            from .common import utils
-            s = utils.create_session()
-            S = ir.MemorySpace.SHARED
-            acc_t = "int32" if dtype == "int8" else "fp32"
-            _, entry = s.new_kernel("tile", [
-                s.memref_type([bk, bm] if trans_a else [bm, bk], dtype, space=S),
-                s.memref_type([bn, bk] if trans_b else [bk, bn], dtype, space=S),
-                s.memref_type([bm, bn], acc_t)])
-            acc = s.alloc_buffer([bm, bn], acc_t)
-            g = s.create_gemm(entry.get_argument(0), entry.get_argument(1), acc, trans_a=trans_a,
-                              trans_b=trans_b, clear_accum=True, legacy_semantics="tensor_v1")
-            if policy is not None:
-                g.set_attr("policy", s.builder.get_gemm_warp_policy_attr(policy))
-            g.set_attr("frisk.execution_threads", s.builder.get_int64_attr(threads))
-            s.builder.create_copy_op(acc, entry.get_argument(2), [], [])
-            fr.normalize_layout_ir(s.module, "gfx950")
-            rep = fr.infer_layouts(s.module)
-            if rep.get("status") != "materialized":
-                raise ValueError(f"layout inference {rep.get('status')}: {rep.get('failure', '')}")
-            found = [a for a in rep["assignments"] if a.startswith("mma#")]
-            _CONTRACTS[key] = (found[0].split(": ", 1)[1], "")
-        except Exception as e:  # reported as the reason; the GEMM still runs
-            _CONTRACTS[key] = (None, f"no instruction contract: {e}")
-    return _CONTRACTS[key]
+    return _tile_contract(bm, bn, bk, dtype, bool(trans_a), bool(trans_b), threads,
+                          None if policy is None else str(policy), policy)
+
+
+@lru_cache(maxsize=256)
+def _tile_contract(bm, bn, bk, dtype, trans_a, trans_b, threads, policy_key, policy):
+    try:
+        from .common import utils
+        s = utils.create_session()
+        S = ir.MemorySpace.SHARED
+        acc_t = "int32" if dtype == "int8" else "fp32"
+        _, entry = s.new_kernel("tile", [
+            s.memref_type([bk, bm] if trans_a else [bm, bk], dtype, space=S),
+            s.memref_type([bn, bk] if trans_b else [bk, bn], dtype, space=S),
+            s.memref_type([bm, bn], acc_t)])
+        acc = s.alloc_buffer([bm, bn], acc_t)
+        g = s.create_gemm(entry.get_argument(0), entry.get_argument(1), acc, trans_a=trans_a,
+                          trans_b=trans_b, clear_accum=True, legacy_semantics="tensor_v1")
+        if policy is not None:
+            g.set_attr("policy", s.builder.get_gemm_warp_policy_attr(policy))
+        g.set_attr("frisk.execution_threads", s.builder.get_int64_attr(threads))
+        s.builder.create_copy_op(acc, entry.get_argument(2), [], [])
+        fr.normalize_layout_ir(s.module, "gfx950")
+        rep = fr.infer_layouts(s.module)
+        if rep.get("status") != "materialized":
+            raise ValueError(f"layout inference {rep.get('status')}: {rep.get('failure', '')}")
+        found = [a for a in rep["assignments"] if a.startswith("mma#")]
+        return found[0].split(": ", 1)[1], ""
+    except (ValueError, RuntimeError) as e:  # reported as the reason; the GEMM still runs
+        return None, f"no instruction contract: {e}"
 
 
 def _bind_variant(p: "GemmPlan", tile) -> "GemmPlan":
@@ -502,7 +505,7 @@ def plan(module, kernel: str):
                       tileprog.plan_tiled):
         try:
             p = recognise(ops, entry)
-            return _bind_variant(p, getattr(p, "_tile", None)) if isinstance(p, GemmPlan) else p
+            return _bind_variant(p, p.tile) if isinstance(p, GemmPlan) else p
         except (_Reject, tileprog.Reject) as e:
             reasons.append(f"{recognise.__name__.lstrip('_')}: {e}")
     raise ValueError(f"execute: kernel @{kernel} is not a recognised GEMM, attention or tile-op "
