@@ -118,11 +118,17 @@ template <int D> struct AttnGeom {
 };
 
 __device__ __forceinline__ float pair_reduce(float x, bool max_op) {
-  // Combines lane l with lane l^32 (ds_bpermute).  The v_permlane32_swap
-  // builtin of this toolchain returns the vdst register for both of its
-  // results, so it is not used.
-  const float y = __shfl_xor(x, 32);
-  return max_op ? fmaxf(x, y) : x + y;
+  // Combines lane l with lane l^32 without the LDS pipe: v_permlane32_swap
+  // of x with itself leaves x[l % 32] in one result and x[l % 32 + 32] in
+  // the other, on every lane (every attention parity test depends on it).  A
+  // ds_bpermute here made the softmax wait, through the in-order LDS
+  // counter, for the Vᵀ fragment reads issued before it.  max and + are
+  // commutative, so every lane gets the bits the exchange gave before.
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  const float a = __builtin_bit_cast(float, (uint32_t)r[0]);
+  const float b = __builtin_bit_cast(float, (uint32_t)r[1]);
+  return max_op ? fmaxf(a, b) : a + b;
 }
 
 }  // namespace
@@ -295,14 +301,16 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(
     };
     // V^T fragments of key steps k0, k0+1 (16 keys each).
     auto read_v = [&](const char* ks, int k0, i32x4 (&vf)[2][G::kDT]) {
-      typedef short s16x4 __attribute__((ext_vector_type(4)));
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int dt = 0; dt < G::kDT; ++dt) {
           const char* p = ks + vt_off[dt] + (k0 + i) * 16 * G::kRV;
-          const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((s16x4*)p);
-          const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((s16x4*)(p + 8 * G::kRV));
+          // Through the restrict-pointer helper: a bare intrinsic here
+          // waited for the next block's K/V DMA (vmcnt(0)) before the first
+          // read (C5 non-causal 1063 -> 1098 TFLOP/s without that wait).
+          const s16x4 lo = lds_read_tr16(p);
+          const s16x4 hi = lds_read_tr16(p + 8 * G::kRV);
           typedef int i32x2 __attribute__((ext_vector_type(2)));
           const i32x2 a = __builtin_bit_cast(i32x2, lo), b = __builtin_bit_cast(i32x2, hi);
           vf[i][dt] = i32x4{a[0], a[1], b[0], b[1]};

@@ -52,27 +52,6 @@
 
 namespace frisk {
 
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
-typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-
-// Transposing LDS reads through a restrict pointer.  The intrinsics carry
-// no pointer information of their own beyond the address, and without an
-// alias scope the waitcnt insertion makes every one of them wait for all
-// LDS-DMA loads in flight (vmcnt(0)), although those write another stage
-// slot: a stall of the whole memory latency in the middle of a stage.  The
-// scope of the restrict parameter lets them issue like the plain
-// ds_read_b128 loads of K-major tiles.  For both, the true dependency (a
-// stage's DMA before its first read) is ordered by the kernels themselves:
-// each wave waits for its own DMA (vmcnt) and a workgroup barrier follows,
-// before any wave reads the stage.
-__device__ __forceinline__ s16x4 lds_read_tr16(const char* __restrict__ p) {
-  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p);
-}
-__device__ __forceinline__ i32x2 lds_read_tr8(const char* __restrict__ p) {
-  return __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2*)p);
-}
-
 template <Elt IN, bool MN, int BT, int KR, int ATOM = 32>
 struct OpTile {
   using Op = MfmaAtom<IN, ATOM>;
