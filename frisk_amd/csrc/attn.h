@@ -428,12 +428,19 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(
             for (int t = 0; t < QT; ++t)
               s[t][kt] = Mf::run(kf1[kt][i], qf[t][G::kH1 + i], s[t][kt]);
       }
+      // The second half of the V^T fragments: without a mask it is read
+      // here, once the K fragments are dead, so that the softmax hides its
+      // latency as well (C5 non-causal 1097 -> 1128 TFLOP/s); the causal
+      // kernel reads it after the softmax, where the masked softmax leaves
+      // the registers for it (read here it needs 262 VGPRs, one workgroup
+      // per CU: causal 938 -> 844).
+      constexpr bool kEarlyV = !CAUSAL;
+      if constexpr (kEarlyV) read_v(ks, 2, vf1);
       __builtin_amdgcn_sched_barrier(0);
       i32x4 pf[QT][4];
       softmax(s, pf, kbase, masked_tag);
-      // O^T += V^T . P^T over 4 key steps of 16; the second half of the V^T
-      // fragments is read under the first half's MFMAs.
-      read_v(ks, 2, vf1);
+      // O^T += V^T . P^T over 4 key steps of 16.
+      if constexpr (!kEarlyV) read_v(ks, 2, vf1);
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
