@@ -100,6 +100,13 @@ def make_workloads(torch, rt):
             return lambda: rt.attn_fwd(q, k, v, o, causal=causal, sm_scale=128 ** -0.5)
         return setup
 
+    def library_gemm(m, n, k):
+        def setup():
+            a = torch.randn(m, k, generator=gen(1), device=dev).to(torch.bfloat16)
+            b = torch.randn(n, k, generator=gen(2), device=dev).to(torch.bfloat16)
+            return lambda: torch.matmul(a, b.t())
+        return setup
+
     def copy(nbytes):
         def setup():
             src = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1)
@@ -165,6 +172,9 @@ def make_workloads(torch, rt):
         # Calibration only (--only): a plain 256 MiB device copy, whose
         # FETCH_SIZE / WRITE_SIZE per dispatch scale the HBM counters.
         "copy_256mib": ("bytes", 0.0, copy(256 << 20)),
+        # Comparison only (--only): hipBLASLt (torch.matmul) on the headline
+        # GEMM's operands, for counter passes beside gemm_bf16_4096.
+        "hipblaslt_bf16_4096": ("ref", 2.0 * 4096 ** 3, library_gemm(4096, 4096, 4096)),
     }
 
 
@@ -435,7 +445,7 @@ def main():
 
     results = {}
     for name, (label, flops, setup) in work.items():
-        if label == "bytes":
+        if label in ("bytes", "ref"):
             continue
         fn = setup()
         steps = args.steps
