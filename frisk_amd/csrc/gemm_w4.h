@@ -112,6 +112,28 @@ __global__ __launch_bounds__(g4::kThreads) void gemm_w4_kernel(
   }
   TA::dma_adv(da, lda_b);
   TB::dma_adv(db, ldb_b);
+  // With four or more k-steps per stage the stage base goes in the scalar
+  // offset of each load, beside stage-invariant lane offsets: every stage
+  // before nk_full holds KR whole bytes of K, so a lane live in the last of
+  // them is live in all; the partial stage nk_full (when KR does not divide
+  // K) keeps only its live chunks; stages past the last read through a
+  // zero-length range.  One VALU select per load instead of an add, a
+  // compare and a select (bf16 4096^3 +0.7%, int8 +0.6%; with two k-steps,
+  // fp8 4096x8192x8192, -1.3%, so those keep the per-lane offsets).
+  constexpr bool kScalarStage = kSteps >= 4;
+  const int nk_full = Kb / KR;
+  uint32_t a_full[kBlocks], a_tail[kBlocks], b_full[kBlocks], b_tail[kBlocks];
+#pragma unroll
+  for (int i = 0; i < kBlocks; ++i) {
+    a_full[i] = (nk_full - 1) * TA::kStep < da.lim[i] ? da.off[i] : 0x80000000u;
+    a_tail[i] = nk_full * TA::kStep < da.lim[i] ? da.off[i] : 0x80000000u;
+    b_full[i] = (nk_full - 1) * TB::kStep < db.lim[i] ? db.off[i] : 0x80000000u;
+    b_tail[i] = nk_full * TB::kStep < db.lim[i] ? db.off[i] : 0x80000000u;
+  }
+  const __amdgpu_buffer_rsrc_t rsa_none = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)TA::origin(A, row0, lda_b), (short)0, 0, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rsb_none = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)TB::origin(B, col0, ldb_b), (short)0, 0, 0x00020000);
   // Workgroups start their K walk at a per-XCD offset: stage kt of the loop
   // holds K stage (kt + krot) mod nk.  The workgroups of one XCD share A and
   // B rows through that XCD's L2 and keep one offset, so the sharing is
@@ -137,14 +159,27 @@ __global__ __launch_bounds__(g4::kThreads) void gemm_w4_kernel(
     constexpr bool is_a = decltype(op)::value;
     const int phys = phys_of(stage);
     char* dst = smem + slot * kTileBytes + wave * kBlocks * 1024;
+    if constexpr (kScalarStage) {
+      const bool past = phys >= nk_all, tail = phys == nk_full;
+      const uint32_t soff = past ? 0u : (uint32_t)phys * (is_a ? da.adv : db.adv);
+      const __amdgpu_buffer_rsrc_t rs = is_a ? (past ? rsa_none : rsa) : (past ? rsb_none : rsb);
 #pragma unroll
-    for (int i = p * kBlocks / np; i < (p + 1) * kBlocks / np; ++i) {
-      uint32_t o = is_a ? TA::offset(da, i, phys) : TB::offset(db, i, phys);
-      // Keep the select a select: otherwise the backend may turn it into a
-      // branch around two copies of the load.
-      asm("" : "+v"(o));
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(is_a ? rsa : rsb, (lds_ptr_t)(dst + i * 1024), 16,
-                                               o, 0, 0, 0);
+      for (int i = p * kBlocks / np; i < (p + 1) * kBlocks / np; ++i) {
+        uint32_t o = is_a ? (tail ? a_tail[i] : a_full[i]) : (tail ? b_tail[i] : b_full[i]);
+        asm("" : "+v"(o));  // a v_cndmask, not a branch around two loads
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(dst + i * 1024), 16, o,
+                                                 __builtin_amdgcn_readfirstlane(soff), 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int i = p * kBlocks / np; i < (p + 1) * kBlocks / np; ++i) {
+        uint32_t o = is_a ? TA::offset(da, i, phys) : TB::offset(db, i, phys);
+        // Keep the select a select: otherwise the backend may turn it into a
+        // branch around two copies of the load.
+        asm("" : "+v"(o));
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(is_a ? rsa : rsb, (lds_ptr_t)(dst + i * 1024),
+                                                 16, o, 0, 0, 0);
+      }
     }
   };
   using OpA = std::true_type;
