@@ -233,16 +233,17 @@ def attention_row_features(d: int, dtype: str, waves: int, key_blocks: float) ->
 def attention_shape(b: int, h: int, s: int, causal: bool, cus: int = 256) -> Tuple[int, int, float]:
     """(waves per workgroup, workgroups, mean key blocks per workgroup) of
     the attention kernel's launch for a square (seq_q = seq_k = s) problem:
-    causal launches take 4 waves x 32 queries; non-causal 8 waves unless 4
-    finish sooner (the launch rule of frisk_amd/csrc/attn.h)."""
-    if causal:
-        waves = 4
-    else:
-        w8, w4 = b * h * -(-s // 256), b * h * -(-s // 128)
-        t8 = -(-w8 // cus)
-        rest = w4 % (2 * cus)
-        t4 = w4 // (2 * cus) + (0.0 if rest == 0 else 0.6 if rest <= cus else 1.0)
-        waves = 4 if t4 < t8 else 8
+    8 waves x 32 queries unless 4 finish sooner, counting workgroups of
+    query blocks (under a causal mask, of pairs of them), the launch rule
+    of frisk_amd/csrc/attn.h."""
+    def workgroups(bm):
+        q = -(-s // bm)
+        return b * h * ((q + 1) // 2 if causal else q)
+    w8, w4 = workgroups(256), workgroups(128)
+    t8 = -(-w8 // cus)
+    rest = w4 % (2 * cus)
+    t4 = w4 // (2 * cus) + (0.0 if rest == 0 else 0.6 if rest <= cus else 1.0)
+    waves = 4 if t4 < t8 else 8
     bm = 32 * waves
     qb = -(-s // bm)
     if causal:

@@ -428,19 +428,15 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(
             for (int t = 0; t < QT; ++t)
               s[t][kt] = Mf::run(kf1[kt][i], qf[t][G::kH1 + i], s[t][kt]);
       }
-      // The second half of the V^T fragments: without a mask it is read
-      // here, once the K fragments are dead, so that the softmax hides its
-      // latency as well (C5 non-causal 1097 -> 1128 TFLOP/s); the causal
-      // kernel reads it after the softmax, where the masked softmax leaves
-      // the registers for it (read here it needs 262 VGPRs, one workgroup
-      // per CU: causal 938 -> 844).
-      constexpr bool kEarlyV = !CAUSAL;
-      if constexpr (kEarlyV) read_v(ks, 2, vf1);
+      // The second half of the V^T fragments, read here once the K
+      // fragments are dead, so that the softmax hides its latency as well
+      // (C5 non-causal 1097 -> 1128 TFLOP/s; causal, with the 8-wave
+      // workgroups, 944 -> 979-989).
+      read_v(ks, 2, vf1);
       __builtin_amdgcn_sched_barrier(0);
       i32x4 pf[QT][4];
       softmax(s, pf, kbase, masked_tag);
       // O^T += V^T . P^T over 4 key steps of 16.
-      if constexpr (!kEarlyV) read_v(ks, 2, vf1);
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -523,33 +519,33 @@ static hipError_t launch_attn_nw(const AttnArgs& a, hipStream_t stream) {
 }
 
 // Workgroup shape per launch (measured on MI355X).  Every query's arithmetic
-// is the same in both shapes (same key blocks in the same order), so the
-// choice never changes a result bit.
-//  * Causal: 4 waves x 32 queries; the smaller query blocks balance the
-//    triangular work better.
-//  * Non-causal: 8 waves x 32 queries (one K/V tile feeds 256 queries)
-//    unless 4 waves finish sooner.  A CU runs one 8-wave workgroup or two
-//    4-wave ones at a time (two waves per SIMD), so in units of one 8-wave
-//    workgroup's run: 8 waves take ceil(w8 / CUs); 4 waves take one unit
-//    per 2 CUs workgroups, and a last round of at most one workgroup per CU
-//    about 0.6 (one wave per SIMD runs each wave faster).  Measured
-//    non-causal: b4 h32 s4096 d128 1030 vs 1012 TFLOP/s (8 kept);
-//    b8 h8 s1024 d64 657 vs 635 (8 kept); b2 h32 s1025 d64 366 vs 475 and
-//    b1 h16 s2048 d128 618 vs 839 (4 chosen).
+// is the same in both shapes (same key blocks in the same order; a masked
+// block with no hidden key computes what an unmasked one does), so the
+// choice never changes a result bit.  8 waves x 32 queries (one K/V tile
+// feeds 256 queries) unless 4 waves finish sooner.  A CU runs one 8-wave
+// workgroup or two 4-wave ones at a time (two waves per SIMD), so in units
+// of one 8-wave workgroup's run: 8 waves take ceil(w8 / CUs); 4 waves take
+// one unit per 2 CUs workgroups, and a last round of at most one workgroup
+// per CU about 0.6 (one wave per SIMD runs each wave faster).  Measured
+// non-causal: b4 h32 s4096 d128 1030 vs 1012 TFLOP/s (8 kept); b8 h8 s1024
+// d64 657 vs 635 (8 kept); b2 h32 s1025 d64 366 vs 475 and b1 h16 s2048
+// d128 618 vs 839 (4 chosen).  Causal b4 h32 s4096 d128 (workgroups of
+// paired query blocks): 979-989 vs 944 (8 kept).
 template <Elt T, Elt OUT, int D, bool CAUSAL>
 static hipError_t launch_attn(const AttnArgs& a, hipStream_t stream) {
-  if constexpr (CAUSAL) {
-    return launch_attn_nw<T, OUT, D, 4, true>(a, stream);
-  } else {
-    const int64_t cus = device_cus();
-    const int64_t bh = a.batch * a.heads;
-    const int64_t w8 = bh * ((a.seq_q + 255) / 256), w4 = bh * ((a.seq_q + 127) / 128);
-    const double t8 = (double)((w8 + cus - 1) / cus);
-    const int64_t rest4 = w4 % (2 * cus);
-    const double t4 = (double)(w4 / (2 * cus)) + (rest4 == 0 ? 0.0 : rest4 <= cus ? 0.6 : 1.0);
-    return t4 < t8 ? launch_attn_nw<T, OUT, D, 4, false>(a, stream)
-                   : launch_attn_nw<T, OUT, D, 8, false>(a, stream);
-  }
+  // Workgroups of bm queries (under a causal mask, pairs of query blocks).
+  const int64_t bh = a.batch * a.heads;
+  auto workgroups = [&](int64_t bm) {
+    const int64_t q = (a.seq_q + bm - 1) / bm;
+    return bh * (CAUSAL ? (q + 1) / 2 : q);
+  };
+  const int64_t cus = device_cus();
+  const int64_t w8 = workgroups(256), w4 = workgroups(128);
+  const double t8 = (double)((w8 + cus - 1) / cus);
+  const int64_t rest4 = w4 % (2 * cus);
+  const double t4 = (double)(w4 / (2 * cus)) + (rest4 == 0 ? 0.0 : rest4 <= cus ? 0.6 : 1.0);
+  return t4 < t8 ? launch_attn_nw<T, OUT, D, 4, CAUSAL>(a, stream)
+                 : launch_attn_nw<T, OUT, D, 8, CAUSAL>(a, stream);
 }
 
 // Every (input dtype, output dtype, mask) variant of one head_dim.

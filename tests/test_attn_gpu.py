@@ -84,16 +84,18 @@ def test_config_c5_every_head_sampled_rows(native_oracle, causal):
     print(f"c5 causal={causal}: worst row-scaled error {worst:.3e}, worst LSE error {worst_lse:.3e}")
 
 
-def test_workgroup_shapes_agree_bitwise():
+@pytest.mark.parametrize("causal", [False, True])
+def test_workgroup_shapes_agree_bitwise(causal):
     # The same two heads computed in a small grid (b1 h2 s1024: the launcher
     # picks 4-wave workgroups) and inside a b128 grid (8-wave workgroups):
-    # every query's arithmetic is the same in both shapes, so the outputs and
-    # LSE must match bit for bit.
-    print("case attn workgroup shapes b1 vs b128 h2 s1024", flush=True)
+    # every query's arithmetic is the same in both shapes (under a causal
+    # mask the diagonal blocks fall differently into the masked loop), so
+    # the outputs and LSE must match bit for bit.
+    print(f"case attn workgroup shapes b1 vs b128 h2 s1024 causal={causal}", flush=True)
     q, k, v = qkv(1, 2, 1024, 1024, torch.bfloat16, seed=11)
-    o_small, l_small = run(q, k, v, False)
+    o_small, l_small = run(q, k, v, causal)
     rep = lambda x: x.expand(128, -1, -1, -1).contiguous()
-    o_big, l_big = run(rep(q), rep(k), rep(v), False)
+    o_big, l_big = run(rep(q), rep(k), rep(v), causal)
     for i in (0, 77, 127):
         assert torch.equal(o_big[i], o_small[0])
         assert torch.equal(l_big[i], l_small[0])

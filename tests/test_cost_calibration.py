@@ -101,14 +101,15 @@ def test_gemm_row_features_check_the_variant():
 
 @pytest.mark.parametrize("b,h,s,causal,waves", [(4, 32, 4096, False, 8), (8, 8, 1024, False, 8),
                                                 (2, 32, 1025, False, 4), (1, 16, 2048, False, 4),
-                                                (4, 32, 4096, True, 4)])
+                                                (4, 32, 4096, True, 8), (1, 2, 1024, True, 4)])
 def test_attention_shape_follows_the_launch_rule(b, h, s, causal, waves):
     # The launch rule's own measured cases (b4 h32 s4096 and b8 h8 s1024
     # keep 8 waves; b2 h32 s1025 and b1 h16 s2048 take 4).
     w, wgs, blocks = C.attention_shape(b, h, s, causal)
     assert w == waves and wgs == b * h * -(-s // (32 * w))
     if causal:
-        assert blocks == pytest.approx(sum(2 * (i + 1) for i in range(s // 128)) / (s // 128))
+        n = s // (32 * w)
+        assert blocks == pytest.approx(sum(w // 2 * (i + 1) for i in range(n)) / n)
     else:
         assert blocks == -(-s // 64)
 
