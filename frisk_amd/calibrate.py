@@ -230,12 +230,14 @@ def attention_row_features(d: int, dtype: str, waves: int, key_blocks: float) ->
     return _axpy(block, key_blocks, rest)
 
 
-def attention_shape(b: int, h: int, s: int, causal: bool, cus: int = 256) -> Tuple[int, int, float]:
+def attention_shape(b: int, h: int, s: int, causal: bool, d: int = 128,
+                    cus: int = 256) -> Tuple[int, int, float]:
     """(waves per workgroup, workgroups, mean key blocks per workgroup) of
     the attention kernel's launch for a square (seq_q = seq_k = s) problem:
-    8 waves x 32 queries unless 4 finish sooner, counting workgroups of
-    query blocks (under a causal mask, of pairs of them), the launch rule
-    of frisk_amd/csrc/attn.h."""
+    head_dim 64 and below take 4 waves x 32 queries; head_dim 128 takes 8
+    unless 4 finish sooner, counting workgroups of query blocks (under a
+    causal mask, of pairs of them), the launch rule of
+    frisk_amd/csrc/attn.h."""
     def workgroups(bm):
         q = -(-s // bm)
         return b * h * ((q + 1) // 2 if causal else q)
@@ -243,7 +245,7 @@ def attention_shape(b: int, h: int, s: int, causal: bool, cus: int = 256) -> Tup
     t8 = -(-w8 // cus)
     rest = w4 % (2 * cus)
     t4 = w4 // (2 * cus) + (0.0 if rest == 0 else 0.6 if rest <= cus else 1.0)
-    waves = 4 if t4 < t8 else 8
+    waves = 4 if d <= 64 or t4 < t8 else 8
     bm = 32 * waves
     qb = -(-s // bm)
     if causal:
@@ -365,7 +367,7 @@ def measure(out: Path) -> dict:
         q, kk, v = (torch.randn(bb, h, s, d, generator=gen, device="cuda").to(tdt[dt]) for _ in range(3))
         o = torch.empty_like(q)
         fn = lambda: rt.attn_fwd(q, kk, v, o, causal=causal)
-        waves, wgs, blocks = attention_shape(bb, h, s, causal, cus)
+        waves, wgs, blocks = attention_shape(bb, h, s, causal, d, cus)
         ms, mhz, spread = _timed_passes(torch, fn)
         rows.append({"kind": "attention", "dtype": dt, "batch": bb, "heads": h, "seq": s, "d": d,
                      "causal": causal, "waves": waves, "workgroups": wgs, "key_blocks": blocks,

@@ -99,13 +99,17 @@ def test_gemm_row_features_check_the_variant():
     assert f["global_lines"] == 64 * 256 + 512
 
 
-@pytest.mark.parametrize("b,h,s,causal,waves", [(4, 32, 4096, False, 8), (8, 8, 1024, False, 8),
-                                                (2, 32, 1025, False, 4), (1, 16, 2048, False, 4),
-                                                (4, 32, 4096, True, 8), (1, 2, 1024, True, 4)])
-def test_attention_shape_follows_the_launch_rule(b, h, s, causal, waves):
-    # The launch rule's own measured cases (b4 h32 s4096 and b8 h8 s1024
-    # keep 8 waves; b2 h32 s1025 and b1 h16 s2048 take 4).
-    w, wgs, blocks = C.attention_shape(b, h, s, causal)
+@pytest.mark.parametrize("b,h,s,d,causal,waves", [(4, 32, 4096, 128, False, 8),
+                                                  (2, 32, 1024, 128, False, 8),
+                                                  (1, 16, 2048, 128, False, 4),
+                                                  (4, 32, 4096, 128, True, 8),
+                                                  (1, 2, 1024, 128, True, 4),
+                                                  (4, 32, 4096, 64, False, 4),
+                                                  (8, 8, 1024, 64, True, 4)])
+def test_attention_shape_follows_the_launch_rule(b, h, s, d, causal, waves):
+    # The launch rule's own measured cases (head_dim 128: b4 h32 s4096 and
+    # b2 h32 s1024 keep 8 waves, b1 h16 s2048 takes 4; head_dim 64 always 4).
+    w, wgs, blocks = C.attention_shape(b, h, s, causal, d)
     assert w == waves and wgs == b * h * -(-s // (32 * w))
     if causal:
         n = s // (32 * w)
