@@ -20,7 +20,8 @@ input byte read once, each output byte written once) against the 8 TB/s
 HBM peak.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
-       python bench.py --only NAME --steps K   (one workload, for rocprofv3)
+       python bench.py --only NAME[,NAME...] --steps K   (for rocprofv3)
+       python bench.py --trace-summary KERNEL_TRACE.csv --steps K
 """
 from __future__ import annotations
 
@@ -46,7 +47,10 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
-    p.add_argument("--only", default=None, help="run a single workload (for profilers)")
+    p.add_argument("--only", default=None,
+                   help="run only these workloads (comma-separated), for profilers")
+    p.add_argument("--trace-summary", default=None, metavar="CSV",
+                   help="summarise a rocprofv3 kernel-trace CSV of a --only run and exit")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--settle", type=float, default=SETTLE_S,
                    help="seconds of untimed load before each workload's warm-up")
@@ -178,17 +182,21 @@ def make_workloads(torch, rt):
     }
 
 
-def time_launches(torch, fn, steps, warmup, settle_s=SETTLE_S):
+def time_launches(torch, fn, steps, warmup, settle_s=SETTLE_S, counts=None):
     # An idle MI355X takes about 50 ms of load to reach its steady clock
     # (measured: the first 25 ms of 4096^3 GEMMs run at 1090 TFLOP/s, every
     # later window at 1230 for seconds).  The untimed settle runs the workload
     # for settle_s before the W warm-up launches, so that the K timed launches
     # see the clock a sustained workload sees.
     t0 = time.perf_counter()
+    settled = 0
     while time.perf_counter() - t0 < settle_s:
         for _ in range(8):
             fn()
+        settled += 8
         torch.cuda.synchronize()
+    if counts is not None:
+        counts.update(settle=settled, warmup=warmup, timed=steps)
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -419,8 +427,40 @@ def traffic_from_profile(name):
     return None
 
 
+def trace_summary(path, steps):
+    """Per-kernel durations from a rocprofv3 kernel-trace CSV (`-f csv`) of
+    a `--only` run: dispatch count, average over every dispatch (settle and
+    warm-up included) and over the last `steps` dispatches of that kernel
+    and grid, which are the timed launches.  Returns a list of dicts."""
+    import csv
+    rows = {}
+    with open(path, newline="") as f:
+        for r in csv.DictReader(f):
+            grid = tuple(int(r[f"Grid_Size_{a}"]) // max(1, int(r[f"Workgroup_Size_{a}"]))
+                         for a in "XYZ")
+            key = (r["Kernel_Name"], grid)
+            rows.setdefault(key, []).append(
+                (int(r["Start_Timestamp"]), (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3))
+    out = []
+    for (name, grid), d in rows.items():
+        d.sort()
+        us = [x[1] for x in d]
+        last = us[-steps:]
+        out.append({"kernel": name.split("(")[0].strip(), "grid": grid, "calls": len(us),
+                    "avg_us": sum(us) / len(us), "timed_calls": len(last),
+                    "timed_avg_us": sum(last) / len(last), "timed_min_us": min(last),
+                    "timed_max_us": max(last),
+                    "timed_span_us": (d[-1][0] - d[-len(last)][0]) / 1e3 + d[-1][1]})
+    out.sort(key=lambda r: -r["timed_avg_us"])
+    return out
+
+
 def main():
     args = parse()
+    if args.trace_summary:
+        for r in trace_summary(args.trace_summary, args.steps):
+            print(json.dumps(r))
+        return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
               "GEMM and attention shard across GPUs without exchange",
@@ -436,11 +476,18 @@ def main():
         print(json.dumps({"workload": args.only, **fixed_tile_latency(torch, rt)}), flush=True)
         return
     if args.only:
-        label, flops, setup = work[args.only]
-        fn = setup()
-        ms = time_launches(torch, fn, args.steps, args.warmup, args.settle)
-        rate = {"gbs": flops / ms / 1e6} if label == "hbm" else {"tflops": flops / ms / 1e9}
-        print(json.dumps({"workload": args.only, "ms": ms, **rate}), flush=True)
+        # Each workload: settle, warm-up, then the K timed launches, and
+        # nothing after them, so the last K dispatches of its kernels in a
+        # kernel trace are the timed ones (--trace-summary).
+        for name in args.only.split(","):
+            label, flops, setup = work[name]
+            fn = setup()
+            counts = {}
+            ms = time_launches(torch, fn, args.steps, args.warmup, args.settle, counts)
+            rate = {"gbs": flops / ms / 1e6} if label == "hbm" else {"tflops": flops / ms / 1e9}
+            print(json.dumps({"workload": name, "ms": ms, **rate, "launches": counts}), flush=True)
+            del fn
+            torch.cuda.empty_cache()
         return
 
     results = {}
