@@ -328,15 +328,18 @@ int frisk_gemm_plan(const frisk_gemm_desc* d, char* buf, int64_t len) {
   if (route == GemmRoute::Generic) {
     n = snprintf(buf, (size_t)len,
                  "{\"kernel\": \"gemm_generic\", \"tile_m\": 64, \"tile_n\": 64, \"atom\": \"fma\", "
-                 "\"a_major\": \"%s\", \"b_major\": \"%s\", \"slices\": 1, \"workspace_bytes\": 0}",
+                 "\"a_major\": \"%s\", \"b_major\": \"%s\", \"slices\": 1, \"slice_sum\": \"none\", "
+                 "\"workspace_bytes\": 0}",
                  a_major, b_major);
   } else if (route == GemmRoute::Skinny && !(ws && g.m > kSkinnySplitMaxM)) {
     const frisk::SkinnyPlan p = frisk::gemm_skinny_plan(g, cus, ws);
     n = snprintf(buf, (size_t)len,
                  "{\"kernel\": \"gemm_skinny\", \"tile_m\": %d, \"tile_n\": %d, "
                  "\"atom\": \"v_mfma_f32_16x16x32_%s\", \"waves\": [1, 1], \"a_major\": \"k\", "
-                 "\"b_major\": \"k\", \"slices\": %d, \"workspace_bytes\": %lld}",
+                 "\"b_major\": \"k\", \"slices\": %d, \"slice_sum\": \"%s\", "
+                 "\"workspace_bytes\": %lld}",
                  16 * p.tm, 16 * p.tn, d->a_type == FRISK_BF16 ? "bf16" : "f16", p.slices,
+                 p.slices > 1 ? "second_launch" : "none",
                  (long long)(p.slices > 1 ? p.workspace_bytes : 0));
   } else {
     const frisk::MfmaChoice c = frisk::gemm_mfma_choice(g, cus, ws);
@@ -355,12 +358,16 @@ int frisk_gemm_plan(const frisk_gemm_desc* d, char* buf, int64_t len) {
                  "{\"kernel\": \"%s\", \"tile_m\": %d, \"tile_n\": %d, \"atom\": \"%s\", "
                  "\"waves\": [%d, %d], \"wave_tile\": [%d, %d], \"stage_bytes\": %d, "
                  "\"a_major\": \"%s\", \"b_major\": \"%s\", \"lds_read_a\": \"%s\", "
-                 "\"lds_read_b\": \"%s\", \"slices\": %d, \"workspace_bytes\": %lld, "
+                 "\"lds_read_b\": \"%s\", \"slices\": %d, \"slice_sum\": \"%s\", "
+                 "\"workspace_bytes\": %lld, "
                  "\"requested\": %s, \"mma_contract\": \"{atom = \\\"%s\\\", wave_grid = [%d, %d], "
                  "repeats = [%d, %d, %d], policy = \\\"%s\\\", swapped = %s}\"}",
                  c.big ? "gemm_w4" : "gemm_128", tile, tile, mfma_atom(g.in), wm, wn, tile / wm,
                  tile / wn, stage, a_major, b_major, lds_read(g.trans_a), lds_read(!g.trans_b),
-                 c.slices, (long long)(c.slices > 1 ? need : 0), g.tile ? "true" : "false",
+                 c.slices,
+                 c.slices <= 1 ? "none"
+                 : !c.big && c.slices <= frisk::kTreeMaxSlices ? "in_launch" : "second_launch",
+                 (long long)(c.slices > 1 ? need : 0), g.tile ? "true" : "false",
                  mfma_atom(g.in), wm, wn, tile / wm / 32, tile / wn / 32,
                  stage / atom_k_bytes(g.in), policy, c.big ? "true" : "false");
   }

@@ -111,6 +111,18 @@ double partial_cost(const GemmArgs& g, int64_t slices) {
 }
 }  // namespace
 
+// The f32 partials of a split (slices x M x N x 4 bytes) stay within
+// 2 x (M + N) x K x 2 / FRISK_SPLIT_CAP bytes: the bytes of A and B.
+// Measured with operands from HBM, us, a quarter of A + B (16) -> all of it
+// (4): 256x4096x4096 27.4 -> 23.1 (2 -> 4 slices), 512x4096x4096 41.8 ->
+// 28.5 (8 slices of 256x256 tiles -> 2 of 128x128); 128x4096x4096 19.3
+// either way (4 -> 8 slices).
+#ifndef FRISK_W4_SPLIT
+#define FRISK_W4_SPLIT 1
+#endif
+#ifndef FRISK_SPLIT_CAP
+#define FRISK_SPLIT_CAP 4
+#endif
 // Bytes of K per pipeline stage of the 128x128-tile kernel (gemm_128.h).
 constexpr int64_t kRow = 64;
 
@@ -125,8 +137,8 @@ SplitPlan gemm_split_plan(const GemmArgs& g, int cus) {
   const int64_t tiles = ((g.m + 127) / 128) * ((g.n + 127) / 128);
   const int64_t kb = g.k * 2;
   // 128x128 tiles.  Split only grids that leave CUs without a tile, each
-  // slice at least 8 stages, and the f32 partials at most a quarter of the
-  // bytes of A and B (their second pass then costs little).  Grids of at
+  // slice at least 8 stages, and the f32 partials at most the bytes of A
+  // and B (FRISK_SPLIT_CAP).  Grids of at
   // most half as many tiles as CUs take slices up to one workgroup per CU,
   // on 128-byte stages (the launch picks them when slices fit one
   // workgroup per CU); larger grids take slices up to two workgroups per
@@ -141,7 +153,7 @@ SplitPlan gemm_split_plan(const GemmArgs& g, int cus) {
     const int64_t row = deep ? 128 : kRow;  // bytes of K per stage
     int64_t slices = deep ? cus / tiles : (2 * (int64_t)cus + tiles - 1) / tiles;
     slices = std::min<int64_t>(slices, kb / (8 * row));
-    slices = std::min<int64_t>(slices, (g.m + g.n) * kb / (16 * g.m * g.n));
+    slices = std::min<int64_t>(slices, (g.m + g.n) * kb / (FRISK_SPLIT_CAP * g.m * g.n));
     slices = std::min<int64_t>(slices, 64);
     if (slices >= 2) {
       const int64_t chunks = (kb + row - 1) / row;  // slices start on stage boundaries
@@ -160,7 +172,7 @@ SplitPlan gemm_split_plan(const GemmArgs& g, int cus) {
   // 1024 x 4096 x 4096 stays on 128x128 tiles (57.6 us split against 54.4)
   // and 256 x 4096 x 4096 on its 128x128 split (34.9 us on 256x256 tiles
   // against 33.2; estimated ratio 0.84).
-  if (g.m > kSkinnyMaxM) {
+  if (g.m > kSkinnyMaxM && FRISK_W4_SPLIT) {
     const double flop128 = 2.0 * 128 * 128 * (double)(p.kb_slice / 2);
     const double t128 = rounds(tiles * p.slices, cus) * flop128 / kRate128 + partial_cost(g, p.slices);
     double best = 0.0;
@@ -181,7 +193,9 @@ SplitPlan gemm_split_plan(const GemmArgs& g, int cus) {
       if (!p.big) p = SplitPlan{1, kb, 0, false};
     }
   }
-  p.workspace_bytes = p.slices > 1 ? (int64_t)p.slices * g.m * g.n * 4 : 0;
+  p.workspace_bytes = p.slices <= 1 ? 0
+                     : !p.big && p.slices <= kTreeMaxSlices ? split_tree_bytes(tiles, p.slices, 128)
+                                                            : (int64_t)p.slices * g.m * g.n * 4;
   return p;
 }
 
@@ -204,10 +218,10 @@ namespace {
 // One storage order: AM = A stored [K, M] (trans_a), BM = B stored [K, N]
 // (not trans_b).
 template <bool AM, bool BM>
-hipError_t run_layout(const GemmArgs& g, hipStream_t s, const MfmaChoice& c, float* partial) {
+hipError_t run_layout(const GemmArgs& g, hipStream_t s, const MfmaChoice& c, void* ws) {
   if (c.slices > 1) {
-    if (c.big) return gemm_w4_split_layout<AM, BM>(g, c.slices, c.kb_slice, partial, s);
-    return gemm_128_split_layout<AM, BM>(g, c.slices, c.kb_slice, partial, s);
+    if (c.big) return gemm_w4_split_layout<AM, BM>(g, c.slices, c.kb_slice, ws, s);
+    return gemm_128_split_layout<AM, BM>(g, c.slices, c.kb_slice, ws, s);
   }
   if (c.big) return gemm_w4_layout<AM, BM>(g, s);
   if (g.tile == 128) return gemm_128_grid_layout<AM, BM>(g, s);
@@ -220,12 +234,12 @@ hipError_t gemm_mfma(const GemmArgs& g, hipStream_t s, void* workspace, int64_t 
   const int cus = device_cus();
   const bool ws = !g.tile && workspace && workspace_bytes >= gemm_split_plan(g, cus).workspace_bytes;
   const MfmaChoice c = gemm_mfma_choice(g, cus, ws);
-  float* partial = c.slices > 1 ? (float*)workspace : nullptr;
+  void* tree_ws = c.slices > 1 ? workspace : nullptr;
   switch ((g.trans_a ? 2 : 0) | (g.trans_b ? 0 : 1)) {
-    case 0: return run_layout<false, false>(g, s, c, partial);  // A [M,K], B [N,K]
-    case 1: return run_layout<false, true>(g, s, c, partial);   // A [M,K], B [K,N]
-    case 2: return run_layout<true, false>(g, s, c, partial);   // A [K,M], B [N,K]
-    default: return run_layout<true, true>(g, s, c, partial);   // A [K,M], B [K,N]
+    case 0: return run_layout<false, false>(g, s, c, tree_ws);  // A [M,K], B [N,K]
+    case 1: return run_layout<false, true>(g, s, c, tree_ws);   // A [M,K], B [K,N]
+    case 2: return run_layout<true, false>(g, s, c, tree_ws);   // A [K,M], B [N,K]
+    default: return run_layout<true, true>(g, s, c, tree_ws);   // A [K,M], B [K,N]
   }
 }
 

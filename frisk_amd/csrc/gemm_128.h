@@ -67,16 +67,19 @@ static_assert(lds_bytes_grid(128, 4, 1, 128) <= 160 * 1024, "one 128x128 workgro
 // owning a (BT/WM) x (BT/WN) sub-tile as TM x TN 32x32 accumulators.
 //
 // Split-K: blockIdx.y is a K slice of kb_slice bytes; the slice's A and B
-// start kb_slice bytes of K further per slice, and its output is the tile
-// of C c_slice_bytes * y bytes further (the f32 partial of that slice).
-template <Elt IN, Elt OUT, bool AM, bool BM, int BT, int WM, int WN, int KROW>
+// start kb_slice bytes of K further per slice.  With TREE the slices of a
+// tile sum through `tree` (splitk_tree, gemm_common.h) and the one holding
+// the total writes C; otherwise a slice's output is the tile of C
+// c_slice_bytes * y bytes further (the f32 partial of that slice).
+template <Elt IN, Elt OUT, bool AM, bool BM, int BT, int WM, int WN, int KROW, bool TREE = false>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_128(const char* __restrict__ A,
                                                               const char* __restrict__ B,
                                                               void* __restrict__ C, int M, int N,
                                                               int Kb, int64_t lda_b, int64_t ldb_b,
                                                               int64_t ldc, float scale,
                                                               int accumulate, int kb_slice,
-                                                              int64_t c_slice_bytes) {
+                                                              int64_t c_slice_bytes,
+                                                              SplitTree tree) {
   // The body is device code only; the host pass just needs the kernel stub.
 #if defined(__HIP_DEVICE_COMPILE__)
   constexpr int kRow = KROW, kStages = g128::kStages;
@@ -243,6 +246,11 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_128(const char* __rest
   // accumulator holds D[8*(r/4) + 4*(lane/32) + r%4][lane%32] in element r.
   constexpr int kPitch = 32 * TN + 4;
   static_assert(kWaves * 32 * kPitch * 4 <= kLdsBytes, "epilogue staging fits in the stage buffers");
+  // The split-K tree's LDS flag sits in the last 16 bytes, past the staging.
+  static_assert(!TREE || kWaves * 32 * kPitch * 4 <= kLdsBytes - 16, "room for the tree's flag");
+  if constexpr (TREE)
+    if (!splitk_tree<kWaves>(acc, tree, blockIdx.x, blockIdx.y, (int*)(smem + kLdsBytes - 16)))
+      return;
   AccS* stage = (AccS*)(smem + wave * (32 * kPitch * 4));
   constexpr int kGroups = 32 * TN / 8;  // 8-column groups per staged row
 #pragma unroll
@@ -287,48 +295,75 @@ static hipError_t launch_128(const GemmArgs& g, hipStream_t stream) {
   const int kb = (int)(g.k * kEsz);
   hipLaunchKernelGGL(kern, dim3(tiles), dim3(64 * WM * WN), kLds, stream, (const char*)g.a,
                      (const char*)g.b, g.c, (int)g.m, (int)g.n, kb, g.lda * kEsz, g.ldb * kEsz,
-                     g.ldc, g.scale, g.accumulate, kb, (int64_t)0);
+                     g.ldc, g.scale, g.accumulate, kb, (int64_t)0, SplitTree{});
   return hipGetLastError();
 }
 
-// Split-K on 128x128 tiles: f32 partial tiles of each K slice into
-// `partial` ([slices][M][N]), then their sum in slice order into C
-// (bf16 / f16 inputs, scale 1).
-template <Elt IN, bool AM, bool BM, int KROW>
-static hipError_t launch_128_split_k(const GemmArgs& g, int slices, int64_t kb_slice,
-                                     float* partial, hipStream_t stream) {
+// Split-K on 128x128 tiles, grid (tiles, slices).  Up to kTreeMaxSlices
+// slices sum inside the launch (splitk_tree: partials and arrival words in
+// the workspace `ws`, split_tree_bytes), and the last slice of each tile
+// writes C.  More slices write f32 partial tiles to `ws` ([slices][M][N])
+// and gemm_splitk_sum adds them in slice order in a second launch: the
+// tree's levels are a serial chain of partial writes, arrivals and reads at
+// memory latency, which two or more levels take longer than a second launch
+// (operands from HBM, us, second launch -> tree: 128x14336x4096 (2 slices)
+// 39.6 -> 36.9, 256x4096x4096 (2) 27.3 -> 26.6; 128x4096x4096 (4) 19.3 ->
+// 20.9, 128x4096x14336 (8) 38.0 -> 42.5).  bf16 / f16 inputs, scale 1.
+template <Elt IN, Elt OUT, bool AM, bool BM, int KROW, bool TREE>
+static hipError_t launch_128_split_k(const GemmArgs& g, int slices, int64_t kb_slice, void* ws,
+                                     hipStream_t stream) {
   constexpr int kEsz = EltInfo<IN>::bytes;
   constexpr int kLds = g128::lds_bytes_grid(128, 2, 2, KROW);
-  auto kern = gemm_mfma_128<IN, Elt::F32, AM, BM, 128, 2, 2, KROW>;
+  auto kern = gemm_mfma_128<IN, OUT, AM, BM, 128, 2, 2, KROW, TREE>;
   static const hipError_t attr =
       hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
   if (attr != hipSuccess) return attr;
-  const int tiles = (int)(((g.m + 127) / 128) * ((g.n + 127) / 128));
-  hipLaunchKernelGGL(kern, dim3(tiles, slices), dim3(256), kLds, stream, (const char*)g.a,
-                     (const char*)g.b, (void*)partial, (int)g.m, (int)g.n, (int)(g.k * kEsz),
-                     g.lda * kEsz, g.ldb * kEsz, g.n, 1.0f, 0, (int)kb_slice,
-                     (int64_t)g.m * g.n * 4);
-  const hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  return gemm_splitk_sum(partial, slices, g, stream);
+  const int64_t tiles = ((g.m + 127) / 128) * ((g.n + 127) / 128);
+  if constexpr (TREE) {
+    const SplitTree tree = split_tree_at(ws, tiles, slices, 128);
+    hipLaunchKernelGGL(kern, dim3((unsigned)tiles, slices), dim3(256), kLds, stream,
+                       (const char*)g.a, (const char*)g.b, g.c, (int)g.m, (int)g.n,
+                       (int)(g.k * kEsz), g.lda * kEsz, g.ldb * kEsz, g.ldc, 1.0f, g.accumulate,
+                       (int)kb_slice, (int64_t)0, tree);
+    return hipGetLastError();
+  } else {
+    hipLaunchKernelGGL(kern, dim3((unsigned)tiles, slices), dim3(256), kLds, stream,
+                       (const char*)g.a, (const char*)g.b, ws, (int)g.m, (int)g.n,
+                       (int)(g.k * kEsz), g.lda * kEsz, g.ldb * kEsz, g.n, 1.0f, 0, (int)kb_slice,
+                       (int64_t)g.m * g.n * 4, SplitTree{});
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    return gemm_splitk_sum((const float*)ws, slices, g, stream);
+  }
 }
 
-// 128-byte stages when the slices are at most one workgroup per CU (the
-// split plan then cuts K on 128-byte boundaries), else 64-byte stages.
+template <Elt IN, bool AM, bool BM, int KROW>
+static hipError_t launch_128_split_out(const GemmArgs& g, int slices, int64_t kb_slice, void* ws,
+                                       hipStream_t stream) {
+  if (slices > kTreeMaxSlices)
+    return launch_128_split_k<IN, Elt::F32, AM, BM, KROW, false>(g, slices, kb_slice, ws, stream);
+  switch (g.out) {
+    case Elt::BF16: return launch_128_split_k<IN, Elt::BF16, AM, BM, KROW, true>(g, slices, kb_slice, ws, stream);
+    case Elt::F16: return launch_128_split_k<IN, Elt::F16, AM, BM, KROW, true>(g, slices, kb_slice, ws, stream);
+    case Elt::F32: return launch_128_split_k<IN, Elt::F32, AM, BM, KROW, true>(g, slices, kb_slice, ws, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
 template <Elt IN, bool AM, bool BM>
-static hipError_t launch_128_split(const GemmArgs& g, int slices, int64_t kb_slice, float* partial,
+static hipError_t launch_128_split(const GemmArgs& g, int slices, int64_t kb_slice, void* ws,
                                    hipStream_t stream) {
   const int64_t tiles = ((g.m + 127) / 128) * ((g.n + 127) / 128);
   if (tiles * slices <= device_cus() && kb_slice % 128 == 0)
-    return launch_128_split_k<IN, AM, BM, 128>(g, slices, kb_slice, partial, stream);
-  return launch_128_split_k<IN, AM, BM, 64>(g, slices, kb_slice, partial, stream);
+    return launch_128_split_out<IN, AM, BM, 128>(g, slices, kb_slice, ws, stream);
+  return launch_128_split_out<IN, AM, BM, 64>(g, slices, kb_slice, ws, stream);
 }
 
 template <bool AM, bool BM>
-hipError_t gemm_128_split_layout(const GemmArgs& g, int slices, int64_t kb_slice, float* partial,
+hipError_t gemm_128_split_layout(const GemmArgs& g, int slices, int64_t kb_slice, void* ws,
                                  hipStream_t s) {
-  if (g.in == Elt::BF16) return launch_128_split<Elt::BF16, AM, BM>(g, slices, kb_slice, partial, s);
-  if (g.in == Elt::F16) return launch_128_split<Elt::F16, AM, BM>(g, slices, kb_slice, partial, s);
+  if (g.in == Elt::BF16) return launch_128_split<Elt::BF16, AM, BM>(g, slices, kb_slice, ws, s);
+  if (g.in == Elt::F16) return launch_128_split<Elt::F16, AM, BM>(g, slices, kb_slice, ws, s);
   return hipErrorInvalidValue;
 }
 

@@ -5,6 +5,6 @@
 namespace frisk {
 template hipError_t gemm_128_layout<true, true>(const GemmArgs&, hipStream_t);
 template hipError_t gemm_128_grid_layout<true, true>(const GemmArgs&, hipStream_t);
-template hipError_t gemm_128_split_layout<true, true>(const GemmArgs&, int, int64_t, float*,
+template hipError_t gemm_128_split_layout<true, true>(const GemmArgs&, int, int64_t, void*,
                                                    hipStream_t);
 }  // namespace frisk

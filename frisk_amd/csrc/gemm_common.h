@@ -4,6 +4,7 @@
 #pragma once
 
 #include "common.h"
+#include "kernels.h"
 
 namespace frisk {
 
@@ -206,6 +207,142 @@ __device__ inline void store4(void* c, int64_t idx, const AccS* v, bool accumula
     const i32x2 r = {(int)pack_f32x2<OUT>(f[0], f[1]), (int)pack_f32x2<OUT>(f[2], f[3])};
     *(i32x2*)p = r;
   }
+}
+
+// ---------------------------------------------------------------------------
+// Split-K summed inside the GEMM launch.  Every K slice of an output tile
+// keeps its f32 sum in registers; the slices of a tile combine in a fixed
+// binary tree over slice indices: at level L the subtree of slices
+// [2g 2^L, (2g+1) 2^L) meets the subtree [(2g+1) 2^L, (2g+2) 2^L).  Each of
+// the two workgroups writes its subtree's sum to the partial slot of the
+// subtree's first slice and arrives at the meeting's word; the second to
+// arrive reads the other sum, adds it and goes up a level, the first one is
+// done.  The workgroup holding the whole sum at the root runs the
+// epilogue into C.  Floating-point addition is commutative, so the result
+// depends on the tree alone, not on which workgroup arrives second: the
+// same inputs give the same bits on every call.  Partials are stored in
+// fragment order (lane-contiguous 16-byte pieces of the accumulators), so
+// both their writes and reads are whole 1 KiB rows per wave instruction.
+//
+// Arrival words (64 bits, one per meeting, 64 per tile): 0 or any value but
+// kTreeArrived reads as "nobody has arrived"; the first arrival writes
+// kTreeArrived, the second writes 0 back.  Every call therefore leaves each
+// word it used at 0, whatever the workspace held before (a never-used
+// workspace holds kTreeArrived in a word with probability 2^-64), and
+// nothing has to be cleared between calls.
+// ---------------------------------------------------------------------------
+struct SplitTree {
+  float* partial;                // [tiles][slices][waves][chunks][64 lanes] f32x4
+  unsigned long long* arrivals;  // [tiles][kTreeWords]
+  int slices;
+};
+constexpr unsigned long long kTreeArrived = 0x5A17C0DE00000001ull;
+// The tree of `tiles` tiles of bt x bt outputs in `slices` slices over a
+// workspace of split_tree_bytes (kernels.h): the partials, then the words.
+inline SplitTree split_tree_at(void* ws, int64_t tiles, int slices, int bt) {
+  const int64_t partial_bytes = tiles * slices * (int64_t)bt * bt * 4;
+  return SplitTree{(float*)ws, (unsigned long long*)((char*)ws + partial_bytes), slices};
+}
+// Meeting word of level L, group g: levels take 32, 16, 8, ... words.
+__device__ __host__ constexpr int tree_word(int level, int group) {
+  return kTreeWords - (kTreeWords >> level) + group;
+}
+
+// An accumulator tile from its f32x4 pieces in element order (whole-vector
+// shuffles: no per-element inserts into the accumulator tuple).
+template <typename Acc, int N>
+__device__ inline Acc join_chunks(const f32x4 (&v)[N]) {
+  if constexpr (N == 1) {
+    return v[0];
+  } else {
+    static_assert(N == 4, "f32x4 or f32x16 accumulators");
+    typedef float f32x8_ __attribute__((ext_vector_type(8)));
+    const f32x8_ lo = __builtin_shufflevector(v[0], v[1], 0, 1, 2, 3, 4, 5, 6, 7);
+    const f32x8_ hi = __builtin_shufflevector(v[2], v[3], 0, 1, 2, 3, 4, 5, 6, 7);
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15);
+  }
+}
+
+// Sums the accumulators of this workgroup's slice with its tile's other
+// slices; true for the one workgroup per tile that then holds the total
+// (every thread of a workgroup gets the same answer).  `flag` is a word of
+// LDS no other wave writes until the next workgroup barrier after the call.
+//
+// Coherence without cache-wide operations: partials are written and read
+// with device-scope (SC1) buffer accesses, which the memory system keeps
+// coherent across the XCDs' L2 caches on their own, and the arrival is a
+// device-scope atomic.  A writer waits for its stores to be acknowledged
+// (vmcnt 0) before the workgroup barrier that precedes the arrival; a
+// reader issues its loads after the barrier that follows it.  Agent-scope
+// fences would order the same accesses but write back and invalidate the
+// whole L2 of the XCD, which every other workgroup's operand tiles then
+// miss (measured: M = 128, N = K = 4096 split 4 ways 19.4 -> 41 us).
+template <int kWaves, typename Acc, int TM, int TN>
+__device__ inline bool splitk_tree(Acc (&acc)[TM][TN], const SplitTree& t, int tile, int slice,
+                                   int* flag) {
+  constexpr int kChunks = sizeof(Acc) / 16;  // f32x4 pieces per accumulator tile
+  constexpr int kQ = TM * TN * kChunks;       // per lane
+  constexpr int kSlotBytes = kWaves * kQ * 64 * 16;
+  constexpr int kSC1 = 0x10;                  // device-scope cache policy of a buffer access
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // The tile's partial slots: [slices][waves][chunks][64 lanes] x 16 bytes.
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(t.partial + (int64_t)tile * t.slices * (kSlotBytes / 4)), (short)0,
+      t.slices * kSlotBytes, 0x00020000);
+  const int lane_off = (wave * kQ * 64 + lane) * 16;
+  for (int level = 0; (1 << level) < t.slices; ++level) {
+    const int span = 1 << level;
+    const int group = slice >> (level + 1);
+    const int right = (2 * group + 1) * span;
+    if (right >= t.slices) continue;  // no right subtree at this level: go up alone
+    const int mine = (slice >> level) << level;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        static_for<0, kChunks>([&](auto cc) {
+          constexpr int c = decltype(cc)::value;
+          const f32x4 v =
+              __builtin_shufflevector(acc[i][j], acc[i][j], 4 * c, 4 * c + 1, 4 * c + 2, 4 * c + 3);
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, v), rs,
+                                                 lane_off + ((i * TN + j) * kChunks + c) * 1024,
+                                                 mine * kSlotBytes, kSC1);
+        });
+    __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));  // vmcnt(0): the stores are acknowledged
+    __syncthreads();
+    if (tid == 0) {
+      unsigned long long* w = t.arrivals + (int64_t)tile * kTreeWords + tree_word(level, group);
+      unsigned long long old = 0;
+      int second = 0;
+      // Two workgroups meet at a word, so after one failed exchange (the
+      // other arrival changed the word) the next succeeds: four attempts
+      // always end.
+      for (int attempt = 0; attempt < 4; ++attempt) {
+        second = old == kTreeArrived;
+        if (__hip_atomic_compare_exchange_strong(w, &old, second ? 0ull : kTreeArrived,
+                                                 __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT))
+          break;
+      }
+      *(volatile int*)flag = second;
+    }
+    __syncthreads();
+    if (!*(volatile int*)flag) return false;
+    const int other = mine == right ? mine - span : right;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        f32x4 v[kChunks];
+#pragma unroll
+        for (int c = 0; c < kChunks; ++c)
+          v[c] = __builtin_bit_cast(
+              f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                         rs, lane_off + ((i * TN + j) * kChunks + c) * 1024, other * kSlotBytes, kSC1));
+        acc[i][j] += join_chunks<Acc>(v);
+      }
+  }
+  return true;
 }
 
 // MFMA operand fragments of one k-step: TM A tiles and TN B tiles.

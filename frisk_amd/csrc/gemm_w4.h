@@ -413,10 +413,13 @@ static hipError_t launch_w4(const GemmArgs& g, hipStream_t stream) {
   return hipGetLastError();
 }
 
-// Split-K: f32 partials of each K slice into `partial` ([slices][M][N]),
-// then their sum in slice order into C (bf16 / f16 inputs, scale 1).
+// Split-K: f32 partials of each K slice into the workspace `ws`
+// ([slices][M][N]), then their sum in slice order into C (bf16 / f16
+// inputs, scale 1).  (Summed inside the launch through splitk_tree instead,
+// the 256x256 kernel spills registers and the tree's serial levels cost
+// more than the second launch: 1024x4096x14336 in 4 slices 120 -> 174 us.)
 template <Elt IN, bool AM, bool BM>
-static hipError_t launch_w4_split(const GemmArgs& g, int slices, int64_t kb_slice, float* partial,
+static hipError_t launch_w4_split(const GemmArgs& g, int slices, int64_t kb_slice, void* ws,
                                   hipStream_t stream) {
   constexpr int KR = FRISK_G4_KR;
   constexpr int kEsz = EltInfo<IN>::bytes;
@@ -427,19 +430,19 @@ static hipError_t launch_w4_split(const GemmArgs& g, int slices, int64_t kb_slic
   if (attr != hipSuccess) return attr;
   const int tiles = (int)(((g.m + g4::kBT - 1) / g4::kBT) * ((g.n + g4::kBT - 1) / g4::kBT));
   hipLaunchKernelGGL(kern, dim3(tiles, slices), dim3(g4::kThreads), kLds, stream, (const char*)g.a,
-                     (const char*)g.b, (void*)partial, (int)g.m, (int)g.n, (int)(g.k * kEsz),
+                     (const char*)g.b, ws, (int)g.m, (int)g.n, (int)(g.k * kEsz),
                      g.lda * kEsz, g.ldb * kEsz, g.n, 1.0f, 0, (int)kb_slice,
                      (int64_t)g.m * g.n * 4);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  return gemm_splitk_sum(partial, slices, g, stream);
+  return gemm_splitk_sum((const float*)ws, slices, g, stream);
 }
 
 template <bool AM, bool BM>
-hipError_t gemm_w4_split_layout(const GemmArgs& g, int slices, int64_t kb_slice, float* partial,
+hipError_t gemm_w4_split_layout(const GemmArgs& g, int slices, int64_t kb_slice, void* ws,
                                 hipStream_t s) {
-  if (g.in == Elt::BF16) return launch_w4_split<Elt::BF16, AM, BM>(g, slices, kb_slice, partial, s);
-  if (g.in == Elt::F16) return launch_w4_split<Elt::F16, AM, BM>(g, slices, kb_slice, partial, s);
+  if (g.in == Elt::BF16) return launch_w4_split<Elt::BF16, AM, BM>(g, slices, kb_slice, ws, s);
+  if (g.in == Elt::F16) return launch_w4_split<Elt::F16, AM, BM>(g, slices, kb_slice, ws, s);
   return hipErrorInvalidValue;
 }
 

@@ -4,6 +4,6 @@
 
 namespace frisk {
 template hipError_t gemm_w4_layout<false, true>(const GemmArgs&, hipStream_t);
-template hipError_t gemm_w4_split_layout<false, true>(const GemmArgs&, int, int64_t, float*,
+template hipError_t gemm_w4_split_layout<false, true>(const GemmArgs&, int, int64_t, void*,
                                                   hipStream_t);
 }  // namespace frisk

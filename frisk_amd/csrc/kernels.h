@@ -27,9 +27,23 @@ struct GemmArgs {
   int tile = 0, wave_m = 0, wave_n = 0;
 };
 
+// Workspace of a split-K launch that sums its slices in the GEMM kernel
+// (splitk_tree, gemm_common.h): an f32 partial tile per (tile, slice) of
+// bt x bt outputs, then kTreeWords 64-bit arrival words per tile.
+constexpr int kTreeWords = 64;
+// The 128x128 kernel's split-K sums at most this many slices inside its
+// launch (gemm_128.h); more go through gemm_splitk_sum.
+#ifndef FRISK_TREE_MAX_SLICES
+#define FRISK_TREE_MAX_SLICES 2
+#endif
+constexpr int kTreeMaxSlices = FRISK_TREE_MAX_SLICES;
+inline int64_t split_tree_bytes(int64_t tiles, int64_t slices, int bt) {
+  return tiles * slices * (int64_t)bt * bt * 4 + tiles * kTreeWords * 8;
+}
+
 // Split-K plan of the LDS-staged MFMA kernels (bf16/f16): `slices` slices
-// of kb_slice bytes of K whose f32 partials take workspace_bytes; slices == 1
-// runs unsplit.
+// of kb_slice bytes of K whose f32 partials and arrival words take
+// workspace_bytes; slices == 1 runs unsplit.
 struct SplitPlan {
   int slices;
   int64_t kb_slice;
@@ -57,11 +71,12 @@ hipError_t gemm_mfma(const GemmArgs& g, hipStream_t s, void* workspace, int64_t 
 hipError_t gemm_splitk_sum(const float* partial, int slices, const GemmArgs& g, hipStream_t s);
 // The kernels of one storage order (AM: A stored [K, M]; BM: B stored
 // [K, N]), instantiated in gemm_w4_a*b*.hip (256x256 tiles) and
-// gemm_128_a*b*.hip (128x128 tiles).  The split variants write f32 partials of
-// `slices` K slices of kb_slice bytes to `partial` and then sum them into C.
+// gemm_128_a*b*.hip (128x128 tiles).  The split variants run `slices` K
+// slices of kb_slice bytes in one launch, summed into C through the
+// workspace `ws` of split_tree_bytes.
 template <bool AM, bool BM> hipError_t gemm_w4_layout(const GemmArgs& g, hipStream_t s);
 template <bool AM, bool BM>
-hipError_t gemm_w4_split_layout(const GemmArgs& g, int slices, int64_t kb_slice, float* partial,
+hipError_t gemm_w4_split_layout(const GemmArgs& g, int slices, int64_t kb_slice, void* ws,
                                 hipStream_t s);
 template <bool AM, bool BM> hipError_t gemm_128_layout(const GemmArgs& g, hipStream_t s);
 // Bytes of K per row per pipeline stage of gemm_128_layout's launch: 128
@@ -75,7 +90,7 @@ inline int gemm_128_stage_bytes(const GemmArgs& g, int cus) {
 // 2x1 or 1x2), 64-byte stages.
 template <bool AM, bool BM> hipError_t gemm_128_grid_layout(const GemmArgs& g, hipStream_t s);
 template <bool AM, bool BM>
-hipError_t gemm_128_split_layout(const GemmArgs& g, int slices, int64_t kb_slice, float* partial,
+hipError_t gemm_128_split_layout(const GemmArgs& g, int slices, int64_t kb_slice, void* ws,
                                  hipStream_t s);
 // Any layout / shape; LDS-tiled FMA kernel.
 hipError_t gemm_generic_any(const GemmArgs& g, hipStream_t s);

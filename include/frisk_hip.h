@@ -89,7 +89,10 @@ typedef enum frisk_dtype {
  * frisk_gemm_workspace_size() bytes splits K over the whole GPU (f32
  * partial tiles, added in a fixed order, so the result does not depend on
  * timing); without it, or when the size is 0, the unsplit kernels run.
- * Calls that share a workspace must not overlap.
+ * Two slices are summed inside the GEMM launch, through partials and
+ * arrival words in the workspace; its contents before the call do not
+ * matter, and nothing needs clearing between calls.  Calls that share a
+ * workspace must not overlap.
  */
 typedef struct frisk_gemm_desc {
   int64_t m, n, k;
@@ -157,7 +160,9 @@ int64_t frisk_gemm_workspace_size(const frisk_gemm_desc* desc);
  * "a_major"/"b_major" ("k" = K-contiguous storage, "m"/"n" otherwise), the
  * LDS fragment read of each operand ("lds_read_a"/"lds_read_b":
  * ds_read_b128, or ds_read_b64_tr_b16 / _tr_b8 for an M/N-major operand),
- * "slices" (split-K) and "workspace_bytes".  desc->workspace_bytes is taken
+ * "slices" (split-K), "slice_sum" ("none", "in_launch": summed by the GEMM
+ * kernel itself, "second_launch": by a slice-sum kernel) and
+ * "workspace_bytes".  desc->workspace_bytes is taken
  * as the workspace a call would pass; pointers are not read.  No
  * counterpart in the reference, whose execution packet records the chosen
  * instruction contract instead (ExportExecution.cpp:46-295): this reports

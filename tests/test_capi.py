@@ -258,15 +258,18 @@ def gemm_size(**over):
 
 def test_gemm_workspace_size_query():
     # The plan assumes 256 CUs where no device answers (and MI355X has 256).
-    # 128 x 4096 x 4096 on 128 x 128 tiles: 32 tiles; 4 slices of 2 KiB of K
-    # (partials at most a quarter of the bytes of A and B: (M + N).K.2 /
-    # (16 M N) = 4; two workgroups per CU would take 16).
-    assert gemm_size() == 4 * 128 * 4096 * 4
-    # 256 x 4096 x 4096: 64 tiles, 2 slices (256x256 tiles are estimated
-    # less than 20% faster).
-    assert gemm_size(m=256) == 2 * 256 * 4096 * 4
-    # 512 x 4096 x 4096: 32 256x256 tiles in 8 slices of 1 KiB of K.
-    assert gemm_size(m=512) == 8 * 512 * 4096 * 4
+    # 128 x 4096 x 4096 on 128 x 128 tiles: 32 tiles; 8 slices of 1 KiB of
+    # K (one workgroup per CU; f32 partials at most the bytes of A and B),
+    # summed by a second launch: slices x M x N f32.
+    assert gemm_size() == 8 * 128 * 4096 * 4
+    # 256 x 4096 x 4096: 64 tiles, 4 slices.
+    assert gemm_size(m=256) == 4 * 256 * 4096 * 4
+    # 512 x 4096 x 4096: 128 tiles in 2 slices, summed inside the GEMM
+    # launch: a 128x128 f32 partial per (tile, slice), then 64 arrival
+    # words of 8 bytes per tile.
+    assert gemm_size(m=512) == 128 * 2 * 128 * 128 * 4 + 128 * 64 * 8
+    # 1024 x 4096 x 14336: 64 256x256 tiles in 4 slices (slice sum).
+    assert gemm_size(m=1024, k=14336, lda=14336, ldb=14336) == 4 * 1024 * 4096 * 4
     # 1024 x 4096 x 4096: 256 128x128 tiles already fill the CUs; no split.
     assert gemm_size(m=1024) == 0
     # 16 x 4096 x 14336 on the small-M kernel: 64-column tiles -> 64 tiles,
@@ -284,8 +287,8 @@ def test_gemm_workspace_size_query():
     assert gemm_size(m=4096) == 0
     assert gemm_size(k=256, lda=256, ldb=256) == 0
     # Every storage order splits alike (the kernels take all four).
-    assert gemm_size(trans_b=0) == 4 * 128 * 4096 * 4
-    assert gemm_size(trans_a=1, lda=128) == 4 * 128 * 4096 * 4
+    assert gemm_size(trans_b=0) == 8 * 128 * 4096 * 4
+    assert gemm_size(trans_a=1, lda=128) == 8 * 128 * 4096 * 4
     assert gemm_size(a_type=rt.E4M3, b_type=rt.E4M3) == 0
     assert gemm_size(m=0) == rt.EINVAL
     assert rt.load().frisk_gemm_workspace_size(None) == rt.EINVAL
@@ -334,9 +337,13 @@ def test_gemm_plan_every_layout_runs_on_the_matrix_cores():
     assert p["kernel"] == "gemm_skinny" and p["atom"] == "v_mfma_f32_16x16x32_bf16"
     # Split-K shows up in the plan when the workspace is there.
     p = plan(m=128, trans_b=0, workspace_bytes=1 << 30)
-    assert p["kernel"] == "gemm_128" and p["slices"] == 4
-    assert p["workspace_bytes"] == 4 * 128 * 4096 * 4
-    assert plan(m=128, trans_b=0)["slices"] == 1
+    assert p["kernel"] == "gemm_128" and p["slices"] == 8 and p["slice_sum"] == "second_launch"
+    assert p["workspace_bytes"] == 8 * 128 * 4096 * 4
+    p = plan(m=512, trans_b=0, workspace_bytes=1 << 30)
+    assert p["kernel"] == "gemm_128" and p["slices"] == 2 and p["slice_sum"] == "in_launch"
+    assert p["workspace_bytes"] == 128 * 2 * 128 * 128 * 4 + 128 * 64 * 8
+    p = plan(m=128, trans_b=0)
+    assert p["slices"] == 1 and p["slice_sum"] == "none"
 
 
 def test_gemm_plan_generic_cases():
@@ -424,7 +431,17 @@ def test_gemm_noalloc_rejects_before_any_device_work():
     assert rc == rt.EINVAL and msg.startswith("legacy-gemm-shape"), msg
     rc, msg = noalloc_call(workspace=16, workspace_bytes=1 << 20)
     assert rc == rt.EINVAL and "takes no workspace" in msg, msg
-    rc, msg = noalloc_call(m=768, n=8192, k=28672, lda=28672, ldb=28672, ldc=8192)
+    # The descriptor carries fake device pointers: it may only reach the
+    # call if the size check is certain to reject it before any launch, so
+    # the split's workspace is checked to exceed the scratch first (on a
+    # device with another CU count the plan could differ).
+    big = dict(m=768, n=8192, k=28672, lda=28672, ldb=28672, ldc=8192)
+    d = rt.GemmDesc(big["m"], big["n"], big["k"], 0, 1, rt.BF16, rt.BF16, rt.BF16, 1, 16,
+                    big["lda"], 16, big["ldb"], 16, big["ldc"], 1.0, 1.0, None, 0, 0, 0, 0, 0)
+    need = rt.load().frisk_gemm_workspace_size(ctypes.byref(d))
+    if need <= rt.NOALLOC_SCRATCH_BYTES:
+        pytest.skip(f"this device splits 768x8192x28672 into {need} bytes, within the scratch")
+    rc, msg = noalloc_call(**big)
     assert rc == rt.EUNSUP and "beyond the 67108864-byte scratch" in msg, msg
     assert rt.NOALLOC_SCRATCH_BYTES == 64 << 20
     assert "#define FRISK_GEMM_NOALLOC_SCRATCH_BYTES (64ll << 20)" in HEADER.read_text()

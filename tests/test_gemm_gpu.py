@@ -265,6 +265,65 @@ def test_split_k_small_m(m, n, k, in_dt, out_dt, accumulate):
         check(decode(c[torch.from_numpy(r).cuda()]), ref, in_dt, out_dt)
 
 
+# Split-K shapes by path: two slices of 128x128 tiles sum inside the GEMM
+# launch (the arrival tree in the workspace), more slices through the
+# separate slice sum; ragged M, N and K tails in both.
+TREE_SHAPES = [(128, 14336, 4096), (512, 4096, 4096), (200, 6000, 3000)]
+SUM_SHAPES = [(256, 4096, 4096), (128, 4096, 14336), (300, 1000, 6144)]
+
+
+@pytest.mark.parametrize("m,n,k", TREE_SHAPES + SUM_SHAPES)
+def test_split_k_workspace_contents_do_not_matter(m, n, k):
+    # The split's result does not depend on what the workspace held before
+    # the call (zeros, all-ones bytes, random bytes, or a previous call's
+    # partials and arrival words): bit for bit, and within the bf16
+    # tolerance of the fp64 oracle.
+    print(f"case split-k workspace m={m} n={n} k={k}", flush=True)
+    a = randn((m, k), 11 + m).to(torch.bfloat16)
+    b = randn((n, k), 12 + n).to(torch.bfloat16)
+    c = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+    plan = rt.gemm_plan(a, b, c, trans_b=True)
+    assert plan["slices"] >= 2, plan
+    need = rt.gemm_workspace_bytes(a, b, c, trans_b=True)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(m + n + k)
+    fills = [torch.zeros(need, dtype=torch.uint8, device="cuda"),
+             torch.full((need,), 0xFF, dtype=torch.uint8, device="cuda"),
+             torch.randint(0, 256, (need,), generator=g, dtype=torch.uint8, device="cuda")]
+    outs = []
+    for ws in fills + [fills[2]]:  # the last one again: the previous call's leftovers
+        rt.gemm(a, b, c, trans_b=True, workspace=ws)
+        torch.cuda.synchronize()
+        outs.append(c.clone())
+    for o in outs[1:]:
+        assert torch.equal(o.view(torch.int16), outs[0].view(torch.int16))
+    r = sample_rows(m, 32, m + n)
+    check(decode(outs[0][torch.from_numpy(r).cuda()]), reference(a, b, False, True, 1.0, 1.0, rows=r),
+          torch.bfloat16, torch.bfloat16)
+
+
+@pytest.mark.parametrize("slices", [2, 3, 4, 5, 6, 7, 8])
+@pytest.mark.parametrize("ta,tb", [(False, True), (True, False)], ids=["nt", "tn"])
+def test_split_k_every_slice_count(slices, ta, tb):
+    # M = 128, N = 256: 2 tiles of 128x128; K picks the slice count (8
+    # stages of 128 bytes per slice at least, so K = 512 * slices bf16
+    # elements gives `slices` slices).  Two slices take the in-launch tree,
+    # more the separate sum; both storage orders of the operands; f32 and
+    # bf16 outputs, accumulating into C.
+    m, n, k = 128, 256, 512 * slices + 40
+    print(f"case split-k slices={slices} ta={ta} tb={tb}", flush=True)
+    a, b, _, _ = make_operands(m, n, k, torch.bfloat16, ta, tb, seed=30 + slices)
+    for out_dt in (torch.float32, torch.bfloat16):
+        c0 = randn((m, n), 40 + slices).to(out_dt)
+        c = c0.clone()
+        plan = rt.gemm_plan(a, b, c, trans_a=ta, trans_b=tb)
+        assert plan["slices"] == slices, plan
+        rt.gemm(a, b, c, trans_a=ta, trans_b=tb, clear_accum=False)
+        torch.cuda.synchronize()
+        ref = reference(a, b, ta, tb, 1.0, 1.0) + decode(c0)
+        check(decode(c), ref, torch.bfloat16, out_dt)
+
+
 def test_config_c1_fp32_512():
     # fp32 C = A.B, row-major A and B, U[-1, 1].
     rng = np.random.default_rng(0)

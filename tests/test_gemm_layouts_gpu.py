@@ -114,7 +114,7 @@ def test_strided_views_and_ragged_n(ta, tb):
     assert torch.all(cb[:, n:] == 7.0), "wrote past the ragged last column"
 
 
-SPLIT = [(128, 4096, 4096, "gemm_128"), (512, 4096, 4096, "gemm_w4"), (100, 1000, 3000, "gemm_128")]
+SPLIT = [(128, 4096, 4096, "gemm_128"), (384, 4096, 8192, "gemm_w4"), (100, 1000, 3000, "gemm_128")]
 
 
 @pytest.mark.parametrize("ta,tb", LAYOUTS, ids=LAYOUT_IDS)

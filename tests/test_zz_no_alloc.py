@@ -12,13 +12,17 @@ from tests.gpu_util import randn
 
 pytestmark = pytest.mark.gpu
 
-# (m, n, k, trans_a, trans_b, kernel the split runs on), largest scratch
-# first: 64 MiB (the whole array) on 256x256 tiles, 8 MiB on 128x128 tiles,
-# 1 MiB on the small-M kernel, then a GEMM that needs no scratch at all.
-CASES = [(512, 4096, 4096, False, True, "gemm_w4"),
-         (128, 4096, 4096, False, False, "gemm_128"),
-         (16, 4096, 14336, False, True, "gemm_skinny"),
-         (1024, 1024, 1024, True, False, None)]
+# (m, n, k, trans_a, trans_b, kernel the split runs on, slices), largest
+# scratch first: 64 MiB (the whole array) on 256x256 tiles through the
+# separate slice sum, 16 MiB on 128x128 tiles through the slice sum,
+# 14 MiB on 128x128 tiles summed inside the launch (two slices, with
+# arrival words), 1 MiB on the small-M kernel, then a GEMM that needs no
+# scratch at all.
+CASES = [(1024, 4096, 14336, False, True, "gemm_w4", 4),
+         (128, 4096, 4096, False, False, "gemm_128", 8),
+         (128, 14336, 4096, True, True, "gemm_128", 2),
+         (16, 4096, 14336, False, True, "gemm_skinny", 4),
+         (1024, 1024, 1024, True, False, None, 1)]
 
 
 def operands(m, n, k, ta, tb, seed):
@@ -30,7 +34,7 @@ def operands(m, n, k, ta, tb, seed):
 @pytest.mark.parametrize("out_dt", [torch.bfloat16, torch.float32], ids=["bf16", "f32"])
 @pytest.mark.parametrize("accumulate", [False, True], ids=["clear", "accum"])
 def test_noalloc_matches_frisk_gemm_with_workspace(out_dt, accumulate):
-    for i, (m, n, k, ta, tb, kernel) in enumerate(CASES):
+    for i, (m, n, k, ta, tb, kernel, slices) in enumerate(CASES):
         print(f"case noalloc m={m} n={n} k={k} ta={ta} tb={tb} out={out_dt} accumulate={accumulate}",
               flush=True)
         a, b = operands(m, n, k, ta, tb, seed=31 + i)
@@ -41,7 +45,7 @@ def test_noalloc_matches_frisk_gemm_with_workspace(out_dt, accumulate):
         if kernel is None:
             assert need == 0 and p["slices"] == 1
         else:
-            assert need > 0 and p["slices"] > 1 and p["kernel"] == kernel, p
+            assert need > 0 and p["slices"] == slices and p["kernel"] == kernel, p
         want = c0.clone()
         ws = torch.empty(max(need, 16), dtype=torch.uint8, device="cuda")
         rt.gemm(a, b, want, trans_a=ta, trans_b=tb, clear_accum=not accumulate, workspace=ws)
@@ -68,3 +72,59 @@ def test_noalloc_repeated_on_one_stream():
         rt.gemm(a, b, want, trans_b=True, workspace=True)
         torch.cuda.synchronize()
         assert torch.equal(c, want)
+
+
+def test_noalloc_allocates_no_device_memory():
+    # Device free memory (hipMemGetInfo, through torch) is the same before
+    # and after a run of split calls, each a different plan; one call per
+    # plan first loads the kernels' code objects, whose loading takes
+    # device memory of its own.
+    ops = []
+    for i, (m, n, k, ta, tb, _, _) in enumerate(CASES):
+        a, b = operands(m, n, k, ta, tb, seed=51 + i)
+        c = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+        ops.append((a, b, c, ta, tb))
+    for a, b, c, ta, tb in ops:
+        rt.gemm_noalloc(a, b, c, trans_a=ta, trans_b=tb)
+    torch.cuda.synchronize()
+    free0, _ = torch.cuda.mem_get_info()
+    for _ in range(3):
+        for a, b, c, ta, tb in ops:
+            rt.gemm_noalloc(a, b, c, trans_a=ta, trans_b=tb)
+    torch.cuda.synchronize()
+    free1, _ = torch.cuda.mem_get_info()
+    assert free1 == free0, f"device free memory moved by {free0 - free1} bytes"
+
+
+@pytest.mark.parametrize("case", [0, 2, 3], ids=["w4-sum", "128-tree", "skinny"])
+def test_noalloc_captured_in_a_graph(case):
+    # A split-K noalloc call captured in a HIP graph (after one call outside
+    # capture, which resolves the scratch address on this device and loads
+    # the kernels), replayed several times with other work and host
+    # synchronisations between the replays: every replay equals frisk_gemm
+    # with a workspace, bit for bit.
+    m, n, k, ta, tb, _, _ = CASES[case]
+    a, b = operands(m, n, k, ta, tb, seed=61 + case)
+    c = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+    want = torch.empty_like(c)
+    rt.gemm(a, b, want, trans_a=ta, trans_b=tb, workspace=True)
+    rt.gemm_noalloc(a, b, c, trans_a=ta, trans_b=tb)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            rt.gemm_noalloc(a, b, c, trans_a=ta, trans_b=tb)
+    torch.cuda.current_stream().wait_stream(s)
+    other = torch.empty_like(c)
+    for r in range(4):
+        c.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(c, want), f"replay {r} differs from frisk_gemm"
+        # Eager work on the scratch's plans between replays.
+        rt.gemm_noalloc(a, b, other, trans_a=ta, trans_b=tb)
+        torch.cuda.synchronize()
+        assert torch.equal(other, want)
