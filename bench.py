@@ -94,14 +94,17 @@ def make_workloads(torch, rt):
             return lambda: rt.gemm(a, b, c, trans_a=trans_a, trans_b=trans_b)
         return setup
 
-    def attn(causal):
+    def attn(causal, k_transposed=False):
         def setup():
             shape = (4, 32, 4096, 128)
             q = torch.randn(shape, generator=gen(5), device=dev).to(torch.bfloat16)
             k = torch.randn(shape, generator=gen(6), device=dev).to(torch.bfloat16)
             v = torch.randn(shape, generator=gen(7), device=dev).to(torch.bfloat16)
             o = torch.empty_like(q)
-            return lambda: rt.attn_fwd(q, k, v, o, causal=causal, sm_scale=128 ** -0.5)
+            if k_transposed:  # K stored [B, H, D, S], read in place
+                k = k.transpose(-1, -2).contiguous()
+            return lambda: rt.attn_fwd(q, k, v, o, causal=causal, sm_scale=128 ** -0.5,
+                                       k_transposed=k_transposed)
         return setup
 
     def library_gemm(m, n, k):
@@ -165,6 +168,10 @@ def make_workloads(torch, rt):
         "gemm_int8_4096": ("int8", 2.0 * 4096 ** 3, gemm(4096, 4096, 4096, "int8")),
         "fa_fwd_b4h32s4096d128": ("bf16", fa, attn(False)),
         "fa_fwd_b4h32s4096d128_causal": ("bf16", fa / 2, attn(True)),
+        # K stored [B, H, D, S]: the reference's FA tile program layout
+        # (tmp/ir.mlir:89-92), read in place.
+        "fa_fwd_b4h32s4096d128_kt": ("bf16", fa, attn(False, True)),
+        "fa_fwd_b4h32s4096d128_kt_causal": ("bf16", fa / 2, attn(True, True)),
         "fa_fwd_d64_b2h32s1025_f16_f32out": ("f16", 4.0 * 2 * 32 * 1025 * 1025 * 64, attn_d64()),
         # HBM-bound tile ops: second entry = algorithmic bytes per launch.
         "reduce_sum_f32_32768x4096_rows": ("hbm", 32768 * 4096 * 4 + 32768 * 4,

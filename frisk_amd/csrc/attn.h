@@ -29,6 +29,12 @@
 //  * K and V tiles (64 keys x 2D bytes each) arrive by LDS-DMA with XOR
 //    swizzles chosen for their read patterns, double-buffered: the loads of
 //    key block j+1 are in flight during the MFMAs and softmax of block j.
+//  * K stored [batch, heads, head_dim, seq] (KT; the layout of the
+//    reference's FA tile program, tmp/ir.mlir:92) is staged as head_dim rows
+//    of 64 keys and its fragments come from the same transposing LDS read
+//    as V^T's, which delivers head_dim in the order (e < 4 ? 4h+e :
+//    8+4h+e-4) per lane half h; the Q fragments are loaded in that order
+//    too, so the products pair up and no transpose or copy of K is made.
 //    Below head_dim 32 the V rows are padded to 32 dims in LDS (the DMA
 //    writes zeros there), so O^T keeps its 32-row MFMA tile; the padded rows
 //    are never stored.
@@ -110,6 +116,10 @@ template <int D> struct AttnGeom {
   static constexpr int kH2 = kKSteps - kH1;
   static constexpr int kDT = kDP / 32;               // O^T tiles of 32 dims
   __device__ static int swz_k(int r) { return (r >> kKShift) & (kKC - 1); }
+  // K^T rows (K stored head_dim-major): 64 keys = 8 chunks, read by the
+  // transposing pattern of V^T at 8 chunks per row, so V's swizzle for
+  // that width.
+  __device__ static int swz_kt(int r) { return 2 * ((r >> 1) & 1); }
   __device__ static int swz_v(int r) {
     if constexpr (kVC == 16) return 4 * (r & 3);
     else if constexpr (kVC == 8) return 2 * ((r >> 1) & 1);
@@ -135,7 +145,7 @@ __device__ __forceinline__ float pair_reduce(float x, bool max_op) {
 
 // QT query tiles of 32 per wave, NW waves per workgroup:
 // BM = 32 * QT * NW queries per workgroup.  OUT is T or F32.
-template <Elt T, Elt OUT, int D, int QT, int NW, bool CAUSAL>
+template <Elt T, Elt OUT, int D, int QT, int NW, bool CAUSAL, bool KT = false>
 __global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(
     const char* __restrict__ Q, const char* __restrict__ K, const char* __restrict__ V,
     char* __restrict__ O, float* __restrict__ LSE, int heads, int seq_q, int seq_k,
@@ -190,14 +200,26 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(
     const char* vh = V + (b * v_sb + h * v_sh) * 2;
 
     // ---- Q fragments (B operand of S^T = K.Q^T), loaded once -------------
+    // Lane half h holds head_dim 16ds + 8h .. +7 of its query, or with KT
+    // 16ds + 4h .. +3 and 16ds + 8 + 4h .. +3 (the order the transposing
+    // read gives the K^T fragments).
     const int wq0 = q0 + wave * 32 * QT;  // first query of this wave
     i32x4 qf[QT][G::kKSteps];
 #pragma unroll
     for (int t = 0; t < QT; ++t) {
       const int qi = min(wq0 + t * 32 + l32, seq_q - 1);
-      const char* row = qh + (int64_t)qi * q_ss * 2 + half * 16;
+      const char* row = qh + (int64_t)qi * q_ss * 2;
 #pragma unroll
-      for (int ds = 0; ds < G::kKSteps; ++ds) qf[t][ds] = *(const i32x4*)(row + ds * 32);
+      for (int ds = 0; ds < G::kKSteps; ++ds) {
+        if constexpr (KT) {
+          typedef int i32x2 __attribute__((ext_vector_type(2)));
+          const i32x2 lo = *(const i32x2*)(row + ds * 32 + half * 8);
+          const i32x2 hi = *(const i32x2*)(row + ds * 32 + 16 + half * 8);
+          qf[t][ds] = i32x4{lo[0], lo[1], hi[0], hi[1]};
+        } else {
+          qf[t][ds] = *(const i32x4*)(row + ds * 32 + half * 16);
+        }
+      }
     }
 
     // ---- K and V tiles by LDS-DMA -------------------------------------------
@@ -205,8 +227,13 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(
     // physical chunk L % chunks-per-row, and fetches the logical chunk that
     // the row's swizzle puts there.  Rows past seq_k and the V padding dims
     // (head_dim < 32) read zeros (offsets past the buffer range).
+    // With KT, k_ss is the stride between head_dim rows of K^T and keys
+    // are contiguous: a row holds seq_k keys.
     const __amdgpu_buffer_rsrc_t rsk = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)kh, (short)0, (int)min((int64_t)(seq_k - 1) * k_ss * 2 + D * 2, (int64_t)0x7fffffff),
+        (void*)kh, (short)0,
+        (int)min(KT ? (int64_t)(D - 1) * k_ss * 2 + (int64_t)seq_k * 2
+                    : (int64_t)(seq_k - 1) * k_ss * 2 + D * 2,
+                 (int64_t)0x7fffffff),
         0x00020000);
     const __amdgpu_buffer_rsrc_t rsv = __builtin_amdgcn_make_buffer_rsrc(
         (void*)vh, (short)0, (int)min((int64_t)(seq_k - 1) * v_ss * 2 + D * 2, (int64_t)0x7fffffff),
@@ -217,10 +244,18 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(
     int k_row[kKI], v_row[kVI];
 #pragma unroll
     for (int i = 0; i < kKI; ++i) {
-      const int r = (wave * kKI + i) * (1024 / G::kRB) + lane / G::kKC;
-      const int c = (lane % G::kKC) ^ G::swz_k(r);
-      k_row[i] = (wave * kKI + i) < kKIns ? r : 1 << 30;
-      k_off[i] = (uint32_t)(r * k_ss * 2) + (c << 4);
+      if constexpr (KT) {
+        // Row r of the K^T tile: head_dim index r, 64 keys (8 chunks).
+        const int r = (wave * kKI + i) * 8 + lane / 8;
+        const int c = (lane % 8) ^ G::swz_kt(r);
+        k_row[i] = (wave * kKI + i) < kKIns ? c * 8 : 1 << 30;  // first key of the chunk
+        k_off[i] = (uint32_t)(r * k_ss * 2) + (c << 4);
+      } else {
+        const int r = (wave * kKI + i) * (1024 / G::kRB) + lane / G::kKC;
+        const int c = (lane % G::kKC) ^ G::swz_k(r);
+        k_row[i] = (wave * kKI + i) < kKIns ? r : 1 << 30;
+        k_off[i] = (uint32_t)(r * k_ss * 2) + (c << 4);
+      }
     }
 #pragma unroll
     for (int i = 0; i < kVI; ++i) {
@@ -230,7 +265,8 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(
       v_off[i] = (uint32_t)(r * v_ss * 2) + (c << 4);
     }
     auto issue_k = [&](int kb, char* dst) {
-      const uint32_t kbase = (uint32_t)((int64_t)kb * kBN * k_ss * 2);
+      // A K block starts kBN keys further: kBN rows, or with KT kBN columns.
+      const uint32_t kbase = (uint32_t)(KT ? (int64_t)kb * kBN * 2 : (int64_t)kb * kBN * k_ss * 2);
 #pragma unroll
       for (int i = 0; i < kKI; ++i) {
         if ((wave * kKI + i) >= kKIns) continue;  // wave-uniform
@@ -275,6 +311,21 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(
       }
     }
 
+    // K^T fragments (KT) by the same transposing read: lane 4e+q of group G
+    // (h = G/2, kg = G%2) reads K^T[16ds + 4h + e (+8)][32kt + 16kg + 4q ..
+    // +3], so lane l receives head_dim 16ds + 4h + 0..3 (+8) of key
+    // 32kt + l%32: the A operand of S^T = K.Q^T in the head_dim order of
+    // the Q fragments above.
+    int kt_off[2];
+    if constexpr (KT) {
+      const int g = lane >> 4, hh = g >> 1, kg = g & 1, e = (lane >> 2) & 3, q = lane & 3;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        const int chunk = (4 * kt + 2 * kg + (q >> 1)) ^ G::swz_kt(4 * hh + e);
+        kt_off[kt] = (4 * hh + e) * 128 + (chunk << 4) + 8 * (q & 1);
+      }
+    }
+
     // ---- state ---------------------------------------------------------------
     f32x16 o[QT][G::kDT];
     float m[QT], l[QT];
@@ -294,9 +345,19 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(
       for (int kt = 0; kt < 2; ++kt) {
         const int r = kt * 32 + l32;
 #pragma unroll
-        for (int i = 0; i < n; ++i)
-          kf[kt][i] =
-              *(const i32x4*)(ks + r * G::kRB + (((2 * (h0 + i) + half) ^ G::swz_k(r)) << 4));
+        for (int i = 0; i < n; ++i) {
+          if constexpr (KT) {
+            const char* p = ks + kt_off[kt] + (h0 + i) * 16 * 128;
+            const s16x4 lo = lds_read_tr16(p);
+            const s16x4 hi = lds_read_tr16(p + 8 * 128);
+            typedef int i32x2 __attribute__((ext_vector_type(2)));
+            const i32x2 a = __builtin_bit_cast(i32x2, lo), b = __builtin_bit_cast(i32x2, hi);
+            kf[kt][i] = i32x4{a[0], a[1], b[0], b[1]};
+          } else {
+            kf[kt][i] =
+                *(const i32x4*)(ks + r * G::kRB + (((2 * (h0 + i) + half) ^ G::swz_k(r)) << 4));
+          }
+        }
       }
     };
     // V^T fragments of key steps k0, k0+1 (16 keys each).
@@ -499,10 +560,10 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(
 }
 
 // One workgroup shape: NW waves x 32 queries.
-template <Elt T, Elt OUT, int D, int NW, bool CAUSAL>
+template <Elt T, Elt OUT, int D, int NW, bool CAUSAL, bool KT>
 static hipError_t launch_attn_nw(const AttnArgs& a, hipStream_t stream) {
   constexpr int QT = 1, BM = 32 * QT * NW;
-  auto kern = attn_fwd_kernel<T, OUT, D, QT, NW, CAUSAL>;
+  auto kern = attn_fwd_kernel<T, OUT, D, QT, NW, CAUSAL, KT>;
   constexpr int lds = 2 * AttnGeom<D>::kBuf;
   static const hipError_t attr =
       hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
@@ -537,10 +598,10 @@ static hipError_t launch_attn_nw(const AttnArgs& a, hipStream_t stream) {
 // b4 h32 s4096 d64 617 vs 630 (causal 336 vs 348), b8 h8 s1024 d64 causal
 // 22.6 vs 33.4, ties elsewhere; only s256 causal favoured 8 (11.6 vs 12.8).
 // Head_dim 64 and below always take 4 waves.
-template <Elt T, Elt OUT, int D, bool CAUSAL>
-static hipError_t launch_attn(const AttnArgs& a, hipStream_t stream) {
+template <Elt T, Elt OUT, int D, bool CAUSAL, bool KT>
+static hipError_t launch_attn_kt(const AttnArgs& a, hipStream_t stream) {
   if constexpr (D <= 64) {
-    return launch_attn_nw<T, OUT, D, 4, CAUSAL>(a, stream);
+    return launch_attn_nw<T, OUT, D, 4, CAUSAL, KT>(a, stream);
   } else {
     // Workgroups of bm queries (under a causal mask, pairs of query blocks).
     const int64_t bh = a.batch * a.heads;
@@ -553,9 +614,16 @@ static hipError_t launch_attn(const AttnArgs& a, hipStream_t stream) {
     const double t8 = (double)((w8 + cus - 1) / cus);
     const int64_t rest4 = w4 % (2 * cus);
     const double t4 = (double)(w4 / (2 * cus)) + (rest4 == 0 ? 0.0 : rest4 <= cus ? 0.6 : 1.0);
-    return t4 < t8 ? launch_attn_nw<T, OUT, D, 4, CAUSAL>(a, stream)
-                   : launch_attn_nw<T, OUT, D, 8, CAUSAL>(a, stream);
+    return t4 < t8 ? launch_attn_nw<T, OUT, D, 4, CAUSAL, KT>(a, stream)
+                   : launch_attn_nw<T, OUT, D, 8, CAUSAL, KT>(a, stream);
   }
+}
+
+// K stored [.., seq, head_dim] or [.., head_dim, seq] (a.k_dmajor).
+template <Elt T, Elt OUT, int D, bool CAUSAL>
+static hipError_t launch_attn(const AttnArgs& a, hipStream_t stream) {
+  return a.k_dmajor ? launch_attn_kt<T, OUT, D, CAUSAL, true>(a, stream)
+                    : launch_attn_kt<T, OUT, D, CAUSAL, false>(a, stream);
 }
 
 // Every (input dtype, output dtype, mask) variant of one head_dim.

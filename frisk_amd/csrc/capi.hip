@@ -423,17 +423,34 @@ int frisk_attn_fwd(const frisk_attn_desc* d, void* stream) {
   for (int i = 0; i < 12; ++i)
     if (strides[i] % 8 != 0 || strides[i] < 0)
       return fail(FRISK_EINVAL, "frisk_attn_fwd: strides must be non-negative multiples of 8 elements");
-  if (d->q_stride_s < d->head_dim || d->k_stride_s < d->head_dim ||
+  if (d->k_transposed != 0 && d->k_transposed != 1)
+    return fail(FRISK_EINVAL, "frisk_attn_fwd: k_transposed must be 0 or 1 (got %d)",
+                (int)d->k_transposed);
+  const bool kt = d->k_transposed != 0;
+  if (d->q_stride_s < d->head_dim || (!kt && d->k_stride_s < d->head_dim) ||
       d->v_stride_s < d->head_dim || d->o_stride_s < d->head_dim)
     return fail(FRISK_EINVAL, "frisk_attn_fwd: sequence stride smaller than head_dim");
+  if (kt && d->k_stride_s < d->seq_k)
+    return fail(FRISK_EINVAL, "frisk_attn_fwd: transposed K needs a head_dim row stride of at "
+                              "least seq_k (got %lld < %lld)",
+                (long long)d->k_stride_s, (long long)d->seq_k);
+  // The loads of a transposed K stop at its last key with 4-byte
+  // granularity (a buffer range check zeroes each dword that extends past
+  // the end), so with an odd seq_k the last key of the last head_dim row
+  // would share a zeroed dword with the element after it.
+  if (kt && d->seq_k % 2 != 0)
+    return fail(FRISK_EUNSUP, "frisk_attn_fwd: transposed K needs an even seq_k (got %lld)",
+                (long long)d->seq_k);
   if (!(d->sm_scale > 0.0f) || !__builtin_isfinite(d->sm_scale))
     return fail(FRISK_EINVAL, "frisk_attn_fwd: sm_scale must be positive and finite");
   if (d->seq_q > INT32_MAX / 2 || d->seq_k > INT32_MAX / 2 || d->batch * d->heads > INT32_MAX / 2)
     return fail(FRISK_EUNSUP, "frisk_attn_fwd: sizes beyond the 32-bit index range");
   // K and V are read through buffer loads with 32-bit offsets from the
-  // head's first row: the last key row must end within 2^31 - 1 bytes.
-  const int64_t kv_reach = (d->seq_k - 1) * std::max(d->k_stride_s, d->v_stride_s) * 2 +
-                           d->head_dim * 2;
+  // head's first row: the last key row (with a transposed K, the last
+  // head_dim row of seq_k keys) must end within 2^31 - 1 bytes.
+  const int64_t k_reach = kt ? (d->head_dim - 1) * d->k_stride_s * 2 + d->seq_k * 2
+                             : (d->seq_k - 1) * d->k_stride_s * 2 + d->head_dim * 2;
+  const int64_t kv_reach = std::max(k_reach, (d->seq_k - 1) * d->v_stride_s * 2 + d->head_dim * 2);
   if (kv_reach > INT32_MAX)
     return fail(FRISK_EUNSUP, "frisk_attn_fwd: K/V rows span %lld bytes of one head, beyond the "
                               "2^31 - 1 bytes the kernel addresses",
@@ -448,6 +465,7 @@ int frisk_attn_fwd(const frisk_attn_desc* d, void* stream) {
   a.sm_scale = d->sm_scale;
   a.q = d->q; a.q_sb = d->q_stride_b; a.q_sh = d->q_stride_h; a.q_ss = d->q_stride_s;
   a.k = d->k; a.k_sb = d->k_stride_b; a.k_sh = d->k_stride_h; a.k_ss = d->k_stride_s;
+  a.k_dmajor = kt ? 1 : 0;
   a.v = d->v; a.v_sb = d->v_stride_b; a.v_sh = d->v_stride_h; a.v_ss = d->v_stride_s;
   a.o = d->o; a.o_sb = d->o_stride_b; a.o_sh = d->o_stride_h; a.o_ss = d->o_stride_s;
   a.lse = d->lse;

@@ -123,7 +123,8 @@ struct AttnArgs {
   const void* q;
   int64_t q_sb, q_sh, q_ss;
   const void* k;
-  int64_t k_sb, k_sh, k_ss;
+  int64_t k_sb, k_sh, k_ss;  // k_ss: between keys, or with k_dmajor between head_dim rows
+  int k_dmajor;              // K stored [batch, heads, head_dim, seq]
   const void* v;
   int64_t v_sb, v_sh, v_ss;
   void* o;

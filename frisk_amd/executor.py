@@ -547,7 +547,7 @@ def execute(module, kernel: str, tensors: Sequence, *, stream=None, causal: bool
                        clear_accum=p.clear_accum, scale_a=scale_a, scale_b=scale_b, stream=stream,
                        variant=p.variant)
     q, kk, v, o = (tensors[i] for i in (p.q, p.k, p.v, p.o))
-    if p.k_transposed:
-        kk = kk.transpose(-1, -2)  # [B, H, S, D] view; the C-ABI needs unit D stride
-        kk = kk.contiguous()
-    return rt.attn_fwd(q, kk, v, o, causal=causal, sm_scale=sm_scale, stream=stream)
+    # A K stored [B, H, D, S] (the reference's FA tile program) is read in
+    # place by the kernel's transposed-K variant.
+    return rt.attn_fwd(q, kk, v, o, causal=causal, sm_scale=sm_scale, stream=stream,
+                       k_transposed=p.k_transposed)

@@ -26,7 +26,7 @@ EXPORTS = ("frisk_gemm", "frisk_gemm_workspace_size", "frisk_gemm_plan", "frisk_
            "frisk_copy", "frisk_fill",
            "frisk_last_error", "frisk_abi_version", "frisk_probe_mfma_layout",
            "frisk_probe_lds_transpose")
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 REDUCE_SUM, REDUCE_MAX, REDUCE_MIN = 0, 1, 2
 REDUCE_KINDS = {"sum": REDUCE_SUM, "add": REDUCE_SUM, "max": REDUCE_MAX, "min": REDUCE_MIN}
@@ -63,6 +63,7 @@ class AttnDesc(ctypes.Structure):
         ("o_stride_s", ctypes.c_int64),
         ("lse", ctypes.c_void_p),
         ("o_dtype", ctypes.c_int32),
+        ("k_transposed", ctypes.c_int32),
     ]
 
 
@@ -297,18 +298,23 @@ def probe_lds_transpose(bits: int, out, stream=None):
     return out
 
 
-def attn_desc(q, k, v, o, *, causal=False, sm_scale=None, lse=None) -> AttnDesc:
+def attn_desc(q, k, v, o, *, causal=False, sm_scale=None, lse=None,
+              k_transposed=False) -> AttnDesc:
+    """Describe the attention forward of [batch, heads, seq, head_dim] device
+    tensors; with k_transposed, K is [batch, heads, head_dim, seq_k] with unit
+    key stride (read in place, not copied)."""
     shapes, strides = [], []
     for name, t in (("Q", q), ("K", k), ("V", v), ("O", o)):
         sh, st = t.shape, t.stride()
         if len(sh) != 4 or st[3] != 1 or not t.is_cuda:
-            raise ValueError(f"{name} must be a [batch, heads, seq, head_dim] device tensor "
-                             "with unit head_dim stride")
+            inner = "seq_k" if name == "K" and k_transposed else "head_dim"
+            raise ValueError(f"{name} must be a rank-4 device tensor with unit {inner} stride")
         shapes.append(tuple(sh))
         strides.append(st)
     b, h, sq, d = shapes[0]
-    sk = shapes[1][2]
-    if shapes[1] != (b, h, sk, d) or shapes[2] != (b, h, sk, d) or shapes[3] != (b, h, sq, d):
+    sk = shapes[1][3] if k_transposed else shapes[1][2]
+    k_shape = (b, h, d, sk) if k_transposed else (b, h, sk, d)
+    if shapes[1] != k_shape or shapes[2] != (b, h, sk, d) or shapes[3] != (b, h, sq, d):
         raise ValueError("attention shapes disagree")
     if not (q.dtype == k.dtype == v.dtype):
         raise ValueError("Q/K/V must share one dtype")
@@ -327,12 +333,16 @@ def attn_desc(q, k, v, o, *, causal=False, sm_scale=None, lse=None) -> AttnDesc:
                     k.data_ptr(), ks[0], ks[1], ks[2],
                     v.data_ptr(), vs[0], vs[1], vs[2],
                     o.data_ptr(), os_[0], os_[1], os_[2],
-                    lse.data_ptr() if lse is not None else None, torch_dtype_code(o.dtype))
+                    lse.data_ptr() if lse is not None else None, torch_dtype_code(o.dtype),
+                    int(bool(k_transposed)))
 
 
-def attn_fwd(q, k, v, o, *, causal=False, sm_scale=None, lse=None, stream=None):
-    """O = softmax(sm_scale . Q K^T [causal mask]) V on the GPU."""
-    d = attn_desc(q, k, v, o, causal=causal, sm_scale=sm_scale, lse=lse)
+def attn_fwd(q, k, v, o, *, causal=False, sm_scale=None, lse=None, stream=None,
+             k_transposed=False):
+    """O = softmax(sm_scale . Q K^T [causal mask]) V on the GPU.  K is
+    [batch, heads, seq_k, head_dim], or [batch, heads, head_dim, seq_k] with
+    k_transposed=True (read in place)."""
+    d = attn_desc(q, k, v, o, causal=causal, sm_scale=sm_scale, lse=lse, k_transposed=k_transposed)
     _check(load().frisk_attn_fwd(ctypes.byref(d), ctypes.c_void_p(_stream_handle(stream))),
            "frisk_attn_fwd")
     return o

@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define FRISK_ABI_VERSION 6
+#define FRISK_ABI_VERSION 7
 
 /* Element types (the dtype strings of ffi/ir.cpp:399-411 plus bf16/i8/i32). */
 typedef enum frisk_dtype {
@@ -180,6 +180,12 @@ int frisk_gemm_plan(const frisk_gemm_desc* desc, char* buf, int64_t len);
  * innermost (head_dim) stride is 1.  lse, if non-NULL, receives the f32
  * natural-log row log-sum-exp of the scaled scores, laid out
  * [batch, heads, seq_q] contiguous.
+ *
+ * k_transposed = 1 takes K stored [batch, heads, head_dim, seq_k] with unit
+ * key stride (the layout of the reference's FA tile program, K as
+ * memref<1x32x128x4096>, tmp/ir.mlir:89-92); k_stride_s is then the stride
+ * between head_dim rows (at least seq_k), and seq_k must be even (odd:
+ * FRISK_EUNSUP).  The kernel reads it in place.
  */
 typedef struct frisk_attn_desc {
   int64_t batch, heads, seq_q, seq_k, head_dim;
@@ -195,7 +201,8 @@ typedef struct frisk_attn_desc {
   void* o;
   int64_t o_stride_b, o_stride_h, o_stride_s;
   float* lse;
-  int32_t o_dtype; /* frisk_dtype: equal to dtype, or FRISK_F32 */
+  int32_t o_dtype;      /* frisk_dtype: equal to dtype, or FRISK_F32 */
+  int32_t k_transposed; /* 0: K [b, h, seq_k, head_dim]; 1: K [b, h, head_dim, seq_k] */
 } frisk_attn_desc;
 
 int frisk_attn_fwd(const frisk_attn_desc* desc, void* stream);

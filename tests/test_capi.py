@@ -84,6 +84,14 @@ def attn_call(**over):
     (dict(v_stride_s=64), rt.EINVAL, "frisk_attn_fwd: sequence stride"),
     (dict(sm_scale=0.0), rt.EINVAL, "frisk_attn_fwd: sm_scale"),
     (dict(o=0), rt.EINVAL, "frisk_attn_fwd: null"),
+    (dict(k_transposed=2), rt.EINVAL, "frisk_attn_fwd: k_transposed must be 0 or 1"),
+    # K stored [b, h, head_dim, seq_k]: its row stride runs over keys.
+    (dict(k_transposed=1, seq_k=4096, k_stride_s=2048, k_stride_h=262144, k_stride_b=262144),
+     rt.EINVAL, "frisk_attn_fwd: transposed K needs a head_dim row stride of at least seq_k"),
+    (dict(k_transposed=1, seq_k=65, seq_q=65, k_stride_s=72, k_stride_h=9216, k_stride_b=9216),
+     rt.EUNSUP, "frisk_attn_fwd: transposed K needs an even seq_k"),
+    (dict(k_transposed=1, seq_k=64, k_stride_s=(1 << 24), k_stride_h=(1 << 31),
+          k_stride_b=(1 << 31)), rt.EUNSUP, "frisk_attn_fwd: K/V rows span"),
 ])
 def test_attn_rejects_invalid_requests(over, code, prefix):
     rc, msg = attn_call(**over)
