@@ -35,7 +35,8 @@ from pathlib import Path
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
-PEAK = {"bf16": 2500.0, "f16": 2500.0, "fp8": 5000.0, "int8": 5000.0}  # dense TFLOP/s (TOP/s)
+PEAK = {"bf16": 2500.0, "f16": 2500.0, "fp8": 5000.0, "int8": 5000.0,
+        "f32": 157.3}  # dense TFLOP/s (TOP/s)
 REF_FIXED_TILE_US = {"single": 21.584, "graph": 6.5386}  # the reference's published H100 figures
 HBM_PEAK_GBS = 8000.0
 PEAK_MHZ = 2400.0  # shader clock of the published MFMA peaks
@@ -87,7 +88,7 @@ def make_workloads(torch, rt):
                 c = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
                 return lambda: rt.gemm(a8, b8, c, trans_a=trans_a, trans_b=trans_b,
                                        scale_a=1 / sa, scale_b=1 / sb)
-            dt = torch.bfloat16 if kind == "bf16" else torch.float16
+            dt = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}[kind]
             a = torch.randn(a_shape, generator=gen(1), device=dev).to(dt)
             b = torch.randn(b_shape, generator=gen(2), device=dev).to(dt)
             c = torch.empty(m, n, dtype=dt, device=dev)
@@ -166,6 +167,10 @@ def make_workloads(torch, rt):
         "gemm_fp8_4096x8192x8192": ("fp8", 2.0 * 4096 * 8192 * 8192,
                                     gemm(4096, 8192, 8192, "fp8")),
         "gemm_int8_4096": ("int8", 2.0 * 4096 ** 3, gemm(4096, 4096, 4096, "int8")),
+        # fp32 on v_mfma_f32_32x32x2_f32: the reference's GEMM tile program
+        # (fp32 1024^3, B [K, N], tmp/ir.mlir:2-16) and configs[0] (512^3).
+        "gemm_f32_1024_nn": ("f32", 2.0 * 1024 ** 3, gemm(1024, 1024, 1024, "f32", False, False)),
+        "gemm_f32_512_nn": ("f32", 2.0 * 512 ** 3, gemm(512, 512, 512, "f32", False, False)),
         "fa_fwd_b4h32s4096d128": ("bf16", fa, attn(False)),
         "fa_fwd_b4h32s4096d128_causal": ("bf16", fa / 2, attn(True)),
         # K stored [B, H, D, S]: the reference's FA tile program layout

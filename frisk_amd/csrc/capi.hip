@@ -197,7 +197,6 @@ int check_gemm(const frisk_gemm_desc* d, const char* fn, bool ptrs, frisk::GemmA
   // one (K - 1) pitches plus a tile row; beyond 2^31 - 1 bytes the generic
   // kernel (64-bit indexing) runs instead.
   const int ies = esize(d->a_type), oes = esize(d->c_type);
-  const bool mfma_type = d->a_type != FRISK_F32;
   const bool a_kmajor = !g.trans_a, b_kmajor = g.trans_b;
   const bool aligned = !ptrs || (aligned16(d->a) && aligned16(d->b) && aligned16(d->c));
   const bool k_pieces = (!a_kmajor && !b_kmajor) || (d->k * ies) % 16 == 0;
@@ -209,8 +208,9 @@ int check_gemm(const frisk_gemm_desc* d, const char* fn, bool ptrs, frisk::GemmA
   };
   const bool offsets_ok = reach(a_kmajor, d->lda) <= INT32_MAX && reach(b_kmajor, d->ldb) <= INT32_MAX;
   const bool nt = a_kmajor && b_kmajor;
-  if (mfma_type && nt && vec_ok && offsets_ok && frisk::gemm_skinny_supported(g)) route = GemmRoute::Skinny;
-  else if (mfma_type && vec_ok && offsets_ok) route = GemmRoute::Mfma;
+  // Every type pair, f32 included, has MFMA kernels.
+  if (nt && vec_ok && offsets_ok && frisk::gemm_skinny_supported(g)) route = GemmRoute::Skinny;
+  else if (vec_ok && offsets_ok) route = GemmRoute::Mfma;
   else route = GemmRoute::Generic;
 
   // A requested kernel variant: the named tile and wave grid, unsplit.
@@ -226,9 +226,9 @@ int check_gemm(const frisk_gemm_desc* d, const char* fn, bool ptrs, frisk::GemmA
                   "%s: no kernel variant tile=%d wave grid %dx%d (flags %d): 256 with 2x2, or 128 "
                   "with 2x2, 4x1, 1x4, 2x1 or 1x2",
                   fn, (int)d->tile, (int)d->wave_m, (int)d->wave_n, (int)d->variant_flags);
-    if (!(mfma_type && vec_ok && offsets_ok))
+    if (!(vec_ok && offsets_ok))
       return fail(FRISK_EUNSUP,
-                  "%s: the %dx%d-tile variant runs on the matrix cores only: bf16/f16/e4m3/int8, "
+                  "%s: the %dx%d-tile variant runs on the matrix cores only: "
                   "16-byte aligned operands and row pitches, whole 16-byte pieces of K in a "
                   "K-contiguous operand, operand reach below 2^31 bytes",
                   fn, (int)d->tile, (int)d->tile);
@@ -263,6 +263,7 @@ int atom_k_bytes(frisk::Elt in) {
     case frisk::Elt::F16: return 32;  // 32x32x16
     case frisk::Elt::E4M3: return 64;  // 32x32x64
     case frisk::Elt::I8: return 32;  // 32x32x32
+    case frisk::Elt::F32: return 32;  // four 32x32x2 per 8 k
     default: return 0;
   }
 }
@@ -273,6 +274,7 @@ const char* mfma_atom(frisk::Elt in) {
     case frisk::Elt::F16: return "v_mfma_f32_32x32x16_f16";
     case frisk::Elt::E4M3: return "v_mfma_scale_f32_32x32x64_f8f6f4";
     case frisk::Elt::I8: return "v_mfma_i32_32x32x32_i8";
+    case frisk::Elt::F32: return "v_mfma_f32_32x32x2_f32";
     default: return "";
   }
 }
@@ -322,7 +324,9 @@ int frisk_gemm_plan(const frisk_gemm_desc* d, char* buf, int64_t len) {
   const char* a_major = g.trans_a ? "m" : "k";
   const char* b_major = g.trans_b ? "k" : "n";
   auto lds_read = [&](bool mn) {
-    return !mn ? "ds_read_b128" : ies == 2 ? "ds_read_b64_tr_b16" : "ds_read_b64_tr_b8";
+    return !mn ? "ds_read_b128"
+           : ies == 4 ? "ds_read_b32"
+           : ies == 2 ? "ds_read_b64_tr_b16" : "ds_read_b64_tr_b8";
   };
   int n = 0;
   if (route == GemmRoute::Generic) {

@@ -127,15 +127,15 @@ double partial_cost(const GemmArgs& g, int64_t slices) {
 constexpr int64_t kRow = 64;
 
 SplitPlan gemm_split_plan(const GemmArgs& g, int cus) {
-  SplitPlan p{1, g.k * 2, 0, false};
-  // bf16 / f16 only (the partials carry no fp8 scale); the slice sum reads
-  // rows of 4 floats.
-  if ((g.in != Elt::BF16 && g.in != Elt::F16) || g.n % 4 != 0) return p;
+  const int64_t kb = g.k * elt_bytes(g.in);  // bytes of K per row
+  SplitPlan p{1, kb, 0, false};
+  // bf16 / f16 / f32 only (the partials carry no fp8 scale, and int8 sums
+  // stay exact in one pass); the slice sum reads rows of 4 floats.
+  if ((g.in != Elt::BF16 && g.in != Elt::F16 && g.in != Elt::F32) || g.n % 4 != 0) return p;
   // Grids of at least CUs / 2 256x256 tiles run unsplit on them.
   const int64_t tiles256 = ((g.m + 255) / 256) * ((g.n + 255) / 256);
   if (tiles256 >= cus / 2) return p;
   const int64_t tiles = ((g.m + 127) / 128) * ((g.n + 127) / 128);
-  const int64_t kb = g.k * 2;
   // 128x128 tiles.  Split only grids that leave CUs without a tile, each
   // slice at least 8 stages, and the f32 partials at most the bytes of A
   // and B (FRISK_SPLIT_CAP).  Grids of at
@@ -152,8 +152,15 @@ SplitPlan gemm_split_plan(const GemmArgs& g, int cus) {
     const bool deep = 2 * tiles <= cus;
     const int64_t row = deep ? 128 : kRow;  // bytes of K per stage
     int64_t slices = deep ? cus / tiles : (2 * (int64_t)cus + tiles - 1) / tiles;
-    slices = std::min<int64_t>(slices, kb / (8 * row));
-    slices = std::min<int64_t>(slices, (g.m + g.n) * kb / (FRISK_SPLIT_CAP * g.m * g.n));
+    if (g.in == Elt::F32) {
+      // fp32 runs the MFMA 16x slower per byte of operand than bf16: the
+      // K loop, not the partials' traffic, sets the time, so slices of 4
+      // stages and no cap on the partials (1024^3: 64 tiles in 4 slices).
+      slices = std::min<int64_t>(slices, kb / (4 * row));
+    } else {
+      slices = std::min<int64_t>(slices, kb / (8 * row));
+      slices = std::min<int64_t>(slices, (g.m + g.n) * kb / (FRISK_SPLIT_CAP * g.m * g.n));
+    }
     slices = std::min<int64_t>(slices, 64);
     if (slices >= 2) {
       const int64_t chunks = (kb + row - 1) / row;  // slices start on stage boundaries
@@ -172,7 +179,8 @@ SplitPlan gemm_split_plan(const GemmArgs& g, int cus) {
   // 1024 x 4096 x 4096 stays on 128x128 tiles (57.6 us split against 54.4)
   // and 256 x 4096 x 4096 on its 128x128 split (34.9 us on 256x256 tiles
   // against 33.2; estimated ratio 0.84).
-  if (g.m > kSkinnyMaxM && FRISK_W4_SPLIT) {
+  // (The rates are those of bf16 / f16; f32 keeps the 128x128 split.)
+  if (g.m > kSkinnyMaxM && FRISK_W4_SPLIT && g.in != Elt::F32) {
     const double flop128 = 2.0 * 128 * 128 * (double)(p.kb_slice / 2);
     const double t128 = rounds(tiles * p.slices, cus) * flop128 / kRate128 + partial_cost(g, p.slices);
     double best = 0.0;

@@ -342,6 +342,10 @@ static hipError_t launch_128_split_out(const GemmArgs& g, int slices, int64_t kb
                                        hipStream_t stream) {
   if (slices > kTreeMaxSlices)
     return launch_128_split_k<IN, Elt::F32, AM, BM, KROW, false>(g, slices, kb_slice, ws, stream);
+  if constexpr (IN == Elt::F32) {
+    if (g.out != Elt::F32) return hipErrorInvalidValue;
+    return launch_128_split_k<IN, Elt::F32, AM, BM, KROW, true>(g, slices, kb_slice, ws, stream);
+  }
   switch (g.out) {
     case Elt::BF16: return launch_128_split_k<IN, Elt::BF16, AM, BM, KROW, true>(g, slices, kb_slice, ws, stream);
     case Elt::F16: return launch_128_split_k<IN, Elt::F16, AM, BM, KROW, true>(g, slices, kb_slice, ws, stream);
@@ -364,6 +368,7 @@ hipError_t gemm_128_split_layout(const GemmArgs& g, int slices, int64_t kb_slice
                                  hipStream_t s) {
   if (g.in == Elt::BF16) return launch_128_split<Elt::BF16, AM, BM>(g, slices, kb_slice, ws, s);
   if (g.in == Elt::F16) return launch_128_split<Elt::F16, AM, BM>(g, slices, kb_slice, ws, s);
+  if (g.in == Elt::F32) return launch_128_split<Elt::F32, AM, BM>(g, slices, kb_slice, ws, s);
   return hipErrorInvalidValue;
 }
 
@@ -380,6 +385,7 @@ static hipError_t gemm_128_pairs(const GemmArgs& g, hipStream_t s) {
     case FRISK_PAIR(Elt::E4M3, Elt::F16): return launch_128<Elt::E4M3, Elt::F16, AM, BM, 2, 2, KROW>(g, s);
     case FRISK_PAIR(Elt::E4M3, Elt::F32): return launch_128<Elt::E4M3, Elt::F32, AM, BM, 2, 2, KROW>(g, s);
     case FRISK_PAIR(Elt::I8, Elt::I32): return launch_128<Elt::I8, Elt::I32, AM, BM, 2, 2, KROW>(g, s);
+    case FRISK_PAIR(Elt::F32, Elt::F32): return launch_128<Elt::F32, Elt::F32, AM, BM, 2, 2, KROW>(g, s);
     default: return hipErrorInvalidValue;
   }
 }
@@ -404,6 +410,7 @@ static hipError_t gemm_128_typed(const GemmArgs& g, hipStream_t s) {
     case FRISK_PAIR(Elt::E4M3, Elt::F16): return launch_128<Elt::E4M3, Elt::F16, AM, BM, WM, WN>(g, s);
     case FRISK_PAIR(Elt::E4M3, Elt::F32): return launch_128<Elt::E4M3, Elt::F32, AM, BM, WM, WN>(g, s);
     case FRISK_PAIR(Elt::I8, Elt::I32): return launch_128<Elt::I8, Elt::I32, AM, BM, WM, WN>(g, s);
+    case FRISK_PAIR(Elt::F32, Elt::F32): return launch_128<Elt::F32, Elt::F32, AM, BM, WM, WN>(g, s);
     default: return hipErrorInvalidValue;
   }
 }

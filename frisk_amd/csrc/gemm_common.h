@@ -53,6 +53,24 @@ template <> struct Mfma32<Elt::I8> {
   }
 };
 
+// fp32 on the matrix cores: v_mfma_f32_32x32x2_f32 takes one k per lane
+// half (lanes 0-31 k = 0, lanes 32-63 k = 1), so the 16 bytes (4 floats) a
+// lane holds per k-step feed four of them, float j of every lane in
+// instruction j.  A and B assign k alike, so the 8 k of a k-step pair up;
+// the products are exact and the sums fp32 (dense peak 157.3 TFLOP/s).
+template <> struct Mfma32<Elt::F32> {
+  static constexpr int kBytes = 32;
+  using Acc = f32x16;
+  __device__ static inline Acc run(const i32x4* a, const i32x4* b, Acc c) {
+    const f32x4 av = __builtin_bit_cast(f32x4, a[0]);
+    const f32x4 bv = __builtin_bit_cast(f32x4, b[0]);
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(av[0], bv[0], c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(av[1], bv[1], c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(av[2], bv[2], c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(av[3], bv[3], c, 0, 0, 0);
+  }
+};
+
 // The 16x16 atoms: kBytes = bytes of one operand row consumed by one MFMA;
 // every lane supplies kBytes/4 of them (four lane groups of 16 split the
 // row), so a lane's share is the same 16 B (32 B for fp8) as with 32x32.

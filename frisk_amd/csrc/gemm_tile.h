@@ -27,7 +27,9 @@
 //    addresses k-row k0 + e at columns c0 + 8b .. +7 and lane j receives 8
 //    consecutive k of column c0 + j; 2 (i8) or 4 (fp8) reads give 16 or 32.
 //    The k order equals the K-major ds_read_b128's, so A and B fragments
-//    agree whatever the storage order of either.
+//    agree whatever the storage order of either.  32-bit types have no
+//    transposing read: lane L reads its 4 consecutive k (k-rows 4 (L / 32)
+//    .. +3 of a step's 8) at column L % 32 with four ds_read_b32.
 //
 // LDS swizzles (16 B chunk c of tile row r is stored at chunk c ^ swz(r)).
 // A read is conflict-free when the lanes served together hit distinct banks
@@ -42,6 +44,10 @@
 //    swz(r) = (r & 7) << 1 gives each row its own 32 B pair of chunks.
 //  * MN-major 8-bit, 128 B rows: two rows share a window (r & 1 picks the
 //    half); swz(r) = ((r >> 1) & 3) << 1 separates the four pairs of rows.
+//  * MN-major 32-bit (rows of 512 or 1024 B): a ds_read_b32 has lanes 0-31
+//    on 128 contiguous bytes of k-row e and lanes 32-63 on k-row 4 + e;
+//    swz(r) = ((r >> 2) & 1) << 3 moves the second row 128 B over, onto the
+//    other 32 banks.
 // Every swizzle is an XOR of row bits into chunk bits, i.e. a GF(2)-linear
 // shared layout, and only reads row bits below 3, which k-row bases
 // (multiples of 8) never change.
@@ -66,10 +72,11 @@ struct OpTile {
   static constexpr int kStepChunks = Op::kBytes / 16;
   static constexpr int kLaneChunks = kStepChunks / kGroups;
   static constexpr int kLaneK = Op::kBytes / kGroups / kEsz;  // k per lane per MFMA
-  static constexpr int kReadsPerChunk = MN ? 2 : 1;  // LDS reads per 16 B of operand
+  static constexpr int kReadsPerChunk = MN ? (kEsz == 4 ? 4 : 2) : 1;  // LDS reads per 16 B
   static_assert(kRows * kRB == kBytes && kRowsPerBlock >= 1, "tile geometry");
   static_assert(!MN || kRB >= 128, "MN-major rows of at least 128 B");
   static_assert(ATOM == 32 || ATOM == 16, "MFMA atom");
+  static_assert(kEsz != 4 || ATOM == 32, "32-bit operands on 32x32 atoms");
   static_assert(KR % Op::kBytes == 0, "whole MFMA k-steps per stage");
 
   // For 16x16 atoms the 32 lanes served together by a transposing read
@@ -79,6 +86,8 @@ struct OpTile {
     if constexpr (!MN) {
       if constexpr (KR == 128) return (r & 7) ^ ((r >> 3) & 1);
       else return (r >> 2) & 3;  // KR == 64
+    } else if constexpr (kEsz == 4) {
+      return ((r >> 2) & 1) << 3;
     } else if constexpr (kEsz == 2) {
       if constexpr (ATOM == 32) return (r & 3) << 2;
       else return ((r & 3) | (((r >> 3) & 1) << 2)) << 1;
@@ -176,7 +185,12 @@ struct OpTile {
       // 16-lane group G of the wave covers columns r0 + 16 dg (dg < ATOM/16)
       // at this lane group's K share kg.
       const int G = lane >> 4, dg = G % (ATOM / 16), kg = G / (ATOM / 16);
-      if constexpr (kEsz == 2) {
+      if constexpr (kEsz == 4) {
+        // Lane L: k-rows 4 (L / 32) .. +3 at column r0 + L % 32 (one
+        // swizzle for the four rows: it reads row bit 2 only).
+        const int col = r0 + (lane & 31), row = kLaneK * (lane >> 5);
+        return Frag{row * kRB + (((col >> 2) ^ swz(row)) << 4) + 4 * (col & 3), 0};
+      } else if constexpr (kEsz == 2) {
         // Lane 16G + 4e + q: k-row kLaneK kg + e, columns r0 + 16 dg + 4q.
         const int e = (lane >> 2) & 3, q = lane & 3;
         const int row = kLaneK * kg + e;
@@ -201,6 +215,11 @@ struct OpTile {
         const int chunk = s * kStepChunks + j;
         out[j] = *(const i32x4*)(base + off + f.off + ((chunk ^ f.sw) << 4));
       }
+    } else if constexpr (kEsz == 4) {
+      static_assert(kLaneChunks == 1, "32-bit operand: 4 k per lane");
+      const char* p = base + f.off + s * (Op::kBytes / 4) * kRB;
+      out[0] = i32x4{*(const int*)p, *(const int*)(p + kRB), *(const int*)(p + 2 * kRB),
+                     *(const int*)(p + 3 * kRB)};
     } else if constexpr (kEsz == 2) {
       static_assert(kLaneChunks == 1, "16-bit operand: 8 k per lane");
       const char* p = base + f.off + s * (Op::kBytes / 2) * kRB;

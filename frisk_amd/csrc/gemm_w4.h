@@ -459,6 +459,7 @@ hipError_t gemm_w4_layout(const GemmArgs& g, hipStream_t s) {
     case FRISK_PAIR(Elt::E4M3, Elt::F16): return launch_w4<Elt::E4M3, Elt::F16, AM, BM>(g, s);
     case FRISK_PAIR(Elt::E4M3, Elt::F32): return launch_w4<Elt::E4M3, Elt::F32, AM, BM>(g, s);
     case FRISK_PAIR(Elt::I8, Elt::I32): return launch_w4<Elt::I8, Elt::I32, AM, BM>(g, s);
+    case FRISK_PAIR(Elt::F32, Elt::F32): return launch_w4<Elt::F32, Elt::F32, AM, BM>(g, s);
     default: return hipErrorInvalidValue;
   }
 }

@@ -311,10 +311,14 @@ class Normalizer {
       const bool intPath = ae.isSignlessInteger(8);
       if (intPath ? !ce.isSignlessInteger(32) : !ce.isF32())
         error(op, "legacy-gemm-accumulator: f32 required; implicit promotion is forbidden");
-      const bool inOk = ae.isF16() || ae.isBF16() || ae.isFloat(FloatKind::E4M3FN) ||
-                        ae.isFloat(FloatKind::E5M2) || intPath;
+      // The reference's SM90 path takes f16/bf16 (LegacyFragmentNormalization
+      // .cpp:478-494); gfx950 has MFMA atoms for fp8, i8 and f32 as well
+      // (v_mfma_f32_32x32x2_f32 for an f32 product such as the reference's
+      // own GEMM tile program, tmp/ir.mlir:2-16).
+      const bool inOk = ae.isF16() || ae.isBF16() || ae.isF32() ||
+                        ae.isFloat(FloatKind::E4M3FN) || ae.isFloat(FloatKind::E5M2) || intPath;
       if (!inOk || ae != bT.elementType())
-        error(op, "legacy-gemm-input: matching f16/bf16/fp8/i8 A/B required");
+        error(op, "legacy-gemm-input: matching f16/bf16/f32/fp8/i8 A/B required");
       if (auto err = legacyGemmValidationError(aT, bT, cT, op->boolAttr("transA"),
                                                op->boolAttr("transB"), op->intAttr("M"),
                                                op->intAttr("N"), op->intAttr("K")))

@@ -34,7 +34,7 @@ _CONTRACT = re.compile(
 # The 32x32 MFMA atom of each input type (the solver's name; the fp8 kernel
 # issues its block-scaled form with unit scales).
 ATOMS_32 = {"v_mfma_f32_32x32x16_bf16", "v_mfma_f32_32x32x16_f16", "v_mfma_f32_32x32x64_f8f6f4",
-            "v_mfma_i32_32x32x32_i8"}
+            "v_mfma_i32_32x32x32_i8", "v_mfma_f32_32x32x2_f32"}
 
 GRIDS_128 = ((2, 2), (4, 1), (1, 4), (2, 1), (1, 2))
 

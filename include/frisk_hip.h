@@ -122,12 +122,12 @@ typedef struct frisk_gemm_desc {
 
 int frisk_gemm(const frisk_gemm_desc* desc, void* stream);
 
-/* Every storage order of A and B runs on the matrix cores (bf16/f16/fp8/i8)
- * when the operands have 16-byte aligned bases and row pitches, K * esize is
- * a multiple of 16 for an operand stored K-contiguous (A without trans_a, B
- * with trans_b), C's row pitch is a multiple of 16 bytes, and every buffer a
- * tile addresses spans less than 2^31 bytes; anything else (and f32) runs a
- * correct but slower generic kernel. */
+/* Every storage order of A and B runs on the matrix cores (f32/bf16/f16/fp8/
+ * i8; f32 on v_mfma_f32_32x32x2_f32) when the operands have 16-byte aligned
+ * bases and row pitches, K * esize is a multiple of 16 for an operand stored
+ * K-contiguous (A without trans_a, B with trans_b), C's row pitch is a
+ * multiple of 16 bytes, and every buffer a tile addresses spans less than
+ * 2^31 bytes; anything else runs a correct but slower generic kernel. */
 
 /* frisk_gemm without any device allocation by the library or the caller:
  * no hipMalloc, hipFree or allocating library routine is called.  No

@@ -355,10 +355,17 @@ def test_gemm_plan_every_layout_runs_on_the_matrix_cores():
 
 
 def test_gemm_plan_generic_cases():
-    # f32, 16 B misalignment of a pitch, a K-contiguous operand without whole
+    # A 16 B misalignment of a pitch, a K-contiguous operand without whole
     # 16 B pieces of K, and a pitch whose tile reaches past 2^31 bytes run the
     # generic kernel.
-    assert plan(a_type=rt.F32, b_type=rt.F32, c_type=rt.F32)["kernel"] == "gemm_generic"
+    # f32 runs on the matrix cores (v_mfma_f32_32x32x2_f32); an N-major f32
+    # B is read with four ds_read_b32 (there is no 32-bit transposing read).
+    p = plan(a_type=rt.F32, b_type=rt.F32, c_type=rt.F32)
+    assert p["kernel"] == "gemm_w4" and p["atom"] == "v_mfma_f32_32x32x2_f32", p
+    p = plan(m=512, n=512, k=512, lda=512, ldb=512, ldc=512, trans_b=0, a_type=rt.F32,
+             b_type=rt.F32, c_type=rt.F32)
+    assert p["kernel"] == "gemm_128" and p["lds_read_b"] == "ds_read_b32", p
+    assert plan(a_type=rt.F32, b_type=rt.F32, c_type=rt.F32, lda=4098)["kernel"] == "gemm_generic"
     assert plan(lda=4100)["kernel"] == "gemm_generic"
     assert plan(k=4092, lda=4096, ldb=4096)["kernel"] == "gemm_generic"
     # ...but an M/N-major operand takes any K (its K tail is per k-row).
@@ -404,7 +411,7 @@ def test_gemm_variant_requests():
         with pytest.raises(ValueError, match="no kernel variant"):
             plan(**bad)
     # Valid variant, but the request is not matrix-core work.
-    for bad in (dict(a_type=rt.F32, b_type=rt.F32, c_type=rt.F32), dict(lda=4100)):
+    for bad in (dict(a_type=rt.F32, b_type=rt.F32, c_type=rt.F32, lda=4098), dict(lda=4100)):
         with pytest.raises(ValueError, match="runs on the matrix cores only"):
             plan(tile=128, **bad)
     rc, msg = gemm_call(tile=256, lda=4100)

@@ -113,3 +113,25 @@ def test_execute_config_c1_fp32_512():
     got = c.cpu().numpy().astype(np.float64)
     assert G.row_scaled_error(got, G.gemm_fp64(a_np, b_np)) <= 1e-5
     assert G.row_scaled_error(got, G.gemm_fp32_rank1(a_np, b_np)) <= 1e-5
+
+
+def test_execute_reference_fp32_tile_program():
+    # The reference's GEMM tile program (tmp/ir.mlir:2-16): fp32 C = A.B at
+    # 1024^3 in 128x128x32 workgroup tiles on 256 threads.  Its instruction
+    # contract selects the 128x128 kernel with a 2x2 wave grid on
+    # v_mfma_f32_32x32x2_f32, which execute() runs; fp32 parity against
+    # the fp64 oracle.
+    from frisk_amd import executor
+    s, _ = P.tiled_gemm(1024, 1024, 1024, BM=128, BN=128, BK=32, dtype="fp32", out="fp32")
+    p = executor.plan(s.module, "matmul")
+    assert p.variant == (128, 2, 2) and p.layouts_match, (p.contract, p.mismatch)
+    assert "v_mfma_f32_32x32x2_f32" in p.contract
+    rng = np.random.default_rng(1)
+    a_np = rng.uniform(-1, 1, (1024, 1024)).astype(np.float32)
+    b_np = rng.uniform(-1, 1, (1024, 1024)).astype(np.float32)
+    a, b = torch.from_numpy(a_np).cuda(), torch.from_numpy(b_np).cuda()
+    c = torch.full((1024, 1024), float("nan"), device="cuda")
+    F.execute(s.module, "matmul", [a, b, c])
+    torch.cuda.synchronize()
+    ref = G.gemm_fp64(a_np, b_np)
+    assert G.row_scaled_error(c.cpu().numpy().astype(np.float64), ref) <= 1e-5

@@ -324,6 +324,32 @@ def test_split_k_every_slice_count(slices, ta, tb):
         check(decode(c), ref, torch.bfloat16, out_dt)
 
 
+@pytest.mark.parametrize("m,n,k", [(512, 512, 512), (1024, 1024, 1024), (300, 500, 1032)])
+@pytest.mark.parametrize("ta,tb", list(itertools.product([False, True], repeat=2)))
+def test_fp32_matrix_cores_split_k(m, n, k, ta, tb):
+    # fp32 on v_mfma_f32_32x32x2_f32, split over K (4 slices summed by a
+    # second launch) in every storage order, accumulating into C: against
+    # the fp64 oracle at 1e-5, bit-identical on a repeat, and the unsplit
+    # kernel within the same tolerance.
+    print(f"case f32 split m={m} n={n} k={k} ta={ta} tb={tb}", flush=True)
+    if ta and m % 4:
+        m += 4 - m % 4  # 16 B row pitch of an M-major A
+    a, b, _, _ = make_operands(m, n, k, torch.float32, ta, tb, seed=70 + m)
+    c0 = randn((m, n), 71)
+    p = rt.gemm_plan(a, b, c0, trans_a=ta, trans_b=tb)
+    assert p["atom"] == "v_mfma_f32_32x32x2_f32" and p["slices"] > 1, p
+    outs = []
+    for ws in (True, True, False):
+        c = c0.clone()
+        rt.gemm(a, b, c, trans_a=ta, trans_b=tb, clear_accum=False, workspace=ws)
+        torch.cuda.synchronize()
+        outs.append(c)
+    assert torch.equal(outs[0], outs[1])
+    ref = reference(a, b, ta, tb, 1.0, 1.0) + decode(c0)
+    for c in (outs[0], outs[2]):
+        assert G.row_scaled_error(decode(c), ref) <= 1e-5
+
+
 def test_config_c1_fp32_512():
     # fp32 C = A.B, row-major A and B, U[-1, 1].
     rng = np.random.default_rng(0)
