@@ -579,43 +579,21 @@ static hipError_t launch_attn_nw(const AttnArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-// Workgroup shape per launch (measured on MI355X).  Every query's arithmetic
-// is the same in both shapes (same key blocks in the same order; a masked
-// block with no hidden key computes what an unmasked one does), so the
-// choice never changes a result bit.  8 waves x 32 queries (one K/V tile
-// feeds 256 queries) unless 4 waves finish sooner.  A CU runs one 8-wave
-// workgroup or two 4-wave ones at a time (two waves per SIMD), so in units
-// of one 8-wave workgroup's run: 8 waves take ceil(w8 / CUs); 4 waves take
-// one unit per 2 CUs workgroups, and a last round of at most one workgroup
-// per CU about 0.6 (one wave per SIMD runs each wave faster).  Measured
-// non-causal: b4 h32 s4096 d128 1030 vs 1012 TFLOP/s (8 kept); b8 h8 s1024
-// d64 657 vs 635 (8 kept); b2 h32 s1025 d64 366 vs 475 and b1 h16 s2048
-// d128 618 vs 839 (4 chosen).  Causal b4 h32 s4096 d128 (workgroups of
-// paired query blocks): 979-989 vs 944 (8 kept).  Below head_dim 128 the
-// kernel takes about 150 VGPRs, three waves per SIMD, so 4-wave workgroups
-// share a CU three at a time and the rule above undercounts them: measured
-// (us, 4 vs 8 waves) b2 h32 s1025 d64 33.9 vs 45.8 (causal 34.2 vs 37.6),
-// b4 h32 s4096 d64 617 vs 630 (causal 336 vs 348), b8 h8 s1024 d64 causal
-// 22.6 vs 33.4, ties elsewhere; only s256 causal favoured 8 (11.6 vs 12.8).
-// Head_dim 64 and below always take 4 waves.
+// Workgroup shape per launch: a.waves when the request names one, else
+// plan::attn_waves (launch_plan.h, which holds the measurements behind the
+// rule).  Head_dim 64 and below run 4-wave workgroups only.  Every query's
+// arithmetic is the same in both shapes (same key blocks in the same order;
+// a masked block with no hidden key computes what an unmasked one does), so
+// the choice never changes a result bit.
 template <Elt T, Elt OUT, int D, bool CAUSAL, bool KT>
 static hipError_t launch_attn_kt(const AttnArgs& a, hipStream_t stream) {
   if constexpr (D <= 64) {
     return launch_attn_nw<T, OUT, D, 4, CAUSAL, KT>(a, stream);
   } else {
-    // Workgroups of bm queries (under a causal mask, pairs of query blocks).
-    const int64_t bh = a.batch * a.heads;
-    auto workgroups = [&](int64_t bm) {
-      const int64_t q = (a.seq_q + bm - 1) / bm;
-      return bh * (CAUSAL ? (q + 1) / 2 : q);
-    };
-    const int64_t cus = device_cus();
-    const int64_t w8 = workgroups(256), w4 = workgroups(128);
-    const double t8 = (double)((w8 + cus - 1) / cus);
-    const int64_t rest4 = w4 % (2 * cus);
-    const double t4 = (double)(w4 / (2 * cus)) + (rest4 == 0 ? 0.0 : rest4 <= cus ? 0.6 : 1.0);
-    return t4 < t8 ? launch_attn_nw<T, OUT, D, 4, CAUSAL, KT>(a, stream)
-                   : launch_attn_nw<T, OUT, D, 8, CAUSAL, KT>(a, stream);
+    const int waves = a.waves ? a.waves
+                              : plan::attn_waves(a.batch * a.heads, a.seq_q, D, CAUSAL, device_cus());
+    return waves == 4 ? launch_attn_nw<T, OUT, D, 4, CAUSAL, KT>(a, stream)
+                      : launch_attn_nw<T, OUT, D, 8, CAUSAL, KT>(a, stream);
   }
 }
 

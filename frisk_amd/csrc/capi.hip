@@ -138,16 +138,17 @@ int frisk_abi_version(void) { return FRISK_ABI_VERSION; }
 
 namespace {
 
-// Which kernel family a GEMM descriptor goes to.
-enum class GemmRoute { Skinny, Mfma, Generic };
+// Which kernel family a GEMM descriptor goes to (launch_plan.h).
+using GemmRoute = frisk::plan::Route;
 
 // Rows of the largest operand tile a GEMM kernel addresses from one buffer
 // base (the 256x256 tiles).
 constexpr int64_t kMaxTileRows = 256;
 
-// Checks of frisk_gemm / frisk_gemm_workspace_size, the kernel arguments
-// and the route; 0 or an error code.  With ptrs == false the operand
-// pointers are neither required nor read (alignment is assumed).
+// Checks of frisk_gemm / frisk_gemm_workspace_size / frisk_gemm_plan, the
+// kernel arguments and the route; 0 or an error code.  With ptrs == false
+// the operand pointers are not required; when all three are given their
+// alignment still counts (they are never read).
 int check_gemm(const frisk_gemm_desc* d, const char* fn, bool ptrs, frisk::GemmArgs& g,
                GemmRoute& route) {
   if (!d) return fail(FRISK_EINVAL, "%s: null descriptor", fn);
@@ -198,7 +199,10 @@ int check_gemm(const frisk_gemm_desc* d, const char* fn, bool ptrs, frisk::GemmA
   // kernel (64-bit indexing) runs instead.
   const int ies = esize(d->a_type), oes = esize(d->c_type);
   const bool a_kmajor = !g.trans_a, b_kmajor = g.trans_b;
-  const bool aligned = !ptrs || (aligned16(d->a) && aligned16(d->b) && aligned16(d->c));
+  // Pointers are never dereferenced here; when a query (ptrs == false)
+  // passes them anyway, their alignment takes part as in the call.
+  const bool have_ptrs = d->a && d->b && d->c;
+  const bool aligned = !(ptrs || have_ptrs) || (aligned16(d->a) && aligned16(d->b) && aligned16(d->c));
   const bool k_pieces = (!a_kmajor && !b_kmajor) || (d->k * ies) % 16 == 0;
   const bool vec_ok = aligned && k_pieces && (d->lda * ies) % 16 == 0 &&
                       (d->ldb * ies) % 16 == 0 && (d->ldc * oes) % 16 == 0;
@@ -207,13 +211,14 @@ int check_gemm(const frisk_gemm_desc* d, const char* fn, bool ptrs, frisk::GemmA
                   : (d->k - 1) * ld * ies + kMaxTileRows * ies;
   };
   const bool offsets_ok = reach(a_kmajor, d->lda) <= INT32_MAX && reach(b_kmajor, d->ldb) <= INT32_MAX;
-  const bool nt = a_kmajor && b_kmajor;
-  // Every type pair, f32 included, has MFMA kernels.
-  if (nt && vec_ok && offsets_ok && frisk::gemm_skinny_supported(g)) route = GemmRoute::Skinny;
-  else if (vec_ok && offsets_ok) route = GemmRoute::Mfma;
-  else route = GemmRoute::Generic;
+  const bool matrix_cores = vec_ok && offsets_ok;  // every type pair, f32 included, has MFMA kernels
 
-  // A requested kernel variant: the named tile and wave grid, unsplit.
+  // A requested kernel variant: the named tile and wave grid, unsplit or in
+  // the K slices the request names.
+  if (d->slices < 0 || d->slices > 64)
+    return fail(FRISK_EINVAL, "%s: slices %d outside 0..64", fn, (int)d->slices);
+  if (d->slices > 1 && !d->tile)
+    return fail(FRISK_EINVAL, "%s: slices name a split of a requested variant (set tile)", fn);
   if (d->tile || d->wave_m || d->wave_n || d->variant_flags) {
     const int wm = d->wave_m ? d->wave_m : 2, wn = d->wave_n ? d->wave_n : 2;
     const bool grid_pair = (d->wave_m == 0) == (d->wave_n == 0);
@@ -226,34 +231,33 @@ int check_gemm(const frisk_gemm_desc* d, const char* fn, bool ptrs, frisk::GemmA
                   "%s: no kernel variant tile=%d wave grid %dx%d (flags %d): 256 with 2x2, or 128 "
                   "with 2x2, 4x1, 1x4, 2x1 or 1x2",
                   fn, (int)d->tile, (int)d->wave_m, (int)d->wave_n, (int)d->variant_flags);
-    if (!(vec_ok && offsets_ok))
+    if (!matrix_cores)
       return fail(FRISK_EUNSUP,
                   "%s: the %dx%d-tile variant runs on the matrix cores only: "
                   "16-byte aligned operands and row pitches, whole 16-byte pieces of K in a "
                   "K-contiguous operand, operand reach below 2^31 bytes",
                   fn, (int)d->tile, (int)d->tile);
-    route = GemmRoute::Mfma;
+    if (d->slices > 1 && !(wm == 2 && wn == 2 &&
+                           (d->a_type == FRISK_BF16 || d->a_type == FRISK_F16 ||
+                            d->a_type == FRISK_F32) && d->n % 4 == 0))
+      return fail(FRISK_EUNSUP,
+                  "%s: a split variant needs the 2x2 wave grid, bf16/f16/f32 inputs and N %% 4 "
+                  "== 0 (got %dx%d, %s, N %lld)",
+                  fn, wm, wn, dtype_name(d->a_type), (long long)d->n);
     g.tile = d->tile;
     g.wave_m = wm;
     g.wave_n = wn;
+    g.slices = d->slices;
   }
+  route = frisk::plan::route_of(frisk::shape_of(g), matrix_cores);
   return 0;
 }
 
-// Small-M rows this many or fewer stay on the skinny kernel when split;
-// more (up to its limit) run split on 128x128 tiles, which share each X
-// tile across the workgroup's waves through LDS.
-constexpr int64_t kSkinnySplitMaxM = 64;
+using frisk::plan::kSkinnySplitMaxM;
 
 // Workspace bytes of the split-K plan frisk_gemm follows (0: none).
 int64_t gemm_workspace(const frisk::GemmArgs& g, GemmRoute route) {
-  const int cus = frisk::device_cus();
-  if (route == GemmRoute::Skinny) {
-    if (g.m > kSkinnySplitMaxM) return frisk::gemm_split_plan(g, cus).workspace_bytes;
-    return frisk::gemm_skinny_plan(g, cus, true).workspace_bytes;
-  }
-  if (route == GemmRoute::Mfma) return g.tile ? 0 : frisk::gemm_split_plan(g, cus).workspace_bytes;
-  return 0;
+  return frisk::plan::workspace_bytes(frisk::shape_of(g), route, frisk::device_cus());
 }
 
 // K bytes per lane row of one MFMA atom (the atom's k times the element size).
@@ -317,9 +321,8 @@ int frisk_gemm_plan(const frisk_gemm_desc* d, char* buf, int64_t len) {
   const int rc = check_gemm(d, "frisk_gemm_plan", false, g, route);
   if (rc) return rc;
   if (!buf || len <= 0) return fail(FRISK_EINVAL, "frisk_gemm_plan: no output buffer");
-  const int cus = frisk::device_cus();
-  const int64_t need = gemm_workspace(g, route);
-  const bool ws = need > 0 && d->workspace_bytes >= need;
+  const frisk::plan::GemmLaunch L =
+      frisk::plan::launch_of(frisk::shape_of(g), route, frisk::device_cus(), d->workspace_bytes);
   const int ies = esize(d->a_type);
   const char* a_major = g.trans_a ? "m" : "k";
   const char* b_major = g.trans_b ? "k" : "n";
@@ -328,32 +331,27 @@ int frisk_gemm_plan(const frisk_gemm_desc* d, char* buf, int64_t len) {
            : ies == 4 ? "ds_read_b32"
            : ies == 2 ? "ds_read_b64_tr_b16" : "ds_read_b64_tr_b8";
   };
+  const char* slice_sum = L.slice_sum == frisk::plan::SliceSum::InLaunch ? "in_launch"
+                          : L.slice_sum == frisk::plan::SliceSum::SecondLaunch ? "second_launch"
+                                                                              : "none";
   int n = 0;
-  if (route == GemmRoute::Generic) {
+  if (L.kernel == frisk::plan::Kernel::Generic) {
     n = snprintf(buf, (size_t)len,
                  "{\"kernel\": \"gemm_generic\", \"tile_m\": 64, \"tile_n\": 64, \"atom\": \"fma\", "
                  "\"a_major\": \"%s\", \"b_major\": \"%s\", \"slices\": 1, \"slice_sum\": \"none\", "
                  "\"workspace_bytes\": 0}",
                  a_major, b_major);
-  } else if (route == GemmRoute::Skinny && !(ws && g.m > kSkinnySplitMaxM)) {
-    const frisk::SkinnyPlan p = frisk::gemm_skinny_plan(g, cus, ws);
+  } else if (L.kernel == frisk::plan::Kernel::Skinny) {
     n = snprintf(buf, (size_t)len,
                  "{\"kernel\": \"gemm_skinny\", \"tile_m\": %d, \"tile_n\": %d, "
                  "\"atom\": \"v_mfma_f32_16x16x32_%s\", \"waves\": [1, 1], \"a_major\": \"k\", "
                  "\"b_major\": \"k\", \"slices\": %d, \"slice_sum\": \"%s\", "
                  "\"workspace_bytes\": %lld}",
-                 16 * p.tm, 16 * p.tn, d->a_type == FRISK_BF16 ? "bf16" : "f16", p.slices,
-                 p.slices > 1 ? "second_launch" : "none",
-                 (long long)(p.slices > 1 ? p.workspace_bytes : 0));
+                 L.tile_m, L.tile_n, d->a_type == FRISK_BF16 ? "bf16" : "f16", L.slices, slice_sum,
+                 (long long)L.workspace_bytes);
   } else {
-    const frisk::MfmaChoice c = frisk::gemm_mfma_choice(g, cus, ws);
-    const int tile = c.big ? 256 : 128;
-    const int wm = c.big || !g.tile ? 2 : g.wave_m, wn = c.big || !g.tile ? 2 : g.wave_n;
-    const int64_t tiles128 = ((g.m + 127) / 128) * ((g.n + 127) / 128);
-    const int stage = c.big ? 128
-                      : g.tile ? 64
-                      : c.slices > 1 ? (tiles128 * c.slices <= cus && c.kb_slice % 128 == 0 ? 128 : 64)
-                                     : frisk::gemm_128_stage_bytes(g, cus);
+    const bool big = L.kernel == frisk::plan::Kernel::W4;
+    const int tile = L.tile_m, wm = L.wave_m, wn = L.wave_n;
     // The workgroup tile's instruction contract in the solver's syntax
     // (#frisk.mma_contract): the 256x256 kernel feeds the B fragment as the
     // MFMA's first operand (swapped), the 128x128 kernel does not.
@@ -362,18 +360,17 @@ int frisk_gemm_plan(const frisk_gemm_desc* d, char* buf, int64_t len) {
                  "{\"kernel\": \"%s\", \"tile_m\": %d, \"tile_n\": %d, \"atom\": \"%s\", "
                  "\"waves\": [%d, %d], \"wave_tile\": [%d, %d], \"stage_bytes\": %d, "
                  "\"a_major\": \"%s\", \"b_major\": \"%s\", \"lds_read_a\": \"%s\", "
-                 "\"lds_read_b\": \"%s\", \"slices\": %d, \"slice_sum\": \"%s\", "
-                 "\"workspace_bytes\": %lld, "
+                 "\"lds_read_b\": \"%s\", \"lds_swizzle_a\": \"%s\", \"lds_swizzle_b\": \"%s\", "
+                 "\"slices\": %d, \"slice_sum\": \"%s\", \"workspace_bytes\": %lld, "
                  "\"requested\": %s, \"mma_contract\": \"{atom = \\\"%s\\\", wave_grid = [%d, %d], "
                  "repeats = [%d, %d, %d], policy = \\\"%s\\\", swapped = %s}\"}",
-                 c.big ? "gemm_w4" : "gemm_128", tile, tile, mfma_atom(g.in), wm, wn, tile / wm,
-                 tile / wn, stage, a_major, b_major, lds_read(g.trans_a), lds_read(!g.trans_b),
-                 c.slices,
-                 c.slices <= 1 ? "none"
-                 : !c.big && c.slices <= frisk::kTreeMaxSlices ? "in_launch" : "second_launch",
-                 (long long)(c.slices > 1 ? need : 0), g.tile ? "true" : "false",
+                 big ? "gemm_w4" : "gemm_128", tile, tile, mfma_atom(g.in), wm, wn, tile / wm,
+                 tile / wn, L.stage_bytes, a_major, b_major, lds_read(g.trans_a), lds_read(!g.trans_b),
+                 frisk::plan::lds_swizzle(g.trans_a, ies, L.stage_bytes, tile * ies),
+                 frisk::plan::lds_swizzle(!g.trans_b, ies, L.stage_bytes, tile * ies), L.slices,
+                 slice_sum, (long long)L.workspace_bytes, L.requested ? "true" : "false",
                  mfma_atom(g.in), wm, wn, tile / wm / 32, tile / wn / 32,
-                 stage / atom_k_bytes(g.in), policy, c.big ? "true" : "false");
+                 L.stage_bytes / atom_k_bytes(g.in), policy, big ? "true" : "false");
   }
   if (n < 0 || n >= len)
     return fail(FRISK_EINVAL, "frisk_gemm_plan: buffer of %lld bytes is too small", (long long)len);
@@ -442,6 +439,11 @@ int frisk_attn_fwd(const frisk_attn_desc* d, void* stream) {
   // granularity (a buffer range check zeroes each dword that extends past
   // the end), so with an odd seq_k the last key of the last head_dim row
   // would share a zeroed dword with the element after it.
+  if (d->waves != 0 && d->waves != 4 && d->waves != 8)
+    return fail(FRISK_EINVAL, "frisk_attn_fwd: waves must be 0, 4 or 8 (got %d)", (int)d->waves);
+  if (d->waves == 8 && d->head_dim != 128)
+    return fail(FRISK_EUNSUP, "frisk_attn_fwd: 8-wave workgroups run head_dim 128 only (got %lld)",
+                (long long)d->head_dim);
   if (kt && d->seq_k % 2 != 0)
     return fail(FRISK_EUNSUP, "frisk_attn_fwd: transposed K needs an even seq_k (got %lld)",
                 (long long)d->seq_k);
@@ -470,6 +472,7 @@ int frisk_attn_fwd(const frisk_attn_desc* d, void* stream) {
   a.q = d->q; a.q_sb = d->q_stride_b; a.q_sh = d->q_stride_h; a.q_ss = d->q_stride_s;
   a.k = d->k; a.k_sb = d->k_stride_b; a.k_sh = d->k_stride_h; a.k_ss = d->k_stride_s;
   a.k_dmajor = kt ? 1 : 0;
+  a.waves = d->waves;
   a.v = d->v; a.v_sb = d->v_stride_b; a.v_sh = d->v_stride_h; a.v_ss = d->v_stride_s;
   a.o = d->o; a.o_sb = d->o_stride_b; a.o_sh = d->o_stride_h; a.o_ss = d->o_stride_s;
   a.lse = d->lse;

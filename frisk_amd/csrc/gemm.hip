@@ -1,7 +1,7 @@
-// GEMM dispatch for gfx950 (MI355X): the generic fallback kernel, the
-// split-K planner and the choice between the LDS-staged MFMA kernels
-// (gemm_w4.h: 256x256 tiles; gemm_128.h: 128x128 tiles), both of which take
-// every storage order of A and B.
+// GEMM dispatch for gfx950 (MI355X): the generic fallback kernel and the
+// launch of the LDS-staged MFMA kernels (gemm_w4.h: 256x256 tiles;
+// gemm_128.h: 128x128 tiles), both of which take every storage order of A
+// and B, as the launch planner (launch_plan.h) decides.
 //
 // Semantics follow frisk.gemm (include/Dialect/Frisk/IR/FriskOps.td:252-292):
 // C = op(A).op(B) when clear_accum, else C += op(A).op(B).
@@ -98,129 +98,6 @@ static hipError_t launch_generic(const GemmArgs& g, hipStream_t stream) {
 
 #define FRISK_PAIR(i, o) (((int)(i) << 8) | (int)(o))
 
-// Time estimates (seconds) of the split choices, from rates measured on
-// MI355X with operands streaming from HBM: a 128x128-tile workgroup
-// computes about 2.5 TFLOP/s on its CU, a 256x256-tile one about 4.7; the
-// f32 partials are written and read back at about 3.5 TB/s plus one launch.
-namespace {
-constexpr double kRate128 = 2.5e12, kRate256 = 4.7e12, kPartialBw = 3.5e12, kLaunch = 3e-6;
-double rounds(int64_t wgs, int64_t slots) { return (double)((wgs + slots - 1) / slots); }
-double partial_cost(const GemmArgs& g, int64_t slices) {
-  return slices > 1 ? ((double)slices * g.m * g.n * 4 + (double)g.m * g.n * 2) / kPartialBw + kLaunch
-                    : 0.0;
-}
-}  // namespace
-
-// The f32 partials of a split (slices x M x N x 4 bytes) stay within
-// 2 x (M + N) x K x 2 / FRISK_SPLIT_CAP bytes: the bytes of A and B.
-// Measured with operands from HBM, us, a quarter of A + B (16) -> all of it
-// (4): 256x4096x4096 27.4 -> 23.1 (2 -> 4 slices), 512x4096x4096 41.8 ->
-// 28.5 (8 slices of 256x256 tiles -> 2 of 128x128); 128x4096x4096 19.3
-// either way (4 -> 8 slices).
-#ifndef FRISK_W4_SPLIT
-#define FRISK_W4_SPLIT 1
-#endif
-#ifndef FRISK_SPLIT_CAP
-#define FRISK_SPLIT_CAP 4
-#endif
-// Bytes of K per pipeline stage of the 128x128-tile kernel (gemm_128.h).
-constexpr int64_t kRow = 64;
-
-SplitPlan gemm_split_plan(const GemmArgs& g, int cus) {
-  const int64_t kb = g.k * elt_bytes(g.in);  // bytes of K per row
-  SplitPlan p{1, kb, 0, false};
-  // bf16 / f16 / f32 only (the partials carry no fp8 scale, and int8 sums
-  // stay exact in one pass); the slice sum reads rows of 4 floats.
-  if ((g.in != Elt::BF16 && g.in != Elt::F16 && g.in != Elt::F32) || g.n % 4 != 0) return p;
-  // Grids of at least CUs / 2 256x256 tiles run unsplit on them.
-  const int64_t tiles256 = ((g.m + 255) / 256) * ((g.n + 255) / 256);
-  if (tiles256 >= cus / 2) return p;
-  const int64_t tiles = ((g.m + 127) / 128) * ((g.n + 127) / 128);
-  // 128x128 tiles.  Split only grids that leave CUs without a tile, each
-  // slice at least 8 stages, and the f32 partials at most the bytes of A
-  // and B (FRISK_SPLIT_CAP).  Grids of at
-  // most half as many tiles as CUs take slices up to one workgroup per CU,
-  // on 128-byte stages (the launch picks them when slices fit one
-  // workgroup per CU); larger grids take slices up to two workgroups per
-  // CU on 64-byte stages.  Measured on the projection sweep: M = 128 runs
-  // 1.6-4.8x faster than on the unsplit small-M kernel; with operands from
-  // HBM, 128 x 4096 x 14336 323 -> 416 TFLOP/s and 128 x 14336 x 4096
-  // 334 -> 373 on 128-byte stages (one workgroup per CU) against 64-byte
-  // ones (two); M = 1024, N = 4096 (256 tiles) runs 1.3x slower split in
-  // two.
-  if (tiles < cus) {
-    const bool deep = 2 * tiles <= cus;
-    const int64_t row = deep ? 128 : kRow;  // bytes of K per stage
-    int64_t slices = deep ? cus / tiles : (2 * (int64_t)cus + tiles - 1) / tiles;
-    if (g.in == Elt::F32) {
-      // fp32 runs the MFMA 16x slower per byte of operand than bf16: the
-      // K loop, not the partials' traffic, sets the time, so slices of 4
-      // stages and no cap on the partials (1024^3: 64 tiles in 4 slices).
-      slices = std::min<int64_t>(slices, kb / (4 * row));
-    } else {
-      slices = std::min<int64_t>(slices, kb / (8 * row));
-      slices = std::min<int64_t>(slices, (g.m + g.n) * kb / (FRISK_SPLIT_CAP * g.m * g.n));
-    }
-    slices = std::min<int64_t>(slices, 64);
-    if (slices >= 2) {
-      const int64_t chunks = (kb + row - 1) / row;  // slices start on stage boundaries
-      p.kb_slice = ((chunks + slices - 1) / slices) * row;
-      p.slices = (int)((kb + p.kb_slice - 1) / p.kb_slice);
-      if (p.slices < 2) p = SplitPlan{1, kb, 0, false};
-    }
-  }
-  // 256x256 tiles split over K, for M past the small-M range, when the
-  // estimate says they end sooner (by 20%) than the 128x128 choice above:
-  // a 256-tile workgroup does twice the work per CU cycle, the split buys
-  // back the parallelism, the partials cost their traffic.  Slices of at
-  // least 8 stages (8 x 128 B of K).  Measured, operands from HBM:
-  // 512 x 4096 x 4096 53.1 -> 44.1 us, 768 x 2048 x 4096 51.4 -> 38.1,
-  // 1024 x 4096 x 14336 179.5 -> 133.3 (estimated ratios 0.66-0.69);
-  // 1024 x 4096 x 4096 stays on 128x128 tiles (57.6 us split against 54.4)
-  // and 256 x 4096 x 4096 on its 128x128 split (34.9 us on 256x256 tiles
-  // against 33.2; estimated ratio 0.84).
-  // (The rates are those of bf16 / f16; f32 keeps the 128x128 split.)
-  if (g.m > kSkinnyMaxM && FRISK_W4_SPLIT && g.in != Elt::F32) {
-    const double flop128 = 2.0 * 128 * 128 * (double)(p.kb_slice / 2);
-    const double t128 = rounds(tiles * p.slices, cus) * flop128 / kRate128 + partial_cost(g, p.slices);
-    double best = 0.0;
-    int64_t best_s = 0;
-    for (int64_t sl = 2; sl <= 16 && kb / sl >= 1024; ++sl) {
-      const int64_t kb_slice = ((kb + 127) / 128 + sl - 1) / sl * 128;
-      const double t = rounds(tiles256 * sl, cus) * 2.0 * 256 * 256 * (double)(kb_slice / 2) / kRate256 +
-                       partial_cost(g, sl);
-      if (best_s == 0 || t < best) {
-        best = t;
-        best_s = sl;
-      }
-    }
-    if (best_s > 0 && best < 0.8 * t128) {
-      p.kb_slice = ((kb + 127) / 128 + best_s - 1) / best_s * 128;
-      p.slices = (int)((kb + p.kb_slice - 1) / p.kb_slice);
-      p.big = p.slices > 1;
-      if (!p.big) p = SplitPlan{1, kb, 0, false};
-    }
-  }
-  p.workspace_bytes = p.slices <= 1 ? 0
-                     : !p.big && p.slices <= kTreeMaxSlices ? split_tree_bytes(tiles, p.slices, 128)
-                                                            : (int64_t)p.slices * g.m * g.n * 4;
-  return p;
-}
-
-MfmaChoice gemm_mfma_choice(const GemmArgs& g, int cus, bool workspace) {
-  // A requested variant runs unsplit on the tile it names.
-  if (g.tile) return MfmaChoice{g.tile == 256, 1, g.k * elt_bytes(g.in)};
-  const SplitPlan p = gemm_split_plan(g, cus);
-  if (workspace && p.slices > 1) return MfmaChoice{p.big, p.slices, p.kb_slice};
-  // 256x256 tiles (4 waves of 128x128, one workgroup per CU) when there are
-  // at least half as many as CUs; otherwise 128x128 tiles (4 waves of 64x64,
-  // two workgroups per CU), which keep more CUs busy (measured on the
-  // projection sweep: M=1024, N=4096 runs 2x faster on 128x128 tiles,
-  // N=14336 (224 big tiles) runs faster on 256x256).
-  const int64_t tiles256 = ((g.m + 255) / 256) * ((g.n + 255) / 256);
-  return MfmaChoice{tiles256 >= cus / 2, 1, g.k * elt_bytes(g.in)};
-}
-
 namespace {
 
 // One storage order: AM = A stored [K, M] (trans_a), BM = B stored [K, N]
@@ -232,15 +109,20 @@ hipError_t run_layout(const GemmArgs& g, hipStream_t s, const MfmaChoice& c, voi
     return gemm_128_split_layout<AM, BM>(g, c.slices, c.kb_slice, ws, s);
   }
   if (c.big) return gemm_w4_layout<AM, BM>(g, s);
-  if (g.tile == 128) return gemm_128_grid_layout<AM, BM>(g, s);
+  // A requested 2x2 grid runs as the library's own 128x128 launch (its
+  // stage depth); the other grids run 64-byte stages.
+  if (g.tile == 128 && !(g.wave_m == 2 && g.wave_n == 2)) return gemm_128_grid_layout<AM, BM>(g, s);
   return gemm_128_layout<AM, BM>(g, s);
 }
 
 }  // namespace
 
+// The launch follows plan::mfma_choice (launch_plan.h): the library's own
+// choice, or the requested variant with the K slices it names.
 hipError_t gemm_mfma(const GemmArgs& g, hipStream_t s, void* workspace, int64_t workspace_bytes) {
   const int cus = device_cus();
-  const bool ws = !g.tile && workspace && workspace_bytes >= gemm_split_plan(g, cus).workspace_bytes;
+  const int64_t need = plan::workspace_bytes(shape_of(g), plan::Route::Mfma, cus);
+  const bool ws = workspace && need > 0 && workspace_bytes >= need;
   const MfmaChoice c = gemm_mfma_choice(g, cus, ws);
   void* tree_ws = c.slices > 1 ? workspace : nullptr;
   switch ((g.trans_a ? 2 : 0) | (g.trans_b ? 0 : 1)) {

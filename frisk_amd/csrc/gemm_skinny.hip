@@ -205,56 +205,6 @@ __global__ __launch_bounds__(256) void gemm_splitk_sum_kernel(const float* __res
   }
 }
 
-SkinnyPlan gemm_skinny_plan(const GemmArgs& g, int cus, bool split) {
-  SkinnyPlan p;
-  p.tm = g.m <= 16 ? 1 : g.m <= 32 ? 2 : g.m <= 64 ? 4 : 8;
-  p.tn = g.n >= 8192 ? 2 : 1;  // 32-column tiles once N alone gives >= 256 of them
-  const int64_t kb = g.k * 2;   // bf16 / f16
-  const int64_t steps = (kb + 63) / 64;
-  p.steps_per_slice = (int)steps;
-  p.slices = 1;
-  p.workspace_bytes = 0;
-  // Below 64 MiB of W the unsplit kernel ends before a second launch pays
-  // (16 x 4096 x 4096: 10.5 us unsplit, 12.7 us split).
-  // (The slice sum reads rows of 4 floats, so N % 4 != 0 runs unsplit too.)
-  if (!split || g.n * kb < ((int64_t)64 << 20) || g.n % 4 != 0) {
-    // 32 < M <= 64 with under 64 MiB of W: 32x32 tiles instead of 64x16,
-    // the same workgroup count with a fifth fewer operand loads per k-step
-    // (64 x 4096 x 4096, operands from HBM: 24.1 -> 19.6 us).
-    if (g.n * kb < ((int64_t)64 << 20) && p.tm == 4 && p.tn == 1) p.tm = p.tn = 2;
-    return p;
-  }
-  // Split-K with wider column tiles when the unsplit grid would stream X
-  // from L2 many times over: 64 columns per tile (32 at TM = 8, for
-  // registers); slices until the grid has one workgroup per CU (with the
-  // double-buffered batches, measured 4-9% faster than two per CU on most
-  // projection shapes, and 30% faster than four), each slice at least
-  // 4 waves x U k-steps, the f32 partials at most a quarter of the bytes of
-  // W (S.M.N.4 <= N.K.2 / 4).
-  const int tn = p.tm <= 4 ? 4 : 2;
-  const int64_t tiles = ((g.n + 16 * tn - 1) / (16 * tn)) * ((g.m + 16 * p.tm - 1) / (16 * p.tm));
-  // Wide tiles that alone fill most CUs in one round need no split: the
-  // second launch would cost more than the idle CUs (16 x 14336 x 4096:
-  // 224 tiles, 28.8 us unsplit against 31.6 us in two slices; 64 x 14336 x
-  // 4096: 43.2 against 49.9 us).
-  if (tiles * 20 >= (int64_t)cus * 17 && tiles <= cus) {
-    p.tn = tn;
-    return p;
-  }
-  const int64_t min_steps = 4 * (p.tm + tn <= 10 ? 4 : 2);
-  int64_t slices = ((int64_t)cus + tiles - 1) / tiles;
-  slices = std::min<int64_t>(slices, steps / min_steps);
-  slices = std::min<int64_t>(slices, kb / (16 * g.m));
-  slices = std::min<int64_t>(slices, 64);
-  if (slices >= 2) {
-    p.tn = tn;
-    p.steps_per_slice = (int)((steps + slices - 1) / slices);
-    p.slices = (int)((steps + p.steps_per_slice - 1) / p.steps_per_slice);
-    p.workspace_bytes = (int64_t)p.slices * g.m * g.n * 4;
-  }
-  return p;
-}
-
 namespace {
 
 template <Elt IN, Elt OUT, int TM, int TN>
@@ -314,12 +264,6 @@ hipError_t gemm_splitk_sum(const float* partial, int slices, const GemmArgs& g, 
       return hipErrorInvalidValue;
   }
   return hipGetLastError();
-}
-
-bool gemm_skinny_supported(const GemmArgs& g) {
-  const bool type_ok = (g.in == Elt::BF16 && (g.out == Elt::BF16 || g.out == Elt::F32)) ||
-                       (g.in == Elt::F16 && (g.out == Elt::F16 || g.out == Elt::F32));
-  return type_ok && g.m <= kSkinnyMaxM && !g.trans_a && g.trans_b;
 }
 
 hipError_t gemm_skinny(const GemmArgs& g, hipStream_t s, void* workspace, int64_t workspace_bytes) {

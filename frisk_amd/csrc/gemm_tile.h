@@ -36,7 +36,13 @@
 // (64 banks of 4 B: a 256 B window).
 //  * K-major: a ds_read_b128 has 16 lanes per cycle reading one logical
 //    chunk of 16 consecutive rows; swz sends them to 16 distinct chunks of
-//    the window (rocprofv3 SQ_LDS_BANK_CONFLICT = 0 for both maps).
+//    the window (rocprofv3 SQ_LDS_BANK_CONFLICT = 0 for both maps).  Both
+//    are the layout target's own proposals (proposeLdsSwizzle,
+//    frisk_amd/ir/layout.cpp): c ^ ((r >> 2) & 3) for 64-byte rows,
+//    c ^ ((r >> 1) & 7) for 128-byte rows; frisk_gemm_plan reports them and
+//    execute() checks them against the proposal.  (The 128-byte rows used
+//    c ^ (r & 7) ^ ((r >> 3) & 1) before: bit-identical results, timings
+//    within 1% on bf16 / fp8 / int8 at 4096^3 and 8192^3.)
 //  * MN-major 16-bit (rows of 512 or 256 B): 32 lanes read 4 k-rows (e) x
 //    64 B; swz(r) = (r & 3) << 2 moves row e to the 64 B quarter
 //    (c / 4) ^ e, four distinct quarters.
@@ -84,7 +90,7 @@ struct OpTile {
   // 16-bit types), so the M/N-major swizzles also fold in that row bit.
   __device__ static __forceinline__ int swz(int r) {
     if constexpr (!MN) {
-      if constexpr (KR == 128) return (r & 7) ^ ((r >> 3) & 1);
+      if constexpr (KR == 128) return (r >> 1) & 7;
       else return (r >> 2) & 3;  // KR == 64
     } else if constexpr (kEsz == 4) {
       return ((r >> 2) & 1) << 3;

@@ -5,6 +5,7 @@
 #include <stdint.h>
 
 #include "common.h"
+#include "launch_plan.h"
 
 
 namespace frisk {
@@ -23,43 +24,37 @@ struct GemmArgs {
   float scale;  // scale_a * scale_b
   int accumulate;
   // Requested kernel variant (0: the library chooses): 256 or 128 tiles,
-  // and the 128x128 kernel's wave grid.
-  int tile = 0, wave_m = 0, wave_n = 0;
+  // the 128x128 kernel's wave grid, and K slices of a 2x2-grid variant.
+  int tile = 0, wave_m = 0, wave_n = 0, slices = 0;
 };
 
-// Workspace of a split-K launch that sums its slices in the GEMM kernel
-// (splitk_tree, gemm_common.h): an f32 partial tile per (tile, slice) of
-// bt x bt outputs, then kTreeWords 64-bit arrival words per tile.
-constexpr int kTreeWords = 64;
-// The 128x128 kernel's split-K sums at most this many slices inside its
-// launch (gemm_128.h); more go through gemm_splitk_sum.
-#ifndef FRISK_TREE_MAX_SLICES
-#define FRISK_TREE_MAX_SLICES 2
-#endif
-constexpr int kTreeMaxSlices = FRISK_TREE_MAX_SLICES;
-inline int64_t split_tree_bytes(int64_t tiles, int64_t slices, int bt) {
-  return tiles * slices * (int64_t)bt * bt * 4 + tiles * kTreeWords * 8;
+// The request as the launch planner (launch_plan.h) sees it.
+inline plan::GemmShape shape_of(const GemmArgs& g) {
+  plan::GemmShape s;
+  s.in = (int)g.in;
+  s.out = (int)g.out;
+  s.m = g.m;
+  s.n = g.n;
+  s.k = g.k;
+  s.trans_a = g.trans_a != 0;
+  s.trans_b = g.trans_b != 0;
+  s.tile = g.tile;
+  s.wave_m = g.wave_m;
+  s.wave_n = g.wave_n;
+  s.slices = g.slices;
+  return s;
 }
 
-// Split-K plan of the LDS-staged MFMA kernels (bf16/f16): `slices` slices
-// of kb_slice bytes of K whose f32 partials and arrival words take
-// workspace_bytes; slices == 1 runs unsplit.
-struct SplitPlan {
-  int slices;
-  int64_t kb_slice;
-  int64_t workspace_bytes;
-  bool big;  // slices run on 256x256 tiles (gemm_w4.h) instead of 128x128
-};
-SplitPlan gemm_split_plan(const GemmArgs& g, int cus);
-// The launch gemm_mfma makes: 256x256 tiles (big) or 128x128, and the K
-// slices (1: unsplit) of kb_slice bytes; `workspace` = a large enough
-// workspace is at hand.
-struct MfmaChoice {
-  bool big;
-  int slices;
-  int64_t kb_slice;
-};
-MfmaChoice gemm_mfma_choice(const GemmArgs& g, int cus, bool workspace);
+using plan::kTreeMaxSlices;
+using plan::kTreeWords;
+using plan::split_tree_bytes;
+using SplitPlan = plan::SplitPlan;
+using MfmaChoice = plan::MfmaChoice;
+using SkinnyPlan = plan::SkinnyPlan;
+inline SplitPlan gemm_split_plan(const GemmArgs& g, int cus) { return plan::split_plan(shape_of(g), cus); }
+inline MfmaChoice gemm_mfma_choice(const GemmArgs& g, int cus, bool workspace) {
+  return plan::mfma_choice(shape_of(g), cus, workspace);
+}
 // LDS-staged MFMA GEMM, any storage order of A and B; the caller checked 16 B
 // aligned operands with 16 B row pitches, K * esize % 16 == 0 for every
 // K-major operand and a 16 B row pitch of C.  With a workspace of at least
@@ -79,12 +74,10 @@ template <bool AM, bool BM>
 hipError_t gemm_w4_split_layout(const GemmArgs& g, int slices, int64_t kb_slice, void* ws,
                                 hipStream_t s);
 template <bool AM, bool BM> hipError_t gemm_128_layout(const GemmArgs& g, hipStream_t s);
-// Bytes of K per row per pipeline stage of gemm_128_layout's launch: 128
-// when its grid of 128x128 tiles is at most one workgroup per CU, else 64
-// (two workgroups per CU fit in LDS).
+// Bytes of K per row per pipeline stage of gemm_128_layout's launch
+// (plan::stage_bytes_128).
 inline int gemm_128_stage_bytes(const GemmArgs& g, int cus) {
-  const int64_t tiles = ((g.m + 127) / 128) * ((g.n + 127) / 128);
-  return tiles <= cus ? 128 : 64;
+  return plan::stage_bytes_128(shape_of(g), cus);
 }
 // The 128x128 kernel with the wave grid g.wave_m x g.wave_n (2x2, 4x1, 1x4,
 // 2x1 or 1x2), 64-byte stages.
@@ -94,21 +87,14 @@ hipError_t gemm_128_split_layout(const GemmArgs& g, int slices, int64_t kb_slice
                                  hipStream_t s);
 // Any layout / shape; LDS-tiled FMA kernel.
 hipError_t gemm_generic_any(const GemmArgs& g, hipStream_t s);
-// Small-M kernel (M <= kSkinnyMaxM, bf16/f16, trans_a == 0, trans_b == 1,
-// 16 B aligned K-contiguous rows); memory-bound regime.
-#ifndef FRISK_SKINNY_MAX_M
-#define FRISK_SKINNY_MAX_M 128
-#endif
-constexpr int kSkinnyMaxM = FRISK_SKINNY_MAX_M;
-bool gemm_skinny_supported(const GemmArgs& g);
-// Launch shape of the small-M kernel: TM x TN 16x16 atoms per workgroup
-// (4 waves), `slices` K slices of `steps_per_slice` 64-byte k-steps, and
-// the f32 workspace the slices' partial tiles need (0 without split-K).
-struct SkinnyPlan {
-  int tm, tn, slices, steps_per_slice;
-  int64_t workspace_bytes;
-};
-SkinnyPlan gemm_skinny_plan(const GemmArgs& g, int cus, bool split);
+// Small-M kernel (plan::skinny_supported: M <= kSkinnyMaxM, bf16/f16,
+// trans_a == 0, trans_b == 1, 16 B aligned K-contiguous rows);
+// memory-bound regime.
+using plan::kSkinnyMaxM;
+inline bool gemm_skinny_supported(const GemmArgs& g) { return plan::skinny_supported(shape_of(g)); }
+inline SkinnyPlan gemm_skinny_plan(const GemmArgs& g, int cus, bool split) {
+  return plan::skinny_plan(shape_of(g), cus, split);
+}
 // Split-K runs when `workspace` holds at least the plan's workspace_bytes
 // (16-byte aligned); otherwise the unsplit kernel runs.
 hipError_t gemm_skinny(const GemmArgs& g, hipStream_t s, void* workspace, int64_t workspace_bytes);
@@ -125,6 +111,7 @@ struct AttnArgs {
   const void* k;
   int64_t k_sb, k_sh, k_ss;  // k_ss: between keys, or with k_dmajor between head_dim rows
   int k_dmajor;              // K stored [batch, heads, head_dim, seq]
+  int waves = 0;             // waves per workgroup (4 or 8); 0: plan::attn_waves
   const void* v;
   int64_t v_sb, v_sh, v_ss;
   void* o;

@@ -29,14 +29,31 @@ whole-tensor operation, and launches the MI355X kernel for it:
   for them are allowed in the loop.  `sm_scale` (default 1/sqrt(D)) and
   `causal` are arguments of execute().
 
-A tiled GEMM program also names its workgroup tile (BM x BN) and thread
-count.  `plan()` runs layout inference (frisk_amd/ir/infer.cpp) on a copy of
-the program and reads the instruction contract of its tile product (MFMA
-atom and wave grid, `#frisk.mma_contract`); when a compiled kernel executes
-exactly that workgroup product (frisk_amd/variants.py) `execute()` runs that
-variant (`frisk_gemm_desc.tile / wave_m / wave_n`), and `plan().layouts_match`
-is True.  Otherwise the library's own tiling runs and `mismatch` says why.
-The attention kernel keeps its own tiling.  Anything else raises ValueError
+The kernel that runs comes from layout decisions made here, not inside the
+library:
+
+* A tiled GEMM program names its workgroup tile (BM x BN) and thread count.
+  `plan()` runs layout inference (frisk_amd/ir/infer.cpp) on a copy of the
+  program and reads the instruction contract of its tile product (MFMA atom
+  and wave grid, `#frisk.mma_contract`); when a compiled kernel executes
+  exactly that workgroup product (frisk_amd/variants.py) `execute()` runs
+  that variant (`frisk_gemm_desc.tile / wave_m / wave_n`, and the K slices
+  the launch contract gives the same tile and grid).
+* A whole-matrix GEMM takes the gfx950 target's launch contract
+  (`F.frisk.gemm_launch_plan`: kernel, workgroup tile, wave grid, stage
+  depth, K slices; launch_plan.h, shared with the C-ABI), then the
+  instruction contract inference solves for that workgroup tile under the
+  op's warp policy, and `execute()` requests that variant with those slices.
+  The small-M and generic kernels have no tile program: their launch
+  contract names them and the library runs them.
+* Attention takes the waves per workgroup from the target's attention
+  launch contract (`F.frisk.attention_launch_plan`) and requests them.
+
+Every request is checked against the C-ABI first (`frisk_gemm_plan`): when
+the tensors do not meet a variant's conditions (alignment, pitches) the
+library's own choice runs and `mismatch` says why; `layouts_match` is False
+whenever the kernel that runs is not the one the contracts name.  Packets
+(`execute_packet`) follow the same rule.  Anything else raises ValueError
 naming the first mismatch.  There is no CPU fallback.
 """
 from __future__ import annotations
@@ -72,6 +89,15 @@ class GemmPlan:
     # The program's workgroup tile (bm, bn, bk, dtype, policy, threads), or
     # None for a whole-matrix program.
     tile: Optional[tuple] = field(default=None, repr=False)
+    # The launch contract of the GEMM (the target's gemm_launch_plan); the
+    # variant above carries its K slices when it runs that tile and grid.
+    launch: Optional[dict] = None
+    # Whether the MFMA kernel's LDS swizzle of each K-major operand is the
+    # layout target's proposal for its stage rows (None: nothing to check).
+    swizzle_match: Optional[bool] = None
+    # A / B and C element types (IR spelling), and the GEMM's warp policy.
+    elems: Optional[tuple] = field(default=None, repr=False)
+    policy: object = field(default=None, repr=False)
 
 
 @dataclass
@@ -85,6 +111,9 @@ class AttnPlan:
     heads: int
     seq: int
     head_dim: int
+    # Waves per workgroup from the attention launch contract (causal and
+    # non-causal: causal is an argument of execute()).
+    waves: Optional[dict] = None
 
 
 class _Reject(ValueError):
@@ -209,7 +238,9 @@ def _gemm_whole(ops, entry) -> GemmPlan:
             _fail("only a zero fill of C may precede the GEMM")
         clear = True
     return GemmPlan(idx[0], idx[1], idx[2], bool(op.get_attr("transA")), bool(op.get_attr("transB")),
-                    clear, op.get_attr("M"), op.get_attr("N"), op.get_attr("K"))
+                    clear, op.get_attr("M"), op.get_attr("N"), op.get_attr("K"),
+                    elems=(_elem(g.get_matrix_A()), _elem(g.get_matrix_C())),
+                    policy=op.get_attr("policy"))
 
 
 def _gemm_tiled(ops, entry) -> GemmPlan:
@@ -307,10 +338,15 @@ def _gemm_tiled(ops, entry) -> GemmPlan:
               f"A{a_shape} B{b_shape} C{c_shape} exactly")
     if _elem(a_t) != _elem(a_src) or _elem(b_t) != _elem(b_src):
         _fail("A/B tiles must keep the input dtype")
-    names = {"f16": "fp16", "bf16": "bf16", "f8E4M3FN": "e4m3fn", "i8": "int8", "f32": "fp32"}
-    tile = (bm, bn, bk, names.get(_elem(a_t), _elem(a_t)), gop.get_attr("policy"),
+    tile = (bm, bn, bk, _HELPER_NAMES.get(_elem(a_t), _elem(a_t)), gop.get_attr("policy"),
             par.get_thread_num())
-    return GemmPlan(ia, ib, ic, ta, tb, True, M, N, K, tile=tile)
+    return GemmPlan(ia, ib, ic, ta, tb, True, M, N, K, tile=tile,
+                    elems=(_elem(a_src), _elem(dst)), policy=gop.get_attr("policy"))
+
+
+# Element type (IR spelling) -> the session helper's dtype name.
+_HELPER_NAMES = {"f16": "fp16", "bf16": "bf16", "f8E4M3FN": "e4m3fn", "i8": "int8", "f32": "fp32"}
+_ESIZE = {"fp16": 2, "bf16": 2, "e4m3fn": 1, "int8": 1, "fp32": 4}
 
 
 # ---------------------------------------------------------------------------
@@ -473,20 +509,104 @@ def _tile_contract(bm, bn, bk, dtype, trans_a, trans_b, threads, policy_key, pol
         return None, f"no instruction contract: {e}"
 
 
+def _device_cus() -> int:
+    """Compute units of the current GPU (256, MI355X's count, without one)."""
+    try:
+        import torch
+        if torch.cuda.is_available():
+            return int(torch.cuda.get_device_properties(torch.cuda.current_device())
+                       .multi_processor_count)
+    except Exception:  # no torch / no device: plan for the MI355X
+        pass
+    return 256
+
+
+_TYPES_SESSION = []  # one session kept alive: its context owns the types below
+
+
+@lru_cache(maxsize=None)
+def _type_of(elem: str):
+    """An IR element type from its spelling, owned by a session that lives as
+    long as the process."""
+    from .common import utils
+    if not _TYPES_SESSION:
+        _TYPES_SESSION.append(utils.create_session())
+    names = dict(_HELPER_NAMES, i32="int32")
+    return _TYPES_SESSION[0]._as_type(names.get(elem, elem))
+
+
+def _launch(p: "GemmPlan") -> dict:
+    """The target's launch contract of the whole GEMM (with a workspace)."""
+    a_ty, c_ty = (_type_of(e) for e in p.elems)
+    return fr.gemm_launch_plan(p.m, p.n, p.k, a_ty, c_ty, p.trans_a, p.trans_b,
+                               cus=_device_cus(), workspace=True)
+
+
 def _bind_variant(p: "GemmPlan", tile) -> "GemmPlan":
-    """Fill p.contract / variant / layouts_match / mismatch for the
-    workgroup tile `tile` = (bm, bn, bk, dtype, policy, threads), or record
-    that the program names none."""
-    if tile is None:
-        p.mismatch = "whole-matrix program: it names no workgroup tile, the library tiles it"
+    """Fill p.launch / contract / variant / layouts_match / mismatch: the
+    kernel variant that executes the program's workgroup tile product (a
+    tiled program), or the one the launch contract names for the whole GEMM
+    (a whole-matrix program)."""
+    try:
+        p.launch = _launch(p)
+    except ValueError as e:
+        p.mismatch = f"no launch contract: {e}"
         return p
+    p.swizzle_match = _swizzles_match(p)
+    if tile is None:
+        L = p.launch
+        if L["kernel"] not in ("gemm_w4", "gemm_128"):
+            # The small-M and generic kernels have no tile program: the
+            # launch contract names them, and the library runs them.
+            p.contract, p.layouts_match = L["contract"], True
+            return p
+        dname = _HELPER_NAMES.get(p.elems[0], p.elems[0])
+        bt, (wm, wn) = L["tile"][0], L["wave_grid"]
+        tile = (bt, bt, L["stage_bytes"] // _ESIZE.get(dname, 2), dname, p.policy, 64 * wm * wn)
     bm, bn, bk, dtype, policy, threads = tile
     p.contract, why = tile_contract(bm, bn, bk, dtype, p.trans_a, p.trans_b, threads, policy)
     if p.contract is not None:
         p.variant, why = variants.variant_for(p.contract, bm, bn, threads)
+    if p.variant is not None:
+        # The launch contract's K split, when it runs this very tile and grid.
+        L = p.launch
+        if L["kernel"] in ("gemm_w4", "gemm_128") and L["tile"] == [bm, bn] and \
+                list(p.variant[1:]) == L["wave_grid"] and L["slices"] > 1:
+            p.variant = tuple(p.variant) + (L["slices"],)
     p.layouts_match = p.variant is not None
     p.mismatch = why
     return p
+
+
+def _swizzles_match(p: "GemmPlan") -> Optional[bool]:
+    """Checks the MFMA kernel's LDS swizzles against the layout target's
+    storage proposal (`F.frisk.lds_swizzle`, the swizzle inference gives a
+    Shared tile read by MFMA fragments) for the kernel's K-major stage rows.
+    The M/N-major tiles are read by transposing loads, which the proposer
+    does not model; they are not compared."""
+    L = p.launch
+    if L is None or L["kernel"] not in ("gemm_w4", "gemm_128"):
+        return None
+    proposal = fr.lds_swizzle(L["stage_bytes"], 32).formula
+    kmajor = [L["lds_swizzle_a"]] if not p.trans_a else []
+    kmajor += [L["lds_swizzle_b"]] if p.trans_b else []
+    return all(sw == proposal for sw in kmajor) if kmajor else None
+
+
+def _checked_variant(p: "GemmPlan", a, b, c):
+    """p.variant if the C-ABI runs it on these tensors, else None (the
+    library's own choice then runs, and p.mismatch / layouts_match say so)."""
+    from . import runtime as rt
+    if p.variant is None:
+        return None
+    try:
+        rt.gemm_plan(a, b, c, trans_a=p.trans_a, trans_b=p.trans_b, variant=p.variant)
+    except ValueError as e:
+        p.mismatch = f"variant {p.variant} does not run on these tensors ({e}); the library's own " \
+                     "choice runs"
+        p.layouts_match = False
+        return None
+    return p.variant
 
 
 def plan(module, kernel: str):
@@ -530,8 +650,11 @@ def _check_tensor(t, value, name):
 
 
 def execute(module, kernel: str, tensors: Sequence, *, stream=None, causal: bool = False,
-            sm_scale: Optional[float] = None, scale_a: float = 1.0, scale_b: float = 1.0):
-    """Run kernel `kernel` of `module` on `tensors` (one per kernel argument)."""
+            sm_scale: Optional[float] = None, scale_a: float = 1.0, scale_b: float = 1.0,
+            require_layout_match: bool = False):
+    """Run kernel `kernel` of `module` on `tensors` (one per kernel argument).
+    With require_layout_match a GEMM whose contracts no kernel runs raises
+    ValueError instead of running the library's own choice."""
     from . import runtime as rt
     p = plan(module, kernel)
     k = module.get_kernel(kernel)
@@ -543,11 +666,18 @@ def execute(module, kernel: str, tensors: Sequence, *, stream=None, causal: bool
     if isinstance(p, tileprog.OpsPlan):
         return tileprog.run(p, tensors, stream=stream)
     if isinstance(p, GemmPlan):
-        return rt.gemm(tensors[p.a], tensors[p.b], tensors[p.c], trans_a=p.trans_a, trans_b=p.trans_b,
-                       clear_accum=p.clear_accum, scale_a=scale_a, scale_b=scale_b, stream=stream,
-                       variant=p.variant)
+        a, b, c = tensors[p.a], tensors[p.b], tensors[p.c]
+        variant = _checked_variant(p, a, b, c)
+        if require_layout_match and not p.layouts_match:
+            raise ValueError(f"execute: no kernel runs the contracts of @{kernel} ({p.mismatch})")
+        return rt.gemm(a, b, c, trans_a=p.trans_a, trans_b=p.trans_b, clear_accum=p.clear_accum,
+                       scale_a=scale_a, scale_b=scale_b, stream=stream, variant=variant)
     q, kk, v, o = (tensors[i] for i in (p.q, p.k, p.v, p.o))
     # A K stored [B, H, D, S] (the reference's FA tile program) is read in
-    # place by the kernel's transposed-K variant.
+    # place by the kernel's transposed-K variant; the waves per workgroup
+    # come from the attention launch contract.
+    waves = fr.attention_launch_plan(p.batch * p.heads, p.seq, p.head_dim, causal,
+                                     _device_cus())["waves"]
+    p.waves = {"causal" if causal else "full": waves}
     return rt.attn_fwd(q, kk, v, o, causal=causal, sm_scale=sm_scale, stream=stream,
-                       k_transposed=p.k_transposed)
+                       k_transposed=p.k_transposed, waves=waves)

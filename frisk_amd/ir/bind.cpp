@@ -1273,6 +1273,34 @@ void bindFrisk(py::module_& m) {
     if (out.empty()) throw InvalidArgument(err);
     return out;
   }, py::arg("module"));
+  m.def("gemm_launch_plan", [](int64_t mm, int64_t n, int64_t k, const PyType& in, const PyType& out,
+                               bool transA, bool transB, int64_t cus, bool workspace,
+                               bool matrixCores) {
+    const GemmLaunchContract c =
+        cdna4GemmLaunch(mm, n, k, in.t, out.t, transA, transB, cus, workspace, matrixCores);
+    py::dict d;
+    d["kernel"] = c.kernel;
+    d["tile"] = std::vector<int64_t>{c.tileM, c.tileN};
+    d["wave_grid"] = std::vector<int64_t>{c.waveM, c.waveN};
+    d["stage_bytes"] = c.stageBytes;
+    d["slices"] = c.slices;
+    d["kb_slice"] = c.kbSlice;
+    d["slice_sum"] = c.sliceSum;
+    d["workspace_bytes"] = c.workspaceBytes;
+    d["lds_swizzle_a"] = c.swizzleA;
+    d["lds_swizzle_b"] = c.swizzleB;
+    d["contract"] = c.str();
+    return d;
+  }, py::arg("m"), py::arg("n"), py::arg("k"), py::arg("in_type"), py::arg("out_type"),
+     py::arg("trans_a") = false, py::arg("trans_b") = false, py::arg("cus") = 256,
+     py::arg("workspace") = true, py::arg("matrix_cores") = true);
+  m.def("attention_launch_plan", [](int64_t batchHeads, int64_t seqQ, int64_t headDim, bool causal,
+                                    int64_t cus) {
+    py::dict d;
+    d["waves"] = cdna4AttentionWaves(batchHeads, seqQ, headDim, causal, cus);
+    return d;
+  }, py::arg("batch_heads"), py::arg("seq_q"), py::arg("head_dim"), py::arg("causal") = false,
+     py::arg("cus") = 256);
   m.def("cost_profile_defaults", []() {
     CostProfile p = CostProfile::defaults();
     py::dict d;

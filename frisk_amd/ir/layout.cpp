@@ -2,6 +2,8 @@
 // (checked GF(2) linear forms) and LDS swizzle proposals.
 #include "layout.h"
 
+#include "../csrc/launch_plan.h"
+
 #include <algorithm>
 #include <cmath>
 #include <sstream>
@@ -231,6 +233,78 @@ SwizzleProposal proposeLdsSwizzle(int64_t rowBytes, int atomM) {
 int64_t sm90StyleSwizzle(int64_t off, int64_t sw) {
   if (sw != 32 && sw != 64 && sw != 128) throw InvalidArgument("swizzle must be 32, 64 or 128 bytes");
   return off ^ (((off >> 7) & (sw / 16 - 1)) << 4);
+}
+
+}  // namespace fir
+
+namespace fir {
+
+namespace {
+
+// frisk_dtype code of an IR element type (include/frisk_hip.h).
+int dtypeCode(Type t) {
+  namespace P = frisk::plan;
+  if (t.isF32()) return P::kF32;
+  if (t.isF16()) return P::kF16;
+  if (t.isBF16()) return P::kBF16;
+  if (t.isFloat(FloatKind::E4M3FN)) return P::kE4M3;
+  if (t.isSignlessInteger(8)) return P::kI8;
+  if (t.isSignlessInteger(32)) return P::kI32;
+  throw InvalidArgument("launch contract: no GEMM kernel takes element type " + t.str());
+}
+
+}  // namespace
+
+std::string GemmLaunchContract::str() const {
+  std::ostringstream o;
+  o << "#frisk.gemm_launch<{kernel = \"" << kernel << "\", tile = [" << tileM << ", " << tileN
+    << "], wave_grid = [" << waveM << ", " << waveN << "], stage_bytes = " << stageBytes
+    << ", slices = " << slices << ", slice_sum = \"" << sliceSum << "\"}>";
+  return o.str();
+}
+
+GemmLaunchContract cdna4GemmLaunch(int64_t m, int64_t n, int64_t k, Type in, Type out, bool transA,
+                                   bool transB, int64_t cus, bool workspace, bool matrixCores) {
+  namespace P = frisk::plan;
+  if (m <= 0 || n <= 0 || k <= 0) throw InvalidArgument("launch contract: M, N and K must be positive");
+  P::GemmShape g;
+  g.in = dtypeCode(in);
+  g.out = dtypeCode(out);
+  g.m = m;
+  g.n = n;
+  g.k = k;
+  g.trans_a = transA;
+  g.trans_b = transB;
+  const P::Route r = P::route_of(g, matrixCores);
+  const P::GemmLaunch L = P::launch_of(g, r, (int)cus, workspace ? INT64_MAX : 0);
+  GemmLaunchContract c;
+  c.kernel = L.kernel == P::Kernel::W4 ? "gemm_w4"
+             : L.kernel == P::Kernel::T128 ? "gemm_128"
+             : L.kernel == P::Kernel::Skinny ? "gemm_skinny" : "gemm_generic";
+  c.tileM = L.tile_m;
+  c.tileN = L.tile_n;
+  c.waveM = L.wave_m;
+  c.waveN = L.wave_n;
+  c.stageBytes = L.stage_bytes;
+  c.slices = L.slices;
+  c.kbSlice = L.kb_slice;
+  c.workspaceBytes = L.workspace_bytes;
+  c.sliceSum = L.slice_sum == P::SliceSum::InLaunch ? "in_launch"
+               : L.slice_sum == P::SliceSum::SecondLaunch ? "second_launch" : "none";
+  if (L.kernel == P::Kernel::W4 || L.kernel == P::Kernel::T128) {
+    const int es = P::dtype_bytes(g.in);
+    c.swizzleA = P::lds_swizzle(transA, es, L.stage_bytes, L.tile_m * es);
+    c.swizzleB = P::lds_swizzle(!transB, es, L.stage_bytes, L.tile_n * es);
+  }
+  return c;
+}
+
+int64_t cdna4AttentionWaves(int64_t batchHeads, int64_t seqQ, int64_t headDim, bool causal,
+                            int64_t cus) {
+  if (batchHeads <= 0 || seqQ <= 0) throw InvalidArgument("launch contract: sizes must be positive");
+  if (headDim != 16 && headDim != 32 && headDim != 64 && headDim != 128)
+    throw InvalidArgument("launch contract: the attention kernel takes head_dim 16, 32, 64 or 128");
+  return frisk::plan::attn_waves(batchHeads, seqQ, headDim, causal, (int)cus);
 }
 
 }  // namespace fir

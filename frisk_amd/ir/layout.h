@@ -108,4 +108,26 @@ SwizzleProposal proposeLdsSwizzle(int64_t rowBytes, int atomM);
 // off ^ (((off >> 7) & (sw/16 - 1)) << 4) for sw in {32, 64, 128}.
 int64_t sm90StyleSwizzle(int64_t off, int64_t swizzleBytes);
 
+// ---- launch contracts ------------------------------------------------------
+// The gfx950 target's launch-level decisions, shared with the C-ABI
+// (frisk_amd/csrc/launch_plan.h): for a whole-matrix GEMM the kernel, its
+// workgroup tile, wave grid, LDS stage depth and K split; for attention the
+// waves per workgroup.  The reference binds the corresponding choice (the
+// warpgroup grid of each MMA) in its SM90 layout target
+// (SM90LayoutTarget.cpp:171-481).
+struct GemmLaunchContract {
+  std::string kernel;  // gemm_w4 (256x256), gemm_128, gemm_skinny, gemm_generic
+  int64_t tileM = 0, tileN = 0, waveM = 0, waveN = 0, stageBytes = 0, slices = 1;
+  int64_t kbSlice = 0, workspaceBytes = 0;
+  std::string sliceSum;  // none, in_launch, second_launch
+  std::string swizzleA, swizzleB;  // LDS stage-tile swizzles of the MFMA kernels
+  std::string str() const;  // #frisk.gemm_launch<{...}>
+};
+// `workspace`: a split-K workspace is at hand; `matrixCores`: the operands
+// meet the MFMA kernels' alignment and reach conditions.
+GemmLaunchContract cdna4GemmLaunch(int64_t m, int64_t n, int64_t k, Type in, Type out, bool transA,
+                                   bool transB, int64_t cus, bool workspace, bool matrixCores);
+int64_t cdna4AttentionWaves(int64_t batchHeads, int64_t seqQ, int64_t headDim, bool causal,
+                            int64_t cus);
+
 }  // namespace fir

@@ -33,7 +33,7 @@ from __future__ import annotations
 import json
 import re
 
-from . import variants
+from . import _ir, variants
 
 __all__ = ["plan_packet", "execute_packet"]
 
@@ -257,23 +257,28 @@ def _plan_reduce(body, producer, values, source_arg, types, args, root):
             "leaf_order": order, "arg_types": [types[a] for a in args]}
 
 
-def execute_packet(packet, tensors, *, stream=None, allow_layout_mismatch=False) -> dict:
+def execute_packet(packet, tensors, *, stream=None, require_layout_match=False,
+                   allow_layout_mismatch=None) -> dict:
     """Run the packet on the GPU with `tensors` bound to the kernel's
     arguments (in order).  Returns the plan that was executed.
 
-    A GEMM packet runs on the kernel variant its MMA contract selects, an
-    attention packet on the attention kernel.  When no kernel executes the
-    packet's contract (`plan_packet(...)["layouts_match"]` is False) this
-    raises ValueError with the reason, unless `allow_layout_mismatch`, which
-    runs the library's own kernel on the same tensors (same mathematics,
-    other register layouts)."""
+    The rule is execute()'s: a GEMM packet runs on the kernel variant its MMA
+    contract selects, an attention packet on the attention kernel with the
+    waves of its launch contract; when no kernel executes the packet's
+    contract (`layouts_match` False, `mismatch` says why) the library's own
+    kernel runs on the same tensors (same mathematics, other register
+    layouts), unless `require_layout_match`, which raises ValueError
+    instead.  (`allow_layout_mismatch=False` is the older spelling of
+    require_layout_match=True.)"""
     from . import runtime as rt
+    from .executor import _device_cus
+    if allow_layout_mismatch is False:
+        require_layout_match = True
     plan = plan_packet(packet)
-    if plan["kind"] in ("gemm", "attention") and not plan["layouts_match"] and \
-            not allow_layout_mismatch:
+    if plan["kind"] in ("gemm", "attention") and not plan["layouts_match"] and require_layout_match:
         raise ValueError(f"execution packet: no kernel executes this {plan['kind']} packet's "
-                         f"instruction contract ({plan['mismatch']}); pass "
-                         "allow_layout_mismatch=True to run the library's own kernel")
+                         f"instruction contract ({plan['mismatch']}); without "
+                         "require_layout_match the library's own kernel runs")
     tensors = list(tensors)
     if len(tensors) != len(plan["arg_types"]):
         raise ValueError(f"execution packet: kernel takes {len(plan['arg_types'])} arguments, "
@@ -284,8 +289,19 @@ def execute_packet(packet, tensors, *, stream=None, allow_layout_mismatch=False)
             raise ValueError(f"execution packet: argument of type {ty} bound to a tensor of shape "
                              f"{tuple(t.shape)}")
     if plan["kind"] == "gemm":
-        rt.gemm(tensors[plan["a"]], tensors[plan["b"]], tensors[plan["c"]], trans_a=plan["trans_a"],
-                trans_b=plan["trans_b"], stream=stream, variant=plan["variant"])
+        a, b, c = tensors[plan["a"]], tensors[plan["b"]], tensors[plan["c"]]
+        variant = plan["variant"]
+        if variant is not None:
+            try:  # the variant's conditions (alignment, pitches) on these tensors
+                rt.gemm_plan(a, b, c, trans_a=plan["trans_a"], trans_b=plan["trans_b"],
+                             variant=variant)
+            except ValueError as e:
+                if require_layout_match:
+                    raise
+                plan["mismatch"] = f"variant {variant} does not run on these tensors ({e})"
+                plan["layouts_match"], variant = False, None
+        rt.gemm(a, b, c, trans_a=plan["trans_a"], trans_b=plan["trans_b"], stream=stream,
+                variant=variant)
     elif plan["kind"] == "reduce":
         dst = tensors[plan["dst"]]
         if plan["init"] is not None:
@@ -299,6 +315,8 @@ def execute_packet(packet, tensors, *, stream=None, allow_layout_mismatch=False)
     else:
         q, k, v, o = (tensors[plan[n]] for n in ("q", "k", "v", "o"))
         view = lambda t: t.view(1, 1, *t.shape)
+        plan["waves"] = _ir().frisk.attention_launch_plan(1, q.shape[0], q.shape[1], False,
+                                                          _device_cus())["waves"]
         rt.attn_fwd(view(q), view(k), view(v), view(o), causal=False, sm_scale=plan["scale"],
-                    stream=stream)
+                    stream=stream, waves=plan["waves"])
     return plan

@@ -44,7 +44,7 @@ class GemmDesc(ctypes.Structure):
         ("scale_a", ctypes.c_float), ("scale_b", ctypes.c_float),
         ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_int64),
         ("tile", ctypes.c_int32), ("wave_m", ctypes.c_int32), ("wave_n", ctypes.c_int32),
-        ("variant_flags", ctypes.c_int32),
+        ("variant_flags", ctypes.c_int32), ("slices", ctypes.c_int32),
     ]
 
 
@@ -63,7 +63,7 @@ class AttnDesc(ctypes.Structure):
         ("o_stride_s", ctypes.c_int64),
         ("lse", ctypes.c_void_p),
         ("o_dtype", ctypes.c_int32),
-        ("k_transposed", ctypes.c_int32),
+        ("k_transposed", ctypes.c_int32), ("waves", ctypes.c_int32),
     ]
 
 
@@ -187,7 +187,8 @@ def _row_major(t, name: str) -> int:
 def gemm_desc(a, b, c, *, trans_a=False, trans_b=False, clear_accum=True,
               scale_a=1.0, scale_b=1.0, variant=None) -> GemmDesc:
     """Describe C (+)= op(A).op(B) for row-major device tensors (see frisk_hip.h).
-    `variant` = (tile, wave_m, wave_n) requests a kernel variant (frisk_gemm_desc.tile)."""
+    `variant` = (tile, wave_m, wave_n) or (tile, wave_m, wave_n, slices)
+    requests a kernel variant (frisk_gemm_desc.tile ... slices)."""
     lda, ldb, ldc = _row_major(a, "A"), _row_major(b, "B"), _row_major(c, "C")
     m = a.shape[1] if trans_a else a.shape[0]
     k = a.shape[0] if trans_a else a.shape[1]
@@ -200,7 +201,8 @@ def gemm_desc(a, b, c, *, trans_a=False, trans_b=False, clear_accum=True,
                     torch_dtype_code(a.dtype), torch_dtype_code(b.dtype), torch_dtype_code(c.dtype),
                     int(bool(clear_accum)), a.data_ptr(), lda, b.data_ptr(), ldb,
                     c.data_ptr(), ldc, float(scale_a), float(scale_b), None, 0,
-                    *(tuple(variant) if variant else (0, 0, 0)), 0)
+                    *(tuple(variant[:3]) if variant else (0, 0, 0)), 0,
+                    int(variant[3]) if variant and len(variant) > 3 else 0)
 
 
 def gemm_workspace_bytes(a, b, c, *, trans_a=False, trans_b=False) -> int:
@@ -214,7 +216,7 @@ def gemm_workspace_bytes(a, b, c, *, trans_a=False, trans_b=False) -> int:
 def plan_of(desc: GemmDesc) -> dict:
     """frisk_gemm_plan for a descriptor: the launch frisk_gemm would make."""
     import json
-    buf = ctypes.create_string_buffer(512)
+    buf = ctypes.create_string_buffer(1024)
     _check(load().frisk_gemm_plan(ctypes.byref(desc), buf, len(buf)), "frisk_gemm_plan")
     return json.loads(buf.value.decode())
 
@@ -237,9 +239,9 @@ def gemm(a, b, c, *, trans_a=False, trans_b=False, clear_accum=True,
 
     `workspace`: True allocates the scratch frisk_gemm_workspace_size asks
     for (torch's caching allocator), a device tensor supplies it, False runs
-    the unsplit kernels.  `variant` = (tile, wave_m, wave_n) runs that kernel
-    variant (unsplit): (256, 2, 2), or (128, gm, gn) with the wave grid
-    2x2, 4x1, 1x4, 2x1 or 1x2."""
+    the unsplit kernels.  `variant` = (tile, wave_m, wave_n[, slices]) runs
+    that kernel variant: (256, 2, 2), or (128, gm, gn) with the wave grid
+    2x2, 4x1, 1x4, 2x1 or 1x2, unsplit or (2x2 grid) in `slices` K slices."""
     d = gemm_desc(a, b, c, trans_a=trans_a, trans_b=trans_b, clear_accum=clear_accum,
                   scale_a=scale_a, scale_b=scale_b, variant=variant)
     ws = None
@@ -299,7 +301,7 @@ def probe_lds_transpose(bits: int, out, stream=None):
 
 
 def attn_desc(q, k, v, o, *, causal=False, sm_scale=None, lse=None,
-              k_transposed=False) -> AttnDesc:
+              k_transposed=False, waves=0) -> AttnDesc:
     """Describe the attention forward of [batch, heads, seq, head_dim] device
     tensors; with k_transposed, K is [batch, heads, head_dim, seq_k] with unit
     key stride (read in place, not copied)."""
@@ -334,15 +336,17 @@ def attn_desc(q, k, v, o, *, causal=False, sm_scale=None, lse=None,
                     v.data_ptr(), vs[0], vs[1], vs[2],
                     o.data_ptr(), os_[0], os_[1], os_[2],
                     lse.data_ptr() if lse is not None else None, torch_dtype_code(o.dtype),
-                    int(bool(k_transposed)))
+                    int(bool(k_transposed)), int(waves))
 
 
 def attn_fwd(q, k, v, o, *, causal=False, sm_scale=None, lse=None, stream=None,
-             k_transposed=False):
+             k_transposed=False, waves=0):
     """O = softmax(sm_scale . Q K^T [causal mask]) V on the GPU.  K is
     [batch, heads, seq_k, head_dim], or [batch, heads, head_dim, seq_k] with
-    k_transposed=True (read in place)."""
-    d = attn_desc(q, k, v, o, causal=causal, sm_scale=sm_scale, lse=lse, k_transposed=k_transposed)
+    k_transposed=True (read in place).  `waves` (4 or 8) requests the
+    workgroup shape; 0 lets the library choose."""
+    d = attn_desc(q, k, v, o, causal=causal, sm_scale=sm_scale, lse=lse, k_transposed=k_transposed,
+                  waves=waves)
     _check(load().frisk_attn_fwd(ctypes.byref(d), ctypes.c_void_p(_stream_handle(stream))),
            "frisk_attn_fwd")
     return o

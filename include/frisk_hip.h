@@ -112,12 +112,17 @@ typedef struct frisk_gemm_desc {
    * the 256x256 kernel (four waves in a 2x2 grid); tile = 128: the 128x128
    * kernel with a wave_m x wave_n wave grid, one of 2x2, 4x1, 1x4 (256
    * threads) or 2x1, 1x2 (128 threads), 0x0 meaning 2x2.  A requested
-   * variant runs unsplit (the workspace is not used), and returns
+   * variant runs unsplit, or with slices > 1 in that many K slices (2x2
+   * grid, bf16/f16/f32, N % 4 == 0; placed on stage boundaries as the
+   * library's own split; it needs the workspace frisk_gemm_workspace_size
+   * reports for the request, and runs unsplit without it).  It returns
    * FRISK_EUNSUP when the descriptor does not meet the matrix-core
    * conditions below.  variant_flags must be 0.  This is how a tile
    * program's instruction contract (its #frisk.mma_contract: MFMA atom and
-   * wave grid of the workgroup tile) selects the kernel that executes it. */
+   * wave grid of the workgroup tile) and the launch contract layout
+   * inference gives a whole-matrix GEMM select the kernel that runs. */
   int32_t tile, wave_m, wave_n, variant_flags;
+  int32_t slices; /* K slices of a requested variant; 0 or 1: unsplit */
 } frisk_gemm_desc;
 
 int frisk_gemm(const frisk_gemm_desc* desc, void* stream);
@@ -163,7 +168,9 @@ int64_t frisk_gemm_workspace_size(const frisk_gemm_desc* desc);
  * "slices" (split-K), "slice_sum" ("none", "in_launch": summed by the GEMM
  * kernel itself, "second_launch": by a slice-sum kernel) and
  * "workspace_bytes".  desc->workspace_bytes is taken
- * as the workspace a call would pass; pointers are not read.  No
+ * as the workspace a call would pass; pointers are never read, but when all
+ * of a, b and c are given their alignment counts as in frisk_gemm (so a
+ * requested variant the tensors cannot run is refused here too).  No
  * counterpart in the reference, whose execution packet records the chosen
  * instruction contract instead (ExportExecution.cpp:46-295): this reports
  * the contract of the kernel the C-ABI selects, for layout checks and
@@ -203,6 +210,10 @@ typedef struct frisk_attn_desc {
   float* lse;
   int32_t o_dtype;      /* frisk_dtype: equal to dtype, or FRISK_F32 */
   int32_t k_transposed; /* 0: K [b, h, seq_k, head_dim]; 1: K [b, h, head_dim, seq_k] */
+  /* Waves per workgroup (32 queries each): 0, the library chooses (the
+   * launch contract layout inference gives an attention program); 4 or 8
+   * (8 needs head_dim 128).  The result bits do not depend on it. */
+  int32_t waves;
 } frisk_attn_desc;
 
 int frisk_attn_fwd(const frisk_attn_desc* desc, void* stream);

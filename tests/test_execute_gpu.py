@@ -124,7 +124,8 @@ def test_execute_reference_fp32_tile_program():
     from frisk_amd import executor
     s, _ = P.tiled_gemm(1024, 1024, 1024, BM=128, BN=128, BK=32, dtype="fp32", out="fp32")
     p = executor.plan(s.module, "matmul")
-    assert p.variant == (128, 2, 2) and p.layouts_match, (p.contract, p.mismatch)
+    # 64 tiles on 256 CUs: the launch contract splits K in 4 on that tile.
+    assert p.variant == (128, 2, 2, 4) and p.layouts_match, (p.contract, p.mismatch)
     assert "v_mfma_f32_32x32x2_f32" in p.contract
     rng = np.random.default_rng(1)
     a_np = rng.uniform(-1, 1, (1024, 1024)).astype(np.float32)
@@ -135,3 +136,49 @@ def test_execute_reference_fp32_tile_program():
     torch.cuda.synchronize()
     ref = G.gemm_fp64(a_np, b_np)
     assert G.row_scaled_error(c.cpu().numpy().astype(np.float64), ref) <= 1e-5
+
+
+def test_execute_falls_back_on_a_misaligned_view():
+    # A 128x128-tile program whose contract selects the 128x128 kernel,
+    # given an A that is a view at an odd element offset (2-byte aligned):
+    # the variant's matrix-core conditions fail on these tensors, so the
+    # library's own choice (the generic kernel) runs, the plan says why, and
+    # the result matches the oracle.
+    from frisk_amd import executor
+    M = N = K = 256
+    s, _ = P.tiled_gemm(M, N, K, BM=128, BN=128, BK=64, trans_b=True)
+    buf = randn((M * K + 1,), 31).to(torch.bfloat16)
+    a = buf[1:].view(M, K)
+    b = randn((N, K), 32).to(torch.bfloat16)
+    c = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device="cuda")
+    p = executor.plan(s.module, "matmul")
+    assert p.variant is not None and p.layouts_match
+    assert executor._checked_variant(p, a, b, c) is None
+    assert not p.layouts_match and "does not run on these tensors" in p.mismatch
+    with pytest.raises(ValueError, match="no kernel runs the contracts"):
+        F.execute(s.module, "matmul", [a, b, c], require_layout_match=True)
+    F.execute(s.module, "matmul", [a, b, c])
+    torch.cuda.synchronize()
+    assert G.row_scaled_error(decode(c), decode(a) @ decode(b).T) <= 1e-2
+
+
+@pytest.mark.parametrize("M,N,K,tb", [(4096, 4096, 4096, True), (1024, 4096, 4096, False),
+                                      (128, 4096, 4096, True), (16, 4096, 14336, True)])
+def test_execute_whole_gemm_runs_the_launch_contract(M, N, K, tb):
+    # Whole-matrix programs take the target's launch contract (tile, wave
+    # grid, K slices), request it through the C-ABI, and match the oracle.
+    from frisk_amd import executor
+    from frisk_amd import runtime as rt
+    s, _ = P.whole_gemm(M, N, K, dtype="bf16", out="bf16", trans_b=tb)
+    p = executor.plan(s.module, "gemm")
+    a = randn((M, K), 41).to(torch.bfloat16)
+    b = randn((N, K) if tb else (K, N), 42).to(torch.bfloat16)
+    c = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device="cuda")
+    if p.variant is not None:
+        req = rt.gemm_plan(a, b, c, trans_b=tb, variant=p.variant)
+        assert req["requested"] and req["slices"] == p.launch["slices"]
+    F.execute(s.module, "gemm", [a, b, c], require_layout_match=True)
+    torch.cuda.synchronize()
+    rows = np.arange(0, M, max(1, M // 32))
+    ref = decode(a)[rows] @ (decode(b).T if tb else decode(b))
+    assert G.row_scaled_error(decode(c)[rows], ref) <= 1e-2

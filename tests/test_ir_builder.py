@@ -617,15 +617,118 @@ def test_plan_recognises_tiled_gemm():
         p = plan(s.module, "matmul")
         assert key(p) == key(GemmPlan(0, 1, 2, ta, tb, True, 512, 256, 1024))
         # 128x128 tiles on 256 threads (the builder's Square policy): the
-        # 2x2 wave grid of the 128x128 kernel executes the tile's contract.
-        assert p.variant == (128, 2, 2) and p.layouts_match and p.mismatch == ""
+        # 2x2 wave grid of the 128x128 kernel executes the tile's contract,
+        # in the K slices the launch contract gives that tile and grid
+        # (8 tiles of 128x128 on 256 CUs: 2 slices).
+        assert p.launch["tile"] == [128, 128] and p.launch["wave_grid"] == [2, 2]
+        assert p.variant == (128, 2, 2, p.launch["slices"]) and p.launch["slices"] == 2
+        assert p.layouts_match and p.mismatch == ""
         assert 'wave_grid = [2, 2]' in p.contract and 'policy = "Square"' in p.contract
     s, _ = P.tiled_gemm(256, 256, 256, k_scale=32)
     assert plan(s.module, "matmul").k == 256
     s, _ = P.whole_gemm(64, 32, 16, clear=False)
     p = plan(s.module, "gemm")
     assert key(p) == key(GemmPlan(0, 1, 2, False, False, False, 64, 32, 16))
-    assert p.variant is None and not p.layouts_match and "whole-matrix" in p.mismatch
+    # A whole-matrix program takes the target's launch contract (here the
+    # 128x128 kernel: B is stored [K, N], which the small-M kernel does not
+    # read), and the solved contract of that workgroup tile selects the
+    # variant execute() requests.
+    assert p.launch["kernel"] == "gemm_128" and p.variant == (128, 2, 2) and p.layouts_match
+    s, _ = P.whole_gemm(16, 4096, 4096, trans_b=True)
+    p = plan(s.module, "gemm")
+    assert p.launch["kernel"] == "gemm_skinny" and p.variant is None and p.layouts_match
+    assert p.contract.startswith("#frisk.gemm_launch<{kernel = \"gemm_skinny\"")
+
+
+@pytest.mark.parametrize("m,n,k,dt,out,ta,tb", [
+    (4096, 4096, 4096, "bf16", "bf16", False, True), (4096, 4096, 4096, "bf16", "bf16", False, False),
+    (4096, 4096, 4096, "bf16", "bf16", True, True), (4096, 4096, 4096, "bf16", "bf16", True, False),
+    (4096, 4096, 4096, "fp16", "fp16", False, True), (4096, 8192, 8192, "e4m3fn", "bf16", False, True),
+    (4096, 4096, 4096, "int8", "int32", False, True), (1024, 1024, 1024, "fp32", "fp32", False, False),
+    (512, 512, 512, "fp32", "fp32", False, False)] + [
+    (m, n, k, "bf16", "bf16", False, True) for n, k in ((4096, 4096), (14336, 4096), (4096, 14336))
+    for m in (16, 128, 1024, 8192)])
+def test_whole_gemm_launch_contract_equals_the_library_plan(m, n, k, dt, out, ta, tb):
+    # Every bench GEMM (configs[1..3] and the fp32 rows), built as a
+    # whole-matrix program: the kernel, tile, wave grid, stage depth and K
+    # split of the target's launch contract equal what frisk_gemm_plan
+    # reports for the same call, and the instruction contract inference
+    # solves for that workgroup tile selects the same kernel variant.
+    import ctypes
+    from frisk_amd import runtime as rt
+    from frisk_amd.executor import plan
+    s, _ = P.whole_gemm(m, n, k, dtype=dt, out=out, trans_a=ta, trans_b=tb)
+    p = plan(s.module, "gemm")
+    codes = {"bf16": rt.BF16, "fp16": rt.F16, "fp32": rt.F32, "int8": rt.I8, "int32": rt.I32,
+             "e4m3fn": rt.E4M3}
+    d = rt.GemmDesc(m, n, k, int(ta), int(tb), codes[dt], codes[dt], codes[out], 1, 16,
+                    m if ta else k, 16, k if tb else n, 16, n, 1.0, 1.0, None, 0, 0, 0, 0, 0, 0)
+    d.workspace_bytes = rt.load().frisk_gemm_workspace_size(ctypes.byref(d))
+    lib = rt.plan_of(d)
+    L = p.launch
+    assert (L["kernel"], L["slices"], L["workspace_bytes"]) == \
+        (lib["kernel"], lib["slices"], lib["workspace_bytes"]), (L, lib)
+    assert L["tile"] == [lib["tile_m"], lib["tile_n"]] and L["wave_grid"] == lib["waves"]
+    assert L["slice_sum"] == lib["slice_sum"]
+    if lib["kernel"] in ("gemm_w4", "gemm_128"):
+        assert L["stage_bytes"] == lib["stage_bytes"]
+        # The kernel's LDS swizzles, and for a K-major operand the layout
+        # target's own storage proposal for its stage rows.
+        assert (L["lds_swizzle_a"], L["lds_swizzle_b"]) == (lib["lds_swizzle_a"], lib["lds_swizzle_b"])
+        assert p.swizzle_match is (True if (not ta or tb) else None)
+        assert p.variant[:3] == (lib["tile_m"], *lib["waves"]) and p.layouts_match, p.mismatch
+        # The solver's contract is the library kernel's contract.
+        from frisk_amd import variants
+        mine, theirs = variants.parse_contract(p.contract), variants.parse_contract(lib["mma_contract"])
+        assert variants.logical_grid(mine) == variants.logical_grid(theirs)
+        assert mine["atom"] == theirs["atom"]
+    # Requested explicitly, the solved variant makes the same launch.
+    if p.variant is not None:
+        d.tile, d.wave_m, d.wave_n = p.variant[:3]
+        d.slices = p.variant[3] if len(p.variant) > 3 else 0
+        d.workspace_bytes = rt.load().frisk_gemm_workspace_size(ctypes.byref(d))
+        req = rt.plan_of(d)
+        assert req["requested"] and (req["kernel"], req["slices"], req["stage_bytes"]) == \
+            (lib["kernel"], lib["slices"], lib["stage_bytes"]), (req, lib)
+
+
+@pytest.mark.parametrize("policy,grid", [("FullRow", (4, 1)), ("FullCol", (1, 4)),
+                                         ("Square", (2, 2))])
+def test_warp_policy_selects_the_wave_grid(policy, grid):
+    # The GEMM op's warp policy reaches the kernel: the solver binds the
+    # policy's wave grid for the 128x128 workgroup tile, and execute()
+    # requests that variant (the 4x1 / 1x4 grids run unsplit; the 2x2 grid
+    # takes the launch contract's K slices).
+    from frisk_amd.executor import plan
+    for whole in (False, True):
+        if whole:
+            s, _ = P.whole_gemm(1024, 4096, 4096, dtype="bf16", out="bf16", trans_b=True)
+            name = "gemm"
+        else:
+            s, _ = P.tiled_gemm(512, 256, 1024, BM=128, BN=128, BK=64)
+            name = "matmul"
+        gemms = []
+        s.module.walk(lambda op: gemms.append(op) if op.get_name() == "frisk.gemm" else None)
+        F.frisk.GemmOp.from_operation(gemms[0]).set_attr(
+            "policy", s.builder.get_gemm_warp_policy_attr(getattr(F.GemmWarpPolicy, policy)))
+        p = plan(s.module, name)
+        assert p.variant is not None and p.variant[:3] == (128, *grid), (whole, p.variant, p.mismatch)
+        assert p.layouts_match and f'policy = "{policy}"' in p.contract
+        if grid != (2, 2):
+            assert len(p.variant) == 3
+
+
+def test_attention_launch_contract():
+    # The target's attention launch contract: the waves per workgroup the
+    # library would choose (8 for C5, 4 for the reference's D64 lengths and
+    # below head_dim 128).
+    fr = F.frisk
+    assert fr.attention_launch_plan(128, 4096, 128, False)["waves"] == 8
+    assert fr.attention_launch_plan(128, 4096, 128, True)["waves"] == 8
+    assert fr.attention_launch_plan(64, 1025, 64, False)["waves"] == 4
+    assert fr.attention_launch_plan(16, 2048, 128, False)["waves"] == 4
+    with pytest.raises(ValueError, match="head_dim"):
+        fr.attention_launch_plan(1, 64, 96, False)
 
 
 @pytest.mark.parametrize("bm,threads,variant", [(256, 256, (256, 2, 2)), (128, 128, (128, 1, 2)),

@@ -318,11 +318,18 @@ def test_plan_packet_gemm_variant_from_contract(m, threads, variant):
     assert V.logical_grid(V.parse_contract(g["contract"])) == variant[1:]
 
 
-def test_execute_packet_refuses_a_contract_no_kernel_executes():
-    with pytest.raises(ValueError, match="allow_layout_mismatch"):
-        F.execute_packet(_packet(_gemm_module()), [None, None, None])
+def test_execute_packet_refuses_a_contract_no_kernel_executes_when_asked():
+    # execute_packet follows execute()'s rule: a packet whose contract no
+    # kernel executes runs the library's own kernel (reporting the
+    # mismatch), unless require_layout_match, which refuses before running.
+    with pytest.raises(ValueError, match="require_layout_match"):
+        F.execute_packet(_packet(_gemm_module()), [None, None, None], require_layout_match=True)
     with pytest.raises(ValueError, match="head_dim >= 32"):
-        F.execute_packet(_packet(_attention(64, 64, 16, 128, dtype="fp16")), [None] * 4)
+        F.execute_packet(_packet(_attention(64, 64, 16, 128, dtype="fp16")), [None] * 4,
+                         require_layout_match=True)
+    # The older spelling still refuses.
+    with pytest.raises(ValueError, match="require_layout_match"):
+        F.execute_packet(_packet(_gemm_module()), [None, None, None], allow_layout_mismatch=False)
 
 
 def test_variant_for_reasons():
