@@ -26,8 +26,10 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 from __future__ import annotations
 
 import argparse
+import hashlib
 import json
 import os
+import platform
 import sys
 import time
 from pathlib import Path
@@ -239,7 +241,6 @@ def launch_percentiles(torch, fn, n=50):
 def provenance(torch):
     """What was measured: hashes of the kernel sources and of the built
     library, the git commit recorded at build time, and the GPU."""
-    import hashlib
     from frisk_amd.build import source_digest
     lib = ROOT / "frisk_amd" / "libfrisk_hip.so"
     info = {}
@@ -380,7 +381,11 @@ def cpu_baseline(torch, min_seconds=10.0, max_passes=8):
     time (at most `max_passes`), on all CPU threads of this process.  `legs`:
     the same GEMM on one core (64 output rows), and the attention forward of
     configs[4] (b4 h32 s4096 d128) for 128 query rows of one head on all
-    threads and 16 rows on one core (4 * rows * s * d FLOPs: QK^T and PV)."""
+    threads and 16 rows on one core (4 * rows * s * d FLOPs: QK^T and PV).
+    `manifest` names the seed and shapes of every sample and carries a
+    SHA-256 over the sample inputs (as bf16 bytes) and the oracle's C
+    source, so two baselines can be checked to have timed the same work;
+    `cpu_model` is the host's CPU."""
     import numpy as np
     from oracle import native
     native.load()
@@ -388,8 +393,15 @@ def cpu_baseline(torch, min_seconds=10.0, max_passes=8):
     m, n, k, blk = 4096, 4096, 4096, 512
     g = torch.Generator()
     g.manual_seed(1)
-    a = torch.randn(m, k, generator=g).to(torch.bfloat16).double().numpy()
-    b = torch.randn(n, k, generator=g).to(torch.bfloat16).double().numpy()
+    digest = hashlib.sha256((ROOT / "oracle" / "oracle.c").read_bytes())
+
+    def sample(rows, cols):
+        t = torch.randn(rows, cols, generator=g).to(torch.bfloat16)
+        digest.update(t.view(torch.int16).numpy().tobytes())
+        return t.double().numpy()
+
+    a = sample(m, k)
+    b = sample(n, k)
     native.gemm_f64(a[:8], b, trans_b=True, threads=threads)  # warm up threads
 
     def gemm_pass():
@@ -408,9 +420,9 @@ def cpu_baseline(torch, min_seconds=10.0, max_passes=8):
         "value": round(2.0 * 64 * reps * n * k / dt / 1e12, 6), "unit": "TFLOP/s", "cores": 1,
         "kind": "port", "sample": f"{reps} x 64 output rows of the 4096^3 GEMM ({dt:.1f} s)"}
     s_len, d = 4096, 128
-    q = torch.randn(s_len, d, generator=g).to(torch.bfloat16).double().numpy()
-    kk = torch.randn(s_len, d, generator=g).to(torch.bfloat16).double().numpy()
-    v = torch.randn(s_len, d, generator=g).to(torch.bfloat16).double().numpy()
+    q = sample(s_len, d)
+    kk = sample(s_len, d)
+    v = sample(s_len, d)
     for name, nrows, nthreads, secs in (("fa_fwd_b4h32s4096d128", 128, threads, 4.0),
                                         ("fa_fwd_b4h32s4096d128_single_core", 16, 1, 2.0)):
         rows_idx = np.arange(0, s_len, s_len // nrows, dtype=np.int64)[:nrows]
@@ -421,7 +433,23 @@ def cpu_baseline(torch, min_seconds=10.0, max_passes=8):
                       "sample": f"{reps} x {nrows} query rows of one head, s=4096 d=128, "
                                 f"non-causal (fp64 oracle_attn_rows_f64, {dt:.1f} s)"}
     out["legs"] = legs
+    out["cpu_model"] = _cpu_model()
+    out["manifest"] = {
+        "seed": 1, "draws": "torch.randn (CPU generator) in order A[4096,4096], B[4096,4096], "
+                            "Q[4096,128], K[4096,128], V[4096,128], each rounded to bf16",
+        "gemm": [m, n, k], "attn": [s_len, d], "oracle": "oracle/oracle.c",
+        "sha256_16": digest.hexdigest()[:16]}
     return out
+
+
+def _cpu_model():
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or None
 
 
 def traffic_from_profile(name):

@@ -85,7 +85,7 @@ typedef enum frisk_dtype {
  * and must be 1.0 for every other type.
  *
  * workspace / workspace_bytes: optional device scratch (16-byte aligned)
- * owned by the caller.  A small-M bf16/f16 GEMM given at least
+ * owned by the caller.  A small-M bf16/f16/f32 GEMM given at least
  * frisk_gemm_workspace_size() bytes splits K over the whole GPU (f32
  * partial tiles, added in a fixed order, so the result does not depend on
  * timing); without it, or when the size is 0, the unsplit kernels run.
