@@ -112,23 +112,27 @@ __global__ __launch_bounds__(g4::kThreads) void gemm_w4_kernel(
   }
   TA::dma_adv(da, lda_b);
   TB::dma_adv(db, ldb_b);
-  // With four or more k-steps per stage the stage base goes in the scalar
-  // offset of each load, beside stage-invariant lane offsets: every stage
-  // before nk_full holds KR whole bytes of K, so a lane live in the last of
-  // them is live in all; the partial stage nk_full (when KR does not divide
-  // K) keeps only its live chunks; stages past the last read through a
-  // zero-length range.  One VALU select per load instead of an add, a
-  // compare and a select (bf16 4096^3 +0.7%, int8 +0.6%; with two k-steps,
-  // fp8 4096x8192x8192, -1.3%, so those keep the per-lane offsets).
+  // Every stage before nk_full holds KR whole bytes of K, so a lane live in
+  // the last of them is live in all: a_full / b_full are the stage-invariant
+  // lane offsets of those stages, and the stage base goes in the scalar
+  // offset.  The steady-state iterations (below) issue exactly that, with no
+  // VALU work (bf16 4096^3 +1.1-2.1%, 8192^3 +1.7-2.4%, int8 +0.6-0.9%, fp8
+  // within noise).  The other iterations: with four or more k-steps per
+  // stage, one VALU select per load between a_full and a_tail (the partial
+  // stage nk_full, when KR does not divide K, keeps only its live chunks)
+  // and a zero-length range past the last stage; with two k-steps (fp8),
+  // per-lane offsets (the select form measured 1.3% slower there).
   constexpr bool kScalarStage = kSteps >= 4;
   const int nk_full = Kb / KR;
   uint32_t a_full[kBlocks], a_tail[kBlocks], b_full[kBlocks], b_tail[kBlocks];
 #pragma unroll
   for (int i = 0; i < kBlocks; ++i) {
     a_full[i] = (nk_full - 1) * TA::kStep < da.lim[i] ? da.off[i] : 0x80000000u;
-    a_tail[i] = nk_full * TA::kStep < da.lim[i] ? da.off[i] : 0x80000000u;
     b_full[i] = (nk_full - 1) * TB::kStep < db.lim[i] ? db.off[i] : 0x80000000u;
-    b_tail[i] = nk_full * TB::kStep < db.lim[i] ? db.off[i] : 0x80000000u;
+    if constexpr (kScalarStage) {
+      a_tail[i] = nk_full * TA::kStep < da.lim[i] ? da.off[i] : 0x80000000u;
+      b_tail[i] = nk_full * TB::kStep < db.lim[i] ? db.off[i] : 0x80000000u;
+    }
   }
   const __amdgpu_buffer_rsrc_t rsa_none = __builtin_amdgcn_make_buffer_rsrc(
       (void*)TA::origin(A, row0, lda_b), (short)0, 0, 0x00020000);
@@ -154,12 +158,23 @@ __global__ __launch_bounds__(g4::kThreads) void gemm_w4_kernel(
   constexpr int kBParts = kSteps >= 2 ? kSteps / 2 : 1;
   constexpr int kAParts = kSteps >= 2 ? kSteps - kBParts : 1;
   static_assert(kBlocks >= kBParts && kBlocks >= kAParts, "DMA parts");
-  auto issue = [&](auto op, int stage, int slot, auto part, auto parts) {
+  // `fast`: the steady state, where the stage is a whole one inside K (no
+  // partial stage exists and the stage is not past the last): every lane's
+  // offset is its stage-invariant one and the stage base is the scalar
+  // offset, so a load is issued with no VALU work at all.
+  auto issue = [&](auto op, int stage, int slot, auto part, auto parts, auto fast) {
     constexpr int p = decltype(part)::value, np = decltype(parts)::value;
     constexpr bool is_a = decltype(op)::value;
     const int phys = phys_of(stage);
     char* dst = smem + slot * kTileBytes + wave * kBlocks * 1024;
-    if constexpr (kScalarStage) {
+    if constexpr (decltype(fast)::value) {
+      const uint32_t soff = (uint32_t)phys * (is_a ? da.adv : db.adv);
+#pragma unroll
+      for (int i = p * kBlocks / np; i < (p + 1) * kBlocks / np; ++i)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(is_a ? rsa : rsb, (lds_ptr_t)(dst + i * 1024), 16,
+                                                 is_a ? a_full[i] : b_full[i],
+                                                 __builtin_amdgcn_readfirstlane(soff), 0, 0);
+    } else if constexpr (kScalarStage) {
       const bool past = phys >= nk_all, tail = phys == nk_full;
       const uint32_t soff = past ? 0u : (uint32_t)phys * (is_a ? da.adv : db.adv);
       const __amdgpu_buffer_rsrc_t rs = is_a ? (past ? rsa_none : rsa) : (past ? rsb_none : rsb);
@@ -239,9 +254,10 @@ __global__ __launch_bounds__(g4::kThreads) void gemm_w4_kernel(
   // Measured against two 64 KiB stages written whole per iteration
   // (4096^3 bf16 / 4096x8192x8192 fp8 / 8192^3 bf16): +2% / +7% / +4%.
   const int nk = (Kb + KR - 1) / KR;
-  static_for<0, kAParts>([&](auto p) { issue(OpA{}, 0, 0, p, std::integral_constant<int, kAParts>{}); });
-  static_for<0, kBParts>([&](auto p) { issue(OpB{}, 0, 1, p, std::integral_constant<int, kBParts>{}); });
-  static_for<0, kAParts>([&](auto p) { issue(OpA{}, 1, 2, p, std::integral_constant<int, kAParts>{}); });
+  using Slow = std::false_type;
+  static_for<0, kAParts>([&](auto p) { issue(OpA{}, 0, 0, p, std::integral_constant<int, kAParts>{}, Slow{}); });
+  static_for<0, kBParts>([&](auto p) { issue(OpB{}, 0, 1, p, std::integral_constant<int, kBParts>{}, Slow{}); });
+  static_for<0, kAParts>([&](auto p) { issue(OpA{}, 1, 2, p, std::integral_constant<int, kAParts>{}, Slow{}); });
   FRISK_WAIT_VMCNT(kBlocks);
   __builtin_amdgcn_s_barrier();
 
@@ -256,21 +272,23 @@ __global__ __launch_bounds__(g4::kThreads) void gemm_w4_kernel(
   auto adv = [](int x) { return x >= 3 ? x - 3 : x + 2; };  // (x + 2) mod 5
   constexpr int kMf = TM * TN;
   constexpr int kHalf = kMf / 2;
-  for (int kt = 0; kt < nk; ++kt) {
+  auto iteration = [&](int kt, auto fast) {
     static_for<0, kSteps>([&](auto step) {
       constexpr int s = decltype(step)::value;
       constexpr int cur = s & 1, nxt = cur ^ 1;
       constexpr int nload = step_loads(s);
       auto issue_step = [&]() {
         if constexpr (kSteps == 1) {
-          issue(OpB{}, kt + 1, b_wr, std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{});
-          issue(OpA{}, kt + 2, a_wr, std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{});
+          issue(OpB{}, kt + 1, b_wr, std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{},
+                fast);
+          issue(OpA{}, kt + 2, a_wr, std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{},
+                fast);
         } else if constexpr (s < kBParts) {
           issue(OpB{}, kt + 1, b_wr, std::integral_constant<int, s>{},
-                std::integral_constant<int, kBParts>{});
+                std::integral_constant<int, kBParts>{}, fast);
         } else {
           issue(OpA{}, kt + 2, a_wr, std::integral_constant<int, s - kBParts>{},
-                std::integral_constant<int, kAParts>{});
+                std::integral_constant<int, kAParts>{}, fast);
         }
       };
       if constexpr (s + 1 < kSteps) {
@@ -321,7 +339,14 @@ __global__ __launch_bounds__(g4::kThreads) void gemm_w4_kernel(
       }
     });
     if constexpr (kSteps == 1) fr[0] = fr[1];
-  }
+  };
+  // Iterations whose loads (stages kt + 1 and kt + 2) are whole stages
+  // inside K take the fast issue; the last two, and every iteration when K
+  // ends in a partial stage, take the general one.
+  const int nk_fast = Kb % KR == 0 ? max(nk - 2, 0) : 0;
+  int kt = 0;
+  for (; kt < nk_fast; ++kt) iteration(kt, std::true_type{});
+  for (; kt < nk; ++kt) iteration(kt, Slow{});
   // Drain the trailing DMA loads before the stage buffers are reused.
   FRISK_WAIT_VMCNT(0);
   __syncthreads();
