@@ -276,7 +276,7 @@ const char* mfma_atom(frisk::Elt in) {
   switch (in) {
     case frisk::Elt::BF16: return "v_mfma_f32_32x32x16_bf16";
     case frisk::Elt::F16: return "v_mfma_f32_32x32x16_f16";
-    case frisk::Elt::E4M3: return "v_mfma_scale_f32_32x32x64_f8f6f4";
+    case frisk::Elt::E4M3: return "v_mfma_f32_32x32x64_f8f6f4";
     case frisk::Elt::I8: return "v_mfma_i32_32x32x32_i8";
     case frisk::Elt::F32: return "v_mfma_f32_32x32x2_f32";
     default: return "";

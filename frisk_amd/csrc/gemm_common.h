@@ -34,14 +34,22 @@ template <> struct Mfma32<Elt::F16> {
   }
 };
 
+#ifndef FRISK_F8_SCALE
+#define FRISK_F8_SCALE 0
+#endif
 template <> struct Mfma32<Elt::E4M3> {
   static constexpr int kBytes = 64;
   using Acc = f32x16;
   __device__ static inline Acc run(const i32x4* a, const i32x4* b, Acc c) {
     const i32x8 av = {a[0][0], a[0][1], a[0][2], a[0][3], a[1][0], a[1][1], a[1][2], a[1][3]};
     const i32x8 bv = {b[0][0], b[0][1], b[0][2], b[0][3], b[1][0], b[1][1], b[1][2], b[1][3]};
-    // Format 0 = fp8 e4m3 for both operands; E8M0 block scales 127 = 2^0.
-    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, bv, c, 0, 0, 0, 127, 0, 127);
+    // Format 0 = fp8 e4m3 for both operands.  Scale operands 0 select the
+    // form without block scales (v_mfma_f32_32x32x64_f8f6f4: 8 bytes of
+    // code instead of 16 and no scale register read per MFMA), whose
+    // products are the unscaled ones that unit E8M0 scales (127 = 2^0)
+    // give; the parity tests hold the products to the oracle.
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, bv, c, 0, 0, 0, FRISK_F8_SCALE, 0,
+                                                           FRISK_F8_SCALE);
   }
 };
 
@@ -100,8 +108,9 @@ template <> struct Mfma16x<Elt::E4M3> {
   __device__ static inline Acc run(const i32x4* a, const i32x4* b, Acc c) {
     const i32x8 av = {a[0][0], a[0][1], a[0][2], a[0][3], a[1][0], a[1][1], a[1][2], a[1][3]};
     const i32x8 bv = {b[0][0], b[0][1], b[0][2], b[0][3], b[1][0], b[1][1], b[1][2], b[1][3]};
-    // Format 0 = fp8 e4m3 for both operands; E8M0 block scales 127 = 2^0.
-    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, c, 0, 0, 0, 127, 0, 127);
+    // Format 0 = fp8 e4m3 for both operands, no block scales (as above).
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, c, 0, 0, 0, FRISK_F8_SCALE, 0,
+                                                            FRISK_F8_SCALE);
   }
 };
 

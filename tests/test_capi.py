@@ -334,7 +334,7 @@ def test_gemm_plan_every_layout_runs_on_the_matrix_cores():
             assert p["lds_read_a"] == ("ds_read_b64_tr_b16" if ta else "ds_read_b128")
             assert p["lds_read_b"] == ("ds_read_b128" if tb else "ds_read_b64_tr_b16")
     p = plan(trans_b=0, a_type=rt.E4M3, b_type=rt.E4M3, c_type=rt.BF16)
-    assert p["atom"] == "v_mfma_scale_f32_32x32x64_f8f6f4" and p["lds_read_b"] == "ds_read_b64_tr_b8"
+    assert p["atom"] == "v_mfma_f32_32x32x64_f8f6f4" and p["lds_read_b"] == "ds_read_b64_tr_b8"
     p = plan(trans_a=1, a_type=rt.I8, b_type=rt.I8, c_type=rt.I32)
     assert p["atom"] == "v_mfma_i32_32x32x32_i8" and p["lds_read_a"] == "ds_read_b64_tr_b8"
     # Fewer than 128 256x256 tiles: 128x128 tiles, in every layout.
