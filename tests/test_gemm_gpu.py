@@ -105,7 +105,9 @@ def test_accumulate_into_c(in_dt, out_dt):
 
 
 SKINNY = [(1, 64, 64), (16, 16, 8), (17, 40, 72), (48, 24, 200), (64, 4096, 512), (100, 136, 1000),
-          (128, 256, 64), (128, 8200, 96)]
+          (128, 256, 64), (128, 8200, 96),
+          # single 16x16 tiles, 8 k-steps per load batch: whole batches and a K tail
+          (16, 4096, 4096), (5, 40, 2056)]
 
 
 @pytest.mark.parametrize("in_dt,out_dt", [(torch.bfloat16, torch.bfloat16),
