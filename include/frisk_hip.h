@@ -147,7 +147,8 @@ int frisk_gemm(const frisk_gemm_desc* desc, void* stream);
  * Calls on one GPU share that array: calls that overlap in time on one GPU
  * (different streams, or host threads) race on it and must be serialised by
  * the caller; calls ordered on one stream are safe.  The first call on a
- * device looks the array up there (hipGetSymbolAddress). */
+ * device looks the array up there (hipGetSymbolAddress): make it outside
+ * graph capture (one warm-up call), then capture freely. */
 #define FRISK_GEMM_NOALLOC_SCRATCH_BYTES (64ll << 20)
 int frisk_gemm_noalloc(const frisk_gemm_desc* desc, void* stream);
 
