@@ -304,6 +304,7 @@ def projection_sweep(torch, rt, steps, warmup, settle_s):
             tf, gbs = flops / ms / 1e9, nbytes / ms / 1e6
             bound = "hbm" if flops / nbytes < ridge else "mfma"
             frac = gbs / HBM_PEAK_GBS if bound == "hbm" else tf / PEAK["bf16"]
+            print(f"bench: projection m{m} n{n} k{k} {ms * 1e3:.2f} us", file=sys.stderr, flush=True)
             out[f"m{m}_n{n}_k{k}"] = {"us": round(ms * 1e3, 2), "tflops": round(tf, 1),
                                        "gbs": round(gbs, 1), "bound": bound,
                                        "frac": round(frac, 4), "split_k": need > 0,
@@ -467,27 +468,47 @@ def traffic_from_profile(name):
     return None
 
 
+def _kernel_short(name):
+    """A kernel's name without its parameter list, `void` and namespace, and
+    with the enum casts of its template arguments dropped."""
+    cut = name.find(">(")
+    base = name[:cut + 1] if cut >= 0 else name.split("(")[0]
+    return base.replace("void ", "").replace("frisk::", "").replace("(Elt)", "").strip()
+
+
 def trace_summary(path, steps):
-    """Per-kernel durations from a rocprofv3 kernel-trace CSV (`-f csv`) of
-    a `--only` run: dispatch count, average over every dispatch (settle and
+    """Per-kernel durations from a rocprofv3 kernel trace, its CSV (`-f csv`)
+    or its results database (`*_results.db`, the default format): dispatch
+    count, average, minimum and maximum over every dispatch (settle and
     warm-up included) and over the last `steps` dispatches of that kernel
-    and grid, which are the timed launches.  Returns a list of dicts."""
-    import csv
+    and grid, which in a `--only` run are the timed launches.  Returns a list
+    of dicts, the longest kernels first."""
     rows = {}
-    with open(path, newline="") as f:
-        for r in csv.DictReader(f):
-            grid = tuple(int(r[f"Grid_Size_{a}"]) // max(1, int(r[f"Workgroup_Size_{a}"]))
-                         for a in "XYZ")
-            key = (r["Kernel_Name"], grid)
-            rows.setdefault(key, []).append(
-                (int(r["Start_Timestamp"]), (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3))
+    if str(path).endswith(".db"):
+        import sqlite3
+        con = sqlite3.connect(path)
+        for name, start, end, gx, gy, gz, wx, wy, wz in con.execute(
+                "select name, start, end, grid_x, grid_y, grid_z, workgroup_x, workgroup_y, "
+                "workgroup_z from kernels"):
+            grid = (gx // max(1, wx), gy // max(1, wy), gz // max(1, wz))
+            rows.setdefault((name, grid), []).append((int(start), (int(end) - int(start)) / 1e3))
+    else:
+        import csv
+        with open(path, newline="") as f:
+            for r in csv.DictReader(f):
+                grid = tuple(int(r[f"Grid_Size_{a}"]) // max(1, int(r[f"Workgroup_Size_{a}"]))
+                             for a in "XYZ")
+                key = (r["Kernel_Name"], grid)
+                rows.setdefault(key, []).append(
+                    (int(r["Start_Timestamp"]), (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3))
     out = []
     for (name, grid), d in rows.items():
         d.sort()
         us = [x[1] for x in d]
         last = us[-steps:]
-        out.append({"kernel": name.split("(")[0].strip(), "grid": grid, "calls": len(us),
-                    "avg_us": sum(us) / len(us), "timed_calls": len(last),
+        out.append({"kernel": _kernel_short(name), "grid": grid, "calls": len(us),
+                    "avg_us": sum(us) / len(us), "min_us": min(us), "max_us": max(us),
+                    "timed_calls": len(last),
                     "timed_avg_us": sum(last) / len(last), "timed_min_us": min(last),
                     "timed_max_us": max(last),
                     "timed_span_us": (d[-1][0] - d[-len(last)][0]) / 1e3 + d[-1][1]})
@@ -551,6 +572,7 @@ def main():
                              "frac_peak_at_sclk": round(tf / (PEAK[label] * mhz / PEAK_MHZ), 4) if mhz else None,
                              "launch_ms": launch_percentiles(torch, fn),
                              "traffic": traffic_from_profile(name)}
+        print(f"bench: {name} {ms * 1e3:.2f} us", file=sys.stderr, flush=True)
         del fn
         torch.cuda.empty_cache()
 
@@ -584,6 +606,7 @@ def main():
         "fixed_tile_64x16": fixed_tile_latency(torch, rt),
     }
     if not args.no_cpu:
+        print("bench: cpu baseline", file=sys.stderr, flush=True)
         line["cpu_baseline"] = cpu_baseline(torch)
     print(json.dumps(line), flush=True)
 
