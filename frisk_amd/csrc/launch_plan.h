@@ -278,6 +278,17 @@ inline SkinnyPlan skinny_plan(const GemmShape& g, int cus, bool split) {
     p.tn = tn;
     return p;
   }
+  // One 16-row block whose unsplit tiles (16 or 32 columns) fill the CUs in
+  // whole rounds, with at most 128 MiB of W: no partials and no second
+  // launch.  Operands from HBM, us, split -> unsplit: 16x4096x14336 30.8 ->
+  // 29.4, 8x4096x14336 29.6 -> 25.0, 1x4096x14336 28.3 -> 22.6, 16x4096x8192
+  // 19.7 -> 17.5, 16x8192x8192 31.2 -> 29.3; with more W the split stays
+  // ahead (16x8192x14336 53.0 against 54.7, 16x4096x28672 54.9 against
+  // 56.0), and so it does when the tiles leave a partial round (16x5120x14336
+  // 49.4 against 53.4, 16x2048x16384 20.7 against 31.0).
+  if (p.tm == 1 && cus > 0 && g.n * kb <= ((int64_t)128 << 20) &&
+      ((g.n + 16 * p.tn - 1) / (16 * p.tn)) % cus == 0)
+    return p;
   const int64_t min_steps = 4 * (p.tm + tn <= 10 ? 4 : 2);
   int64_t slices = ((int64_t)cus + tiles - 1) / tiles;
   slices = std::min<int64_t>(slices, steps / min_steps);

@@ -280,14 +280,20 @@ def test_gemm_workspace_size_query():
     assert gemm_size(m=1024, k=14336, lda=14336, ldb=14336) == 4 * 1024 * 4096 * 4
     # 1024 x 4096 x 4096: 256 128x128 tiles already fill the CUs; no split.
     assert gemm_size(m=1024) == 0
-    # 16 x 4096 x 14336 on the small-M kernel: 64-column tiles -> 64 tiles,
-    # 4 slices (one workgroup per CU).
-    assert gemm_size(m=16, k=14336, lda=14336, ldb=14336) == 4 * 16 * 4096 * 4
+    # 16 x 2048 x 16384 on the small-M kernel: 64-column tiles -> 32 tiles,
+    # 8 slices (one workgroup per CU).
+    assert gemm_size(m=16, n=2048, k=16384, lda=16384, ldb=16384, ldc=2048) == 8 * 16 * 2048 * 4
+    # 16 x 4096 x 14336: 256 unsplit 16-column tiles fill the CUs in one
+    # round, so it does not split; 16 x 5120 x 14336 (320 tiles) does.
+    assert gemm_size(m=16, k=14336, lda=14336, ldb=14336) == 0
+    assert gemm_size(m=16, n=5120, k=14336, lda=14336, ldb=14336, ldc=5120) == 4 * 16 * 5120 * 4
     # 16 x 14336 x 4096: 224 tiles fill 7/8 of 256 CUs in one round, no split
-    # (also at M = 64); 16 x 8192 x 8192: 128 tiles, 2 slices.
+    # (also at M = 64); 16 x 8192 x 8192: 256 unsplit 32-column tiles, no
+    # split; M = 32 there: 128 tiles, 2 slices.
     assert gemm_size(m=16, n=14336, ldc=14336) == 0
     assert gemm_size(m=64, n=14336, ldc=14336) == 0
-    assert gemm_size(m=16, n=8192, k=8192, lda=8192, ldb=8192, ldc=8192) == 2 * 16 * 8192 * 4
+    assert gemm_size(m=16, n=8192, k=8192, lda=8192, ldb=8192, ldc=8192) == 0
+    assert gemm_size(m=32, n=8192, k=8192, lda=8192, ldb=8192, ldc=8192) == 2 * 32 * 8192 * 4
     # 16 x 4096 x 4096: W below 64 MiB, no split.
     assert gemm_size(m=16) == 0
     # No split: grids of at least CUs / 2 256x256 tiles, K too short to

@@ -233,8 +233,9 @@ def run_sampled(m, n, k, in_dt, out_dt, seed, rows=48, std_a=1.0, std_b=1.0):
 # Small-M kernel split (M <= 64 with >= 64 MiB of W), 128x128-tile split
 # (64 < M <= 128, few tiles) and 256x256-tile split (larger M), with ragged
 # M, N and K tails.
-SPLIT_SHAPES = [(128, 4096, 4096), (16, 4096, 14336), (100, 1000, 3000), (48, 2600, 16384),
-                (1, 4096, 8192), (256, 520, 8192), (300, 1000, 6144), (768, 2048, 4096)]
+SPLIT_SHAPES = [(128, 4096, 4096), (16, 2048, 16384), (100, 1000, 3000), (48, 2600, 16384),
+                (1, 2048, 16384), (16, 5120, 14336), (256, 520, 8192), (300, 1000, 6144),
+                (768, 2048, 4096)]
 
 
 @pytest.mark.parametrize("m,n,k", SPLIT_SHAPES)

@@ -21,7 +21,7 @@ pytestmark = pytest.mark.gpu
 CASES = [(1024, 4096, 14336, False, True, "gemm_w4", 4),
          (128, 4096, 4096, False, False, "gemm_128", 8),
          (128, 14336, 4096, True, True, "gemm_128", 2),
-         (16, 4096, 14336, False, True, "gemm_skinny", 4),
+         (16, 2048, 16384, False, True, "gemm_skinny", 8),
          (1024, 1024, 1024, True, False, None, 1)]
 
 
