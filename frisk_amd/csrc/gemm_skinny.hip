@@ -64,7 +64,8 @@ constexpr int kSkinnyWaves = 4;
 // (U (TM + TN) 4 VGPRs beside the TM TN 4 accumulator VGPRs).
 // A single 16 x 16 tile per workgroup loads 8 k-steps ahead: its 128 KiB
 // of W at N = K = 4096 are then half in flight at once (16 x 4096 x 4096,
-// operands from HBM: 11.4 -> 10.5 us; the wider tiles measured no change).
+// operands from HBM: 11.4 -> 10.5 us; 12 or 16 k-steps ran 4% and 13% slower,
+// and the wider tiles measured no change with 8).
 template <int TM, int TN> constexpr int skinny_unroll() {
   return TM + TN <= 2 ? 8 : TM + TN <= 10 ? 4 : 2;
 }
