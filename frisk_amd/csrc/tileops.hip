@@ -261,13 +261,23 @@ __global__ __launch_bounds__(kColThreads) void reduce_cols_kernel(
   for (int j = 0; j < 4; ++j)
     part[(g * cvb + cs) * 4 + j] = n8 ? ctr[j].finish(n8) : identity<KIND>();
   __syncthreads();
+  // The pairwise tree over the row groups, one level at a time across the
+  // workgroup: at level w group g (a multiple of 2w) takes in group g + w.
+  // The same combines as a serial walk, so the same bits; serially, one
+  // group's threads spent about 60 us on 128 groups' chains of dependent
+  // LDS accesses (33 x 777 f16).
+  for (int w = 1; w < groups; w <<= 1) {
+    if ((g & (2 * w - 1)) == 0) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        part[(g * cvb + cs) * 4 + j] = combine<E, KIND>(part[(g * cvb + cs) * 4 + j],
+                                                        part[((g + w) * cvb + cs) * 4 + j]);
+    }
+    __syncthreads();
+  }
   if (g == 0) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      for (int w = 1; w < groups; w <<= 1)
-        for (int i = 0; i < groups; i += 2 * w)
-          part[(i * cvb + cs) * 4 + j] = combine<E, KIND>(part[(i * cvb + cs) * 4 + j],
-                                                          part[((i + w) * cvb + cs) * 4 + j]);
       const int64_t c = c0 + j;
       if (c < cols) {
         float res = part[cs * 4 + j];
@@ -355,15 +365,21 @@ __global__ __launch_bounds__(tile::kThreads) void reduce_cols_blocks_kernel(
 #pragma unroll
   for (int j = 0; j < 4; ++j) part[(g * sps + cs) * 4 + j] = n8 ? ctr[j].finish(n8) : identity<KIND>();
   __syncthreads();
+  // The pairwise tree over the row groups, a level at a time (as in
+  // reduce_cols_kernel).
+  for (int w = 1; w < groups; w <<= 1) {
+    if ((g & (2 * w - 1)) == 0) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        part[(g * sps + cs) * 4 + j] =
+            combine<E, KIND>(part[(g * sps + cs) * 4 + j], part[((g + w) * sps + cs) * 4 + j]);
+    }
+    __syncthreads();
+  }
   if (g == 0) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      for (int w = 1; w < groups; w <<= 1)
-        for (int i = 0; i < groups; i += 2 * w)
-          part[(i * sps + cs) * 4 + j] =
-              combine<E, KIND>(part[(i * sps + cs) * 4 + j], part[((i + w) * sps + cs) * 4 + j]);
+    for (int j = 0; j < 4; ++j)
       if (c0 + j < cols) partial[(int64_t)blockIdx.y * cols + c0 + j] = part[cs * 4 + j];
-    }
   }
 }
 
