@@ -52,6 +52,90 @@ constexpr int lds_bytes(int kr) { return kRing * kBT * kr; }
 
 }  // namespace g4
 
+// Epilogue of 16-bit outputs, one pass: each wave rounds its 128x128
+// sub-tile (32x32 atoms) to OUT in registers and stages it in its own
+// 32 KiB of LDS, then stores whole 256-byte row pieces.  Accumulator
+// elements 8p .. 8p+7 of lane L hold columns 16p + 4h .. +3 and
+// 16p + 8 + 4h .. +3 (h = L / 32) of row L % 32; one v_permlane32_swap per
+// packed pair hands lane L the 8 consecutive columns 16p + 8h .. +7, so each
+// lane writes one 16-byte chunk per atom and p.  Staged row R keeps chunk c
+// at c ^ (R & 15): the 16 lanes of a write (16 rows, one chunk) and of a
+// read (one row, 16 chunks) touch every bank once.  Each output is
+// acc * scale (+ C when accumulating, read as f32 before the rounding),
+// rounded once to nearest even, as in the f32-staged path; each wave reads
+// back only what it wrote, so no workgroup barrier is needed.
+template <Elt OUT, bool ACCUMULATE, int TM, int TN>
+__device__ __forceinline__ void epilogue16(const f32x16 (&acc)[TM][TN], float scale, int lane, char* stage, int r0, int c0,
+                                           int M, int N, int64_t ldc, void* C) {
+  constexpr int kPitch = 256;
+  auto at = [](int R, int c) { return R * kPitch + ((c ^ (R & 15)) << 4); };
+  const int half = lane >> 5;
+  // C[r0 + R][c0 + c .. c + 3] as f32 (0 outside the matrix).
+  auto old4 = [&](int R, int c, float* o) {
+    const int gr = r0 + R, gc = c0 + c;
+    const uint16_t* src = (const uint16_t*)C + (int64_t)gr * ldc + gc;
+    i32x2 w = {0, 0};
+    if (gr < M && gc + 4 <= N) {
+      w = *(const i32x2*)src;
+    } else if (gr < M) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        if (gc + k < N) w[k >> 1] |= (int)((uint32_t)src[k] << (16 * (k & 1)));
+    }
+    const uint16_t* e = (const uint16_t*)&w;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) o[k] += load_as_f32<OUT>(e, k);
+  };
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+      static_for<0, 2>([&](auto pc) {
+        constexpr int p = decltype(pc)::value;
+        // Read from the AGPRs one element at a time: used by VALU code
+        // directly, the compiler copies all 256 accumulators to VGPRs at
+        // once and spills.
+        float f[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(f[k]) : "a"(acc[i][j][8 * p + k]));
+          f[k] *= scale;
+        }
+        const int R = i * 32 + (lane & 31);
+        if constexpr (ACCUMULATE) {
+          old4(R, j * 32 + 16 * p + 4 * half, f);
+          old4(R, j * 32 + 16 * p + 8 + 4 * half, f + 4);
+        }
+        const uint32_t x0 = pack_f32x2<OUT>(f[0], f[1]), x1 = pack_f32x2<OUT>(f[2], f[3]);
+        const uint32_t y0 = pack_f32x2<OUT>(f[4], f[5]), y1 = pack_f32x2<OUT>(f[6], f[7]);
+        // Lanes 0-31 keep x and take the partner's x; lanes 32-63 take the
+        // partner's y and keep y.
+        const auto s0 = __builtin_amdgcn_permlane32_swap(x0, y0, false, false);
+        const auto s1 = __builtin_amdgcn_permlane32_swap(x1, y1, false, false);
+        const i32x4 w = {(int)s0[0], (int)s1[0], (int)s0[1], (int)s1[1]};
+        *(i32x4*)(stage + at(R, 4 * j + 2 * p + half)) = w;
+        // One atom's conversions at a time.
+        __builtin_amdgcn_sched_barrier(0);
+      });
+#pragma unroll
+  for (int it = 0; it < TM * 32 * 16 / 64; ++it) {
+    if (it % 8 == 0) __builtin_amdgcn_sched_barrier(0);
+    const int q = it * 64 + lane, rr = q >> 4, g = q & 15;
+    const i32x4 v = *(const i32x4*)(stage + at(rr, g));
+    const int gr = r0 + rr, gc = c0 + 8 * g;
+    if (gr < M && gc < N) {
+      uint16_t* dst = (uint16_t*)C + (int64_t)gr * ldc + gc;
+      if (gc + 8 <= N) {
+        __builtin_nontemporal_store(v, (i32x4*)dst);
+      } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+          if (gc + k < N) dst[k] = (uint16_t)((uint32_t)v[k >> 1] >> (16 * (k & 1)));
+      }
+    }
+  }
+}
+
 template <Elt IN, Elt OUT, bool AM, bool BM, int KR, int ATOM>
 __global__ __launch_bounds__(g4::kThreads) void gemm_w4_kernel(
     const char* __restrict__ A, const char* __restrict__ B, void* __restrict__ C, int M, int N,
@@ -355,14 +439,25 @@ __global__ __launch_bounds__(g4::kThreads) void gemm_w4_kernel(
   // accumulator element r of lane L in atom (i, j) is output row
   // i ATOM + L % ATOM, column j ATOM + Op::acc_row(r, L) of the wave's
   // 128x128 sub-tile, and elements 4q .. 4q+3 are four consecutive columns.
-  // Each wave stages half of its sub-tile at a time in LDS by rows, one
-  // 16-byte write of four accumulators straight from the AGPRs per column
-  // group, then stores row pieces, consecutive lanes on consecutive pieces:
-  // 8 outputs (16 bytes) per lane for 16-bit outputs through store8, 4 (16
-  // bytes) for 32-bit ones through store4; both scale, accumulate and
-  // convert.  Staged row R keeps 16-byte chunk c at c ^ (R & 15) ^ (c >> 4):
-  // the writes of 16 lanes (16 rows, one column group) and each read of 16
-  // lanes (one row; chunks 2g or 2g+1, or g) touch every bank once.
+  // 16-bit outputs of 32x32 atoms round in registers and stage once
+  // (epilogue16).  Otherwise each wave stages half of its sub-tile at a time
+  // in LDS by rows as 32-bit values, one 16-byte write of four accumulators
+  // straight from the AGPRs per column group, then stores row pieces,
+  // consecutive lanes on consecutive pieces: 8 outputs (16 bytes) per lane
+  // for 16-bit outputs through store8, 4 (16 bytes) for 32-bit ones through
+  // store4; both scale, accumulate and convert.  Staged row R keeps 16-byte
+  // chunk c at c ^ (R & 15) ^ (c >> 4): the writes of 16 lanes (16 rows, one
+  // column group) and each read of 16 lanes (one row; chunks 2g or 2g+1, or
+  // g) touch every bank once.  (16-bit outputs staged that way, in two
+  // passes of f32: bf16 4096^3 -0.4-1.3%, fp8 -0.2-0.7%, bit-identical.)
+  if constexpr (EltInfo<OUT>::bytes == 2 && ATOM == 32) {
+    char* stage = smem + wave * (128 * 256);
+    if (accumulate)
+      epilogue16<OUT, true>(acc, scale, lane, stage, row0 + wm * 128, col0 + wn * 128, M, N, ldc, C);
+    else
+      epilogue16<OUT, false>(acc, scale, lane, stage, row0 + wm * 128, col0 + wn * 128, M, N, ldc, C);
+    return;
+  }
   {
     constexpr int kOut = EltInfo<OUT>::bytes == 2 ? 8 : 4;  // outputs per lane per store
     constexpr int kPPR = 128 / kOut;         // pieces per staged row

@@ -86,6 +86,27 @@ def test_small_shapes_every_type_and_layout(in_dt, out_dt, ta, tb):
         check(got if in_dt != torch.int8 else decode(c), ref, in_dt, out_dt)
 
 
+@pytest.mark.parametrize("in_dt,out_dt,ta,tb", [(torch.bfloat16, torch.bfloat16, False, True),
+                                                (torch.bfloat16, torch.bfloat16, False, False),
+                                                (torch.float16, torch.float16, True, True),
+                                                (FP8, torch.bfloat16, False, True),
+                                                (FP8, torch.float16, True, False)],
+                         ids=lambda x: str(x).replace("torch.", ""))
+def test_two_rounds_of_tiles_with_edges(in_dt, out_dt, ta, tb):
+    # 16 x 18 = 288 tiles of 256 x 256, more than the CUs: a second round of
+    # workgroups.  The last tile row (160 rows) and column (8 columns) are
+    # partial; C starts as NaN, so an output left unwritten fails too.
+    m, n, k = 4000, 4360, 264
+    print(f"case two rounds {in_dt}->{out_dt} ta={ta} tb={tb}", flush=True)
+    a, b, sa, sb = make_operands(m, n, k, in_dt, ta, tb, seed=61)
+    c = torch.full((m, n), float("nan"), dtype=out_dt, device="cuda")
+    rt.gemm(a, b, c, trans_a=ta, trans_b=tb, scale_a=sa, scale_b=sb)
+    torch.cuda.synchronize()
+    got = decode(c).astype(np.float64)
+    assert not np.isnan(got).any()
+    check(got, np.asarray(reference(a, b, ta, tb, sa, sb), dtype=np.float64), in_dt, out_dt)
+
+
 @pytest.mark.parametrize("in_dt,out_dt", [(torch.bfloat16, torch.bfloat16),
                                           (torch.bfloat16, torch.float32),
                                           (torch.int8, torch.int32), (FP8, torch.float32)],
