@@ -50,6 +50,11 @@ namespace frisk {
 
 namespace {
 
+// Every building block of the kernel body is inlined: a lambda left as a
+// call keeps its captures in private memory, and the buffer resources
+// loaded from there are no longer known to be uniform.
+#define FRISK_INLINE __attribute__((always_inline))
+
 constexpr int kBN = 64;       // keys per block
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
@@ -264,7 +269,7 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(
       v_row[i] = ((wave * kVI + i) < kVIns && c * 8 < D) ? r : 1 << 30;
       v_off[i] = (uint32_t)(r * v_ss * 2) + (c << 4);
     }
-    auto issue_k = [&](int kb, char* dst) {
+    auto issue_k = [&](int kb, char* dst) FRISK_INLINE {
       // A K block starts kBN keys further: kBN rows, or with KT kBN columns.
       const uint32_t kbase = (uint32_t)(KT ? (int64_t)kb * kBN * 2 : (int64_t)kb * kBN * k_ss * 2);
 #pragma unroll
@@ -276,7 +281,7 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(
             r < seq_k ? kbase + k_off[i] : 0x80000000u, 0, 0, 0);
       }
     };
-    auto issue_v = [&](int kb, char* dst) {
+    auto issue_v = [&](int kb, char* dst) FRISK_INLINE {
       const uint32_t vbase = (uint32_t)((int64_t)kb * kBN * v_ss * 2);
 #pragma unroll
       for (int i = 0; i < kVI; ++i) {
@@ -287,7 +292,7 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(
             r < seq_k ? vbase + v_off[i] : 0x80000000u, 0, 0, 0);
       }
     };
-    auto issue_kv = [&](int kb, int buf) {
+    auto issue_kv = [&](int kb, int buf) FRISK_INLINE {
       char* dst = smem + buf * G::kBuf;
       issue_k(kb, dst);
       issue_v(kb, dst);
@@ -339,7 +344,7 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(
 
     // ---- building blocks ----------------------------------------------------
     // K fragments of head-dim steps h0 .. h0+n-1 for both 32-key tiles.
-    auto read_k = [&](const char* ks, int h0, auto& kf) {
+    auto read_k = [&](const char* ks, int h0, auto& kf) FRISK_INLINE {
       constexpr int n = sizeof(kf[0]) / sizeof(kf[0][0]);
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt) {
@@ -361,7 +366,7 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(
       }
     };
     // V^T fragments of key steps k0, k0+1 (16 keys each).
-    auto read_v = [&](const char* ks, int k0, i32x4 (&vf)[2][G::kDT]) {
+    auto read_v = [&](const char* ks, int k0, i32x4 (&vf)[2][G::kDT]) FRISK_INLINE {
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -381,7 +386,7 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(
     // p = exp2(s * scale_log2 - m).  The max is taken on raw scores
     // (scale_log2 > 0 commutes with max).  Masked blocks (the sequence tail,
     // and blocks crossing this wave's causal diagonal) apply the key mask.
-    auto softmax = [&](f32x16 (&s)[QT][2], i32x4 (&pf)[QT][4], int kbase, auto masked_tag) {
+    auto softmax = [&](f32x16 (&s)[QT][2], i32x4 (&pf)[QT][4], int kbase, auto masked_tag) FRISK_INLINE {
       constexpr bool kMasked = decltype(masked_tag)::value;
 #pragma unroll
       for (int t = 0; t < QT; ++t) {
@@ -457,7 +462,7 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(
     // half's reads issue under the first half's MFMAs.  The first half of
     // the V^T fragments is read before the softmax, whose VALU work hides
     // it.
-    auto key_block = [&](const char* ks, int kbase, auto masked_tag) {
+    auto key_block = [&](const char* ks, int kbase, auto masked_tag) FRISK_INLINE {
       // Under a causal mask a block that starts past the last key this
       // wave's queries see gives p = 0 in every row: the wave skips its
       // arithmetic (still taking part in the loads and barriers); its state
@@ -513,16 +518,33 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(
           for (int t = 0; t < QT; ++t) o[t][dt] = Mf::run(vf1[i][dt], pf[t][2 + i], o[t][dt]);
     };
 
-    auto step = [&](int j, auto masked_tag) {
-      const int buf = j & 1;
+    // Block j uses buffer j & 1.  In the unmasked blocks of 8-wave
+    // workgroups that is a compile-time constant (two steps per trip), so
+    // the fragment reads add the buffer base as an immediate offset to
+    // block-invariant lane addresses instead of a VALU add per read (C5
+    // non-causal +1.5-2.7%, bit-identical).  The masked blocks, and the
+    // 4-wave kernels, keep one copy of the step: the second copy's hoisted
+    // addresses cost the registers they do not have (4 waves: -17%).
+    auto step = [&](int j, auto masked_tag, auto bufc) FRISK_INLINE {
+      const int buf = decltype(bufc)::value < 0 ? (j & 1) : decltype(bufc)::value;
       const bool more = j + 1 < nkb;
       if (more) issue_kv(j + 1, buf ^ 1);
       key_block(smem + buf * G::kBuf, j * kBN, masked_tag);
       if (more) FRISK_WAIT_VMCNT0();
       __syncthreads();
     };
-    for (int j = 0; j < n_plain; ++j) step(j, std::false_type{});
-    for (int j = n_plain; j < nkb; ++j) step(j, std::true_type{});
+    using BufRt = std::integral_constant<int, -1>;
+    using Buf0 = std::integral_constant<int, 0>;
+    using Buf1 = std::integral_constant<int, 1>;
+    int j = 0;
+    if constexpr (NW == 8) {
+      for (; j + 1 < n_plain; j += 2) {
+        step(j, std::false_type{}, Buf0{});
+        step(j + 1, std::false_type{}, Buf1{});
+      }
+    }
+    for (; j < n_plain; ++j) step(j, std::false_type{}, BufRt{});
+    for (; j < nkb; ++j) step(j, std::true_type{}, BufRt{});
 
     // ---- epilogue: O = O^T / l, LSE -----------------------------------------
     constexpr int kOB = EltInfo<OUT>::bytes;
