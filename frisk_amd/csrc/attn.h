@@ -519,12 +519,13 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(
     };
 
     // Block j uses buffer j & 1.  In the unmasked blocks of 8-wave
-    // workgroups that is a compile-time constant (two steps per trip), so
-    // the fragment reads add the buffer base as an immediate offset to
-    // block-invariant lane addresses instead of a VALU add per read (C5
-    // non-causal +1.5-2.7%, bit-identical).  The masked blocks, and the
-    // 4-wave kernels, keep one copy of the step: the second copy's hoisted
-    // addresses cost the registers they do not have (4 waves: -17%).
+    // workgroups without a causal mask that is a compile-time constant (two
+    // steps per trip), so the fragment reads add the buffer base as an
+    // immediate offset to block-invariant lane addresses instead of a VALU
+    // add per read (C5 non-causal +2.9-3.6%, bit-identical).  The masked
+    // blocks, the causal kernels (no gain measured, 256 VGPRs) and the
+    // 4-wave kernels (-17%) keep one copy of the step: the second copy's
+    // hoisted addresses cost registers they do not have.
     auto step = [&](int j, auto masked_tag, auto bufc) FRISK_INLINE {
       const int buf = decltype(bufc)::value < 0 ? (j & 1) : decltype(bufc)::value;
       const bool more = j + 1 < nkb;
@@ -537,7 +538,7 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(
     using Buf0 = std::integral_constant<int, 0>;
     using Buf1 = std::integral_constant<int, 1>;
     int j = 0;
-    if constexpr (NW == 8) {
+    if constexpr (NW == 8 && !CAUSAL) {
       for (; j + 1 < n_plain; j += 2) {
         step(j, std::false_type{}, Buf0{});
         step(j + 1, std::false_type{}, Buf1{});
