@@ -462,18 +462,25 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(
     // half's reads issue under the first half's MFMAs.  The first half of
     // the V^T fragments is read before the softmax, whose VALU work hides
     // it.
-    auto key_block = [&](const char* ks, int kbase, auto masked_tag) FRISK_INLINE {
+    auto key_block = [&](const char* ks, int kbase, auto masked_tag, auto&& dma) FRISK_INLINE {
       // Under a causal mask a block that starts past the last key this
       // wave's queries see gives p = 0 in every row: the wave skips its
       // arithmetic (still taking part in the loads and barriers); its state
       // is unchanged, as the masked arithmetic would leave it.
       if constexpr (CAUSAL && decltype(masked_tag)::value)
-        if (kbase > wq0 + 32 * QT - 1 + diag) return;
+        if (kbase > wq0 + 32 * QT - 1 + diag) {
+          dma();  // this wave's share of the next block's loads
+          return;
+        }
       f32x16 s[QT][2];
 #pragma unroll
       for (int t = 0; t < QT; ++t) s[t][0] = s[t][1] = f32x16{};
       i32x4 kf0[2][G::kH1], kf1[2][G::kH2 > 0 ? G::kH2 : 1];
       read_k(ks, 0, kf0);
+      __builtin_amdgcn_sched_barrier(0);
+      // The next block's loads (dma) go out behind the first fragment
+      // reads, whose latency they fill.
+      dma();
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (G::kH2 > 0) read_k(ks, G::kH1, kf1);
 #pragma unroll
@@ -529,8 +536,17 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(
     auto step = [&](int j, auto masked_tag, auto bufc) FRISK_INLINE {
       const int buf = decltype(bufc)::value < 0 ? (j & 1) : decltype(bufc)::value;
       const bool more = j + 1 < nkb;
-      if (more) issue_kv(j + 1, buf ^ 1);
-      key_block(smem + buf * G::kBuf, j * kBN, masked_tag);
+      // Without a causal mask the next block's loads go out behind this
+      // block's first K fragment reads; the causal kernels, at their
+      // register limit (spills), issue them first.
+      if constexpr (CAUSAL) {
+        if (more) issue_kv(j + 1, buf ^ 1);
+        key_block(smem + buf * G::kBuf, j * kBN, masked_tag, []() FRISK_INLINE {});
+      } else {
+        key_block(smem + buf * G::kBuf, j * kBN, masked_tag, [&]() FRISK_INLINE {
+          if (more) issue_kv(j + 1, buf ^ 1);
+        });
+      }
       if (more) FRISK_WAIT_VMCNT0();
       __syncthreads();
     };
