@@ -64,9 +64,10 @@ constexpr int lds_bytes(int kr) { return kRing * kBT * kr; }
 // acc * scale (+ C when accumulating, read as f32 before the rounding),
 // rounded once to nearest even, as in the f32-staged path; each wave reads
 // back only what it wrote, so no workgroup barrier is needed.
-template <Elt OUT, bool ACCUMULATE, int TM, int TN>
-__device__ __forceinline__ void epilogue16(const f32x16 (&acc)[TM][TN], float scale, int lane, char* stage, int r0, int c0,
-                                           int M, int N, int64_t ldc, void* C) {
+template <Elt OUT, bool ACCUMULATE, bool SCALED, int TM, int TN>
+__device__ __forceinline__ void epilogue16(const f32x16 (&acc)[TM][TN], float scale, int lane,
+                                           char* stage, int r0, int c0, int M, int N, int64_t ldc,
+                                           void* C) {
   constexpr int kPitch = 256;
   auto at = [](int R, int c) { return R * kPitch + ((c ^ (R & 15)) << 4); };
   const int half = lane >> 5;
@@ -99,7 +100,7 @@ __device__ __forceinline__ void epilogue16(const f32x16 (&acc)[TM][TN], float sc
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
           asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(f[k]) : "a"(acc[i][j][8 * p + k]));
-          f[k] *= scale;
+          if constexpr (SCALED) f[k] *= scale;  // x * 1 == x: skipped for scale 1
         }
         const int R = i * 32 + (lane & 31);
         if constexpr (ACCUMULATE) {
@@ -452,10 +453,13 @@ __global__ __launch_bounds__(g4::kThreads) void gemm_w4_kernel(
   // passes of f32: bf16 4096^3 -0.4-1.3%, fp8 -0.2-0.7%, bit-identical.)
   if constexpr (EltInfo<OUT>::bytes == 2 && ATOM == 32) {
     char* stage = smem + wave * (128 * 256);
+    const int r0 = row0 + wm * 128, c0 = col0 + wn * 128;
     if (accumulate)
-      epilogue16<OUT, true>(acc, scale, lane, stage, row0 + wm * 128, col0 + wn * 128, M, N, ldc, C);
+      epilogue16<OUT, true, true>(acc, scale, lane, stage, r0, c0, M, N, ldc, C);
+    else if (scale == 1.0f)
+      epilogue16<OUT, false, false>(acc, scale, lane, stage, r0, c0, M, N, ldc, C);
     else
-      epilogue16<OUT, false>(acc, scale, lane, stage, row0 + wm * 128, col0 + wn * 128, M, N, ldc, C);
+      epilogue16<OUT, false, true>(acc, scale, lane, stage, r0, c0, M, N, ldc, C);
     return;
   }
   {
