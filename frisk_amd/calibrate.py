@@ -2,7 +2,7 @@
 
 Layout inference (frisk_amd/ir/infer.cpp) scores a candidate assignment as
 sum_f w_f x_f over named features x_f (MFMA issue cycles, LDS read/write
-cycles, 128-byte global lines, VALU / transcendental / cross-lane issue,
+cycles, fragment LDS read instructions, 128-byte global lines, VALU / transcendental / cross-lane issue,
 conversion bytes, barriers).  The default profile `cdna4-layout-v1` takes w
 from hardware rates.  This module fits w to what the compiled kernels take on
 the MI355X, and writes the result as a cost profile that inference loads
@@ -37,12 +37,15 @@ the solver's own, for the tile program one workgroup executes:
     one 64-key block and against two; the difference is one key block, and
     the row is the workgroup's key blocks plus the rest.
 
-Per-wave features (MFMA, VALU, transcendental, cross-lane) are scaled by
-waves / 4, the share of a CU's four SIMDs the workgroup occupies, so the
-model is in CU cycles (the profile's `simd_share`).  The fit is non-negative
-least squares on relative error; a feature that no row exercises keeps its
-default weight.  Beside the fit the summary reports, per decision the solver
-makes on these tiles (the wave grid of a 128x128 tile at fixed threads), the
+Per-wave features (MFMA, fragment reads, VALU, transcendental, cross-lane)
+are scaled by waves / 4, the share of a CU's four SIMDs the workgroup
+occupies, so the model is in CU cycles (the profile's `simd_share`).  The
+fit is least squares on relative error with each weight bounded to a factor
+BAND of its static hardware rate (unbounded, the attention rows' unmodelled
+waits drive the cross-lane weight to thousands of cycles and the LDS weights
+to zero); a feature that no row exercises keeps its default weight.  Beside
+the fit the summary reports, per decision the solver makes on these tiles
+(the wave grid of a 128x128 tile at fixed threads), the
 grid each profile picks against the one that ran fastest.
 
 Usage:
@@ -395,8 +398,8 @@ def design_matrix(rows: List[dict], simd_share: bool):
     """Feature matrix (rows x features) as the solver weighs it: per-wave
     features scaled by waves / 4 when simd_share."""
     import numpy as np
-    names = list(_ir().frisk.cost_profile_defaults()["weights"])
-    per_wave = {"mfma_cycles", "valu_issues", "trans_issues", "reduction_shuffles"}
+    defaults = _ir().frisk.cost_profile_defaults()
+    names, per_wave = list(defaults["weights"]), set(defaults["per_wave"])
     x = np.zeros((len(rows), len(names)))
     for i, r in enumerate(rows):
         share = row_waves(r) / 4.0 if simd_share else 1.0
@@ -405,12 +408,17 @@ def design_matrix(rows: List[dict], simd_share: bool):
     return x, names
 
 
-def _nnls_relative(x, y):
+BAND = 4.0  # each fitted weight stays within [w0 / BAND, w0 * BAND] of its static rate w0
+
+
+def _fit_relative(x, y, w0):
+    """Least squares on relative error, each weight bounded to the band
+    around its static (hardware-rate) weight w0."""
     import numpy as np
-    from scipy.optimize import nnls
+    from scipy.optimize import lsq_linear
     a = x / y[:, None]
-    w, _ = nnls(a, np.ones(len(y)), maxiter=50 * x.shape[1])
-    return w
+    w0 = np.asarray(w0, dtype=float)
+    return lsq_linear(a, np.ones(len(y)), bounds=(w0 / BAND, w0 * BAND), method="bvls").x
 
 
 def canonical_weights(weights: Dict[str, float]) -> str:
@@ -462,8 +470,9 @@ def fit(sweep: dict, *, with_decisions: bool = True) -> Tuple[dict, dict]:
     y = np.array([target_cycles(r, cus) for r in rows])
     x, names = design_matrix(rows, simd_share=True)
     excited = [j for j in range(len(names)) if np.any(x[:, j] != 0)]
-    w_exc = _nnls_relative(x[:, excited], y)
     defaults = _ir().frisk.cost_profile_defaults()["weights"]
+    w0 = [defaults[names[j]] for j in excited]
+    w_exc = _fit_relative(x[:, excited], y, w0)
     weights = dict(defaults)
     for j, wj in zip(excited, w_exc):
         weights[names[j]] = float(f"{wj:.6g}")
@@ -474,7 +483,7 @@ def fit(sweep: dict, *, with_decisions: bool = True) -> Tuple[dict, dict]:
     loo = []
     for i in range(len(rows)):
         keep = np.arange(len(rows)) != i
-        wi = _nnls_relative(x[keep][:, excited], y[keep])
+        wi = _fit_relative(x[keep][:, excited], y[keep], w0)
         loo.append(float(x[i, excited] @ wi / y[i] - 1))
     loo = np.array(loo)
     x0, _ = design_matrix(rows, simd_share=False)
@@ -494,8 +503,8 @@ def fit(sweep: dict, *, with_decisions: bool = True) -> Tuple[dict, dict]:
             "gpu": sweep["gpu"],
             "source_sha256_16": sweep.get("source_sha256_16"),
             "target": "CU cycles per workgroup = t * f_sclk * CUs / workgroups",
-            "fit": "non-negative least squares on relative error; unexercised features keep "
-                   "the cdna4-layout-v1 weight",
+            "fit": "least squares on relative error, each weight within a factor "
+                   f"{BAND:g} of its cdna4-layout-v1 rate; unexercised features keep that weight",
             "fitted_features": [names[j] for j in excited],
             "rel_rms": round(float(np.sqrt(np.mean(rel ** 2))), 4),
             "loo_rel_rms": round(float(np.sqrt(np.mean(loo ** 2))), 4),

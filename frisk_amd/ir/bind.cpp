@@ -1307,6 +1307,7 @@ void bindFrisk(py::module_& m) {
     d["id"] = p.id;
     d["weights"] = p.weights;
     d["simd_share"] = p.simdShare;
+    d["per_wave"] = CostProfile::perWaveFeatures();
     return d;
   });
   m.def("mma_bindings", [](int64_t mm, int64_t n, int64_t k, const PyType& in, const PyType& acc,

@@ -311,6 +311,7 @@ const std::vector<std::string>& CostProfile::featureNames() {
   static const std::vector<std::string> names = {
       "mfma_cycles",         // MFMA issue cycles per wave
       "lds_read_cycles",     // LDS read cycles per workgroup (phases x conflict)
+      "lds_read_issues",     // MMA fragment LDS read instructions per wave
       "lds_write_cycles",    // LDS write cycles per workgroup
       "global_lines",        // 128-byte lines touched per workgroup
       "valu_issues",         // VALU instructions per wave
@@ -322,8 +323,8 @@ const std::vector<std::string>& CostProfile::featureNames() {
 }
 
 const std::vector<std::string>& CostProfile::perWaveFeatures() {
-  static const std::vector<std::string> names = {"mfma_cycles", "valu_issues", "trans_issues",
-                                                 "reduction_shuffles"};
+  static const std::vector<std::string> names = {"mfma_cycles", "lds_read_issues", "valu_issues",
+                                                 "trans_issues", "reduction_shuffles"};
   return names;
 }
 
@@ -332,12 +333,17 @@ CostProfile CostProfile::defaults() {
   // modelled phases (16 lanes x 16 B at 64 banks of 4 B).  A 128-byte global
   // line takes 2 cycles of the 64 B/clk L1 return path.  A wave64 VALU op
   // issues over 4 cycles; transcendentals run at quarter rate (16).  A
-  // cross-lane step is a DPP/permlane move plus the combine (8).  LDS moves
+  // cross-lane step is a DPP/permlane move plus the combine (8).  A fragment
+  // LDS read instruction takes a wave64 issue slot (4): the transposing
+  // 8-byte reads of M/N-major operands need twice the instructions of
+  // ds_read_b128 for the same bytes, so the wave that reads more of the
+  // transposed operand issues more.  LDS moves
   // 128 B/clk.  A workgroup barrier costs ~150 cycles (measured: the ping-pong
   // GEMM's extra barrier per phase cost 150 cycles, SQ_BUSY_CYCLES).
   CostProfile p;
-  p.weights = {{"mfma_cycles", 1.0},       {"lds_read_cycles", 1.0},  {"lds_write_cycles", 1.0},
-               {"global_lines", 2.0},      {"valu_issues", 4.0},      {"trans_issues", 16.0},
+  p.weights = {{"mfma_cycles", 1.0},       {"lds_read_cycles", 1.0},  {"lds_read_issues", 4.0},
+               {"lds_write_cycles", 1.0},  {"global_lines", 2.0},     {"valu_issues", 4.0},
+               {"trans_issues", 16.0},
                {"reduction_shuffles", 8.0}, {"conversion_bytes", 1.0 / 128.0}, {"barriers", 150.0}};
   return p;
 }
@@ -929,9 +935,14 @@ class Inference {
         const std::string key = "fr" + std::to_string((uintptr_t)op) + ":" + std::to_string(w) + ":" +
                                 std::to_string(asg[s.var]) + ":" + std::to_string(storageChoice(v, asg));
         auto it = memo_.find(key);
-        if (it == memo_.end())
-          it = memo_.emplace(key, fragmentReadCycles(v, req, which == 'A' ? !s.ta : s.tb, asg)).first;
+        if (it == memo_.end()) {
+          double issues = 0;
+          const double cycles = fragmentReadCycles(v, req, which == 'A' ? !s.ta : s.tb, asg, issues);
+          memo_.emplace(key + ":issues", issues);
+          it = memo_.emplace(key, cycles).first;
+        }
         f["lds_read_cycles"] += it->second;
+        f["lds_read_issues"] += memo_.at(key + ":issues");
       } else {
         const int c = classOf(v);
         auto have = classLayout(c, asg);
@@ -964,8 +975,10 @@ class Inference {
 
   // LDS cycles of reading an MMA operand fragment `l` (over the memref's own
   // shape) from `memref`; kContig: the per-lane k run is along the memref's
-  // contiguous dimension.
-  double fragmentReadCycles(Value memref, const DistLayout& l, bool kContig, const std::vector<int64_t>& asg) {
+  // contiguous dimension.  `issues` receives the read instructions one wave
+  // issues.
+  double fragmentReadCycles(Value memref, const DistLayout& l, bool kContig, const std::vector<int64_t>& asg,
+                            double& issues) {
     Type t = memref.type();
     const int64_t eb = elemBytes(t.elementType());
     // Per-lane vector: the consecutive register bits that walk the
@@ -981,9 +994,14 @@ class Inference {
       // k-consecutive elements per lane (modelled at the lanes' first element).
       vecElems = 4;
       bytes = 8;
+    } else if (!kContig && eb == 1) {
+      // ds_read_b64_tr_b8 likewise delivers 8 k-consecutive bytes per lane.
+      vecElems = 8;
+      bytes = 8;
     }
     double cycles = 0;
     const int64_t instrPerLane = std::max<int64_t>(1, l.regs() / vecElems);
+    issues = (double)instrPerLane;
     for (int64_t wv = 0; wv < l.waves(); ++wv)
       for (int64_t ins = 0; ins < instrPerLane; ++ins) {
         std::vector<int64_t> addrs(64);

@@ -46,11 +46,34 @@ def test_refit_reproduces_the_shipped_profile():
     import hashlib
     digest = hashlib.sha256(C.canonical_weights(shipped["weights"]).encode()).hexdigest()
     assert shipped["id"].endswith(digest[:16])
-    # The calibrated model predicts the measured CU cycles per workgroup far
-    # better than the hardware-rate profile does even at its best scale.
+    # The calibrated model predicts the measured CU cycles per workgroup
+    # better than the hardware-rate profile does even at its best scale, with
+    # every fitted weight inside the band around its hardware rate.
     rms = lambda v: (sum(x * x for x in v) / len(v)) ** 0.5
-    assert rms(report["rel"]) < 0.2 and rms(report["rel"]) < 0.5 * rms(report["default_rel"])
+    assert rms(report["rel"]) < 0.2 and rms(report["rel"]) < rms(report["default_rel"])
     assert rms(report["loo"]) < 0.2
+    for f in report["excited"]:
+        w, w0 = shipped["weights"][f], report["defaults"][f]
+        assert w0 / C.BAND * (1 - 1e-6) <= w <= w0 * C.BAND * (1 + 1e-6), f
+
+
+def test_wave_grid_decisions_follow_the_measured_kernels():
+    # On the sweep's 32 wave-grid decisions (128x128 tile at 128 and 256
+    # threads, four input types, four storage orders) both profiles pick
+    # the fastest measured grid in 27 and one within 2% of it in 30.  The
+    # transposed operand's 8-byte fragment reads are what separate 2x1 from
+    # 1x2 on tt storage (2x1 measured 3.5% faster for bf16 and f16).
+    rows = json.loads(C.SWEEP_FILE.read_text())["rows"]
+    dec = C.decisions(rows, {"static": None, "calibrated": C.PROFILE_FILE.read_text()})
+    assert len(dec) == 32
+    for name in ("static", "calibrated"):
+        fastest = sum(d["picked"][name] == d["fastest"] for d in dec)
+        near = sum(d["picked"][name] in d["near"] for d in dec)
+        assert fastest >= 27 and near >= 30, (name, fastest, near)
+    tt = {d["dtype"]: d for d in dec if d["trans_a"] and d["trans_b"] and d["threads"] == 128}
+    for dt in ("bf16", "fp16"):
+        assert tt[dt]["fastest"] == "2x1"
+        assert tt[dt]["picked"]["static"] == tt[dt]["picked"]["calibrated"] == "2x1"
 
 
 def test_sweep_rows_cover_every_variant_type_and_order():
@@ -65,7 +88,7 @@ def test_sweep_rows_cover_every_variant_type_and_order():
 
 
 def test_simd_share_scales_per_wave_features():
-    only_mfma = {"mfma_cycles": 1.0, "lds_read_cycles": 0, "lds_write_cycles": 0,
+    only_mfma = {"mfma_cycles": 1.0, "lds_read_cycles": 0, "lds_read_issues": 0, "lds_write_cycles": 0,
                  "global_lines": 0, "barriers": 0, "conversion_bytes": 0}
     for threads in (128, 256):
         plain = C.staged_tile_report(128, 128, 64, "bf16", False, False, threads, "Square",
