@@ -316,15 +316,30 @@ def _time_launches(torch, fn, window_ms: float = 200.0) -> Tuple[float, Optional
     return a.elapsed_time(b) / reps, (samples[len(samples) // 2] if samples else None)
 
 
-def _timed_passes(torch, fn, passes: int = 2):
-    """(mean ms, mean MHz, relative spread of the cycle counts) over
-    `passes` timed windows of fn."""
-    got = [_time_launches(torch, fn) for _ in range(passes)]
-    ms = sum(g[0] for g in got) / passes
+def _summarize(got):
+    """(mean ms, mean MHz, relative spread of the cycle counts) of timed
+    windows [(ms, MHz), ...] of one launch."""
+    ms = sum(g[0] for g in got) / len(got)
     clocks = [g[1] for g in got if g[1] is not None]
     mhz = round(sum(clocks) / len(clocks)) if clocks else None
     cyc = [g[0] * (g[1] or 1) for g in got]
-    return ms, mhz, round((max(cyc) - min(cyc)) / (sum(cyc) / passes), 4)
+    return ms, mhz, round((max(cyc) - min(cyc)) / (sum(cyc) / len(got)), 4)
+
+
+def _timed_passes(torch, fn, passes: int = 2):
+    """_summarize of `passes` timed windows of fn."""
+    return _summarize([_time_launches(torch, fn) for _ in range(passes)])
+
+
+def _timed_interleaved(torch, fns, passes: int = 3):
+    """_summarize per launch of `passes` rounds that time every fn once in
+    turn, so that a drift of the clock between rounds reaches all of them
+    alike (the wave grids of one group differ by a few percent)."""
+    got = [[] for _ in fns]
+    for _ in range(passes):
+        for i, fn in enumerate(fns):
+            got[i].append(_time_launches(torch, fn))
+    return [_summarize(g) for g in got]
 
 
 def measure(out: Path) -> dict:
@@ -351,13 +366,16 @@ def measure(out: Path) -> dict:
             a = mk(k, m) if ta else mk(m, k)
             b = mk(n, k) if tb else mk(k, n)
             c = torch.empty(m, n, device="cuda", dtype=odt[dt])
-            for var in GEMM_VARIANTS:
+            fns = [lambda var=var: rt.gemm(a, b, c, trans_a=ta, trans_b=tb, workspace=False,
+                                           variant=var) for var in GEMM_VARIANTS]
+            if not rows:
+                _time_launches(torch, fns[0], window_ms=1000.0)  # the clock's first ramp
+            timed = _timed_interleaved(torch, fns)
+            for var, (ms, mhz, spread) in zip(GEMM_VARIANTS, timed):
                 plan = rt.gemm_plan(a, b, c, trans_a=ta, trans_b=tb, workspace=False, variant=var)
                 ct = variants.parse_contract(plan["mma_contract"])
                 atom_k = int(ct["atom"].rsplit("x", 1)[1].split("_")[0])
                 bk = ct["repeats"][2] * atom_k
-                fn = lambda: rt.gemm(a, b, c, trans_a=ta, trans_b=tb, workspace=False, variant=var)
-                ms, mhz, spread = _timed_passes(torch, fn)
                 wgs = -(-m // var[0]) * -(-n // var[0])
                 rows.append({"kind": "gemm", "dtype": dt, "trans_a": ta, "trans_b": tb,
                              "variant": list(var), "m": m, "n": n, "k": k, "bk": bk,
