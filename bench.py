@@ -117,6 +117,20 @@ def make_workloads(torch, rt):
             return lambda: torch.matmul(a, b.t())
         return setup
 
+    def library_gemm_fp8(m, n, k):
+        # torch._scaled_mm (hipBLASLt) on the fp8 workload's operands and scales.
+        def setup():
+            a = torch.randn(m, k, generator=gen(1), device=dev)
+            b = torch.randn(n, k, generator=gen(2), device=dev)
+            sa, sb = 448.0 / float(a.abs().max()), 448.0 / float(b.abs().max())
+            a8, b8 = (a * sa).to(torch.float8_e4m3fn), (b * sb).to(torch.float8_e4m3fn)
+            del a, b
+            ia = torch.tensor(1 / sa, device=dev)
+            ib = torch.tensor(1 / sb, device=dev)
+            return lambda: torch._scaled_mm(a8, b8.t(), scale_a=ia, scale_b=ib,
+                                            out_dtype=torch.bfloat16)
+        return setup
+
     def copy(nbytes):
         def setup():
             src = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1)
@@ -193,6 +207,8 @@ def make_workloads(torch, rt):
         # Comparison only (--only): hipBLASLt (torch.matmul) on the headline
         # GEMM's operands, for counter passes beside gemm_bf16_4096.
         "hipblaslt_bf16_4096": ("ref", 2.0 * 4096 ** 3, library_gemm(4096, 4096, 4096)),
+        "hipblaslt_fp8_4096x8192x8192": ("ref", 2.0 * 4096 * 8192 * 8192,
+                                         library_gemm_fp8(4096, 8192, 8192)),
     }
 
 

@@ -50,6 +50,23 @@ constexpr int kThreads = 256;
 constexpr int kRing = 5;  // operand-tile slots of the LDS ring
 constexpr int lds_bytes(int kr) { return kRing * kBT * kr; }
 
+// Load q of an iteration (B(kt+1) blocks 0..nb-1, then A(kt+2) blocks) goes
+// out beside MFMA pos(q) of the iteration's t MFMAs: evenly spread, the last
+// beside the last MFMA.
+constexpr int load_pos(int q, int nb, int t) { return (q + 1) * t / (2 * nb) - 1; }
+// Loads placed beside MFMAs [g0, g1) of the iteration.
+constexpr int loads_in(int nb, int t, int g0, int g1) {
+  int c = 0;
+  for (int q = 0; q < 2 * nb; ++q) c += load_pos(q, nb, t) >= g0 && load_pos(q, nb, t) < g1;
+  return c;
+}
+// A loads placed before MFMA g (all B loads are older than every A load).
+constexpr int a_loads_before(int nb, int t, int g) {
+  int c = 0;
+  for (int q = nb; q < 2 * nb; ++q) c += load_pos(q, nb, t) < g;
+  return c;
+}
+
 }  // namespace g4
 
 // Epilogue of 16-bit outputs, one pass: each wave rounds its 128x128
@@ -159,11 +176,7 @@ __global__ __launch_bounds__(g4::kThreads) void gemm_w4_kernel(
   constexpr int kLaneChunks = TA::kLaneChunks;  // 16 B pieces per lane per MFMA
   constexpr int kSteps = KR / Op::kBytes;       // MFMA k-steps per stage
   constexpr int kBlocks = kTileBytes / 1024 / 4;  // DMA blocks per wave per operand
-  // LDS read instructions per lane per k-step (two per 16 B of an MN-major
-  // operand, one of a K-major one).
-  constexpr int kFragReads =
-      (TM * TA::kReadsPerChunk + TN * TB::kReadsPerChunk) * kLaneChunks;
-  static_assert(kSteps >= 1, "pipeline shape");
+  static_assert(kSteps >= 2, "a stage holds at least two MFMA k-steps");
 
   extern __shared__ __attribute__((aligned(1024))) char smem[];
 
@@ -236,14 +249,8 @@ __global__ __launch_bounds__(g4::kThreads) void gemm_w4_kernel(
     if (phys >= nk_all) phys -= nk_all;
     return stage >= nk_all ? stage : phys;
   };
-  // The DMA of one operand tile goes out in parts, one per k-step: B in
-  // kBParts parts over the first k-steps of an iteration, A in kAParts parts
-  // over the rest (both in the one k-step of a single-step stage).  Part p
-  // of P covers blocks [p kBlocks / P, (p+1) kBlocks / P).
-  constexpr int kBParts = kSteps >= 2 ? kSteps / 2 : 1;
-  constexpr int kAParts = kSteps >= 2 ? kSteps - kBParts : 1;
-  static_assert(kBlocks >= kBParts && kBlocks >= kAParts, "DMA parts");
-  // `fast`: the steady state, where the stage is a whole one inside K (no
+  // issue() sends part p of np of one operand tile: blocks
+  // [p kBlocks / np, (p+1) kBlocks / np).  `fast`: the steady state, where the stage is a whole one inside K (no
   // partial stage exists and the stage is not past the last): every lane's
   // offset is its stage-invariant one and the stage base is the scalar
   // offset, so a load is issued with no VALU work at all.
@@ -284,13 +291,6 @@ __global__ __launch_bounds__(g4::kThreads) void gemm_w4_kernel(
   };
   using OpA = std::true_type;
   using OpB = std::false_type;
-  // Loads issued by k-step s of an iteration.
-  auto step_loads = [](int s) {
-    if (kSteps == 1) return 2 * kBlocks;
-    if (s < kBParts) return (s + 1) * kBlocks / kBParts - s * kBlocks / kBParts;
-    const int p = s - kBParts;
-    return (p + 1) * kBlocks / kAParts - p * kBlocks / kAParts;
-  };
 
   // ---- fragment reads -----------------------------------------------------
   // K-major operands share one Frag (tile 0's) across their tiles.
@@ -333,16 +333,24 @@ __global__ __launch_bounds__(g4::kThreads) void gemm_w4_kernel(
   // its MFMAs, each wave waits for its LDS reads and for all but its newest
   // kBlocks loads (A(kt+2)), which leaves A(kt+1) (issued an iteration
   // earlier) and B(kt+1) landed; the workgroup barrier then publishes them.
-  // Every k-step issues DMA, so no k-step carries a burst of issues, and
-  // every iteration issues the same loads (past the last stage they are
-  // zero-reads without memory traffic), so the vmcnt bookkeeping is static.
-  // Measured against two 64 KiB stages written whole per iteration
-  // (4096^3 bf16 / 4096x8192x8192 fp8 / 8192^3 bf16): +2% / +7% / +4%.
+  // The iteration's 2 kBlocks loads (B(kt+1) blocks, then A(kt+2) blocks)
+  // go out one beside every (kSteps kMf) / (2 kBlocks)-th MFMA over the
+  // whole iteration (g4::load_pos), the A loads of the last k-step's second
+  // half after its barrier, so the load rate never bunches up (TA
+  // address-FIFO-full cycles; bit-identical, bf16 +0.4-0.8%, int8 +0.5%,
+  // fp8 within noise against B over the first k-steps' second halves and A
+  // over the rest's).  Every iteration issues the same loads (past the last
+  // stage they are zero-reads without memory traffic), so the vmcnt
+  // bookkeeping is static.  Measured against two 64 KiB stages written
+  // whole per iteration (4096^3 bf16 / 4096x8192x8192 fp8 / 8192^3 bf16):
+  // +2% / +7% / +4%.
   const int nk = (Kb + KR - 1) / KR;
   using Slow = std::false_type;
-  static_for<0, kAParts>([&](auto p) { issue(OpA{}, 0, 0, p, std::integral_constant<int, kAParts>{}, Slow{}); });
-  static_for<0, kBParts>([&](auto p) { issue(OpB{}, 0, 1, p, std::integral_constant<int, kBParts>{}, Slow{}); });
-  static_for<0, kAParts>([&](auto p) { issue(OpA{}, 1, 2, p, std::integral_constant<int, kAParts>{}, Slow{}); });
+  using Whole = std::integral_constant<int, 0>;
+  using One = std::integral_constant<int, 1>;
+  issue(OpA{}, 0, 0, Whole{}, One{}, Slow{});
+  issue(OpB{}, 0, 1, Whole{}, One{}, Slow{});
+  issue(OpA{}, 1, 2, Whole{}, One{}, Slow{});
   FRISK_WAIT_VMCNT(kBlocks);
   __builtin_amdgcn_s_barrier();
 
@@ -357,65 +365,74 @@ __global__ __launch_bounds__(g4::kThreads) void gemm_w4_kernel(
   auto adv = [](int x) { return x >= 3 ? x - 3 : x + 2; };  // (x + 2) mod 5
   constexpr int kMf = TM * TN;
   constexpr int kHalf = kMf / 2;
+  static_assert(TM + TN == kHalf, "one fragment unit per MFMA of a half step");
+  // The loads that may still be in flight at the last k-step's barrier: the
+  // A(kt+2) loads issued before it (every B(kt+1) load is older).
+  constexpr int kT = kSteps * kMf;
+  constexpr int kInFlight = g4::a_loads_before(kBlocks, kT, kT - kHalf);
+  // Fragment unit u of k-step s: A tile u (u < TM) or B tile u - TM.
+  auto read_unit = [&](int aslot, int bslot, int s, Frag& f, int u) {
+    if (u < TM) TA::read(smem + aslot * kTileBytes, fa[TA::kSharedFrag ? 0 : u], s, f.a[u],
+                         TA::tile_off(u * ATOM));
+    else TB::read(smem + bslot * kTileBytes, fb[TB::kSharedFrag ? 0 : u - TM], s, f.b[u - TM],
+                  TB::tile_off((u - TM) * ATOM));
+  };
   auto iteration = [&](int kt, auto fast) {
     static_for<0, kSteps>([&](auto step) {
       constexpr int s = decltype(step)::value;
       constexpr int cur = s & 1, nxt = cur ^ 1;
-      constexpr int nload = step_loads(s);
-      auto issue_step = [&]() {
-        if constexpr (kSteps == 1) {
-          issue(OpB{}, kt + 1, b_wr, std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{},
-                fast);
-          issue(OpA{}, kt + 2, a_wr, std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{},
-                fast);
-        } else if constexpr (s < kBParts) {
-          issue(OpB{}, kt + 1, b_wr, std::integral_constant<int, s>{},
-                std::integral_constant<int, kBParts>{}, fast);
-        } else {
-          issue(OpA{}, kt + 2, a_wr, std::integral_constant<int, s - kBParts>{},
-                std::integral_constant<int, kAParts>{}, fast);
-        }
+      constexpr bool last = s + 1 == kSteps;
+      auto load = [&](auto qc) {
+        constexpr int q = decltype(qc)::value;
+        if constexpr (q < kBlocks)
+          issue(OpB{}, kt + 1, b_wr, std::integral_constant<int, q>{},
+                std::integral_constant<int, kBlocks>{}, fast);
+        else
+          issue(OpA{}, kt + 2, a_wr, std::integral_constant<int, q - kBlocks>{},
+                std::integral_constant<int, kBlocks>{}, fast);
       };
-      if constexpr (s + 1 < kSteps) {
-        // Program order: fragment reads, then DMA (the compiler keeps LDS
-        // reads and LDS-DMA writes in order, as it cannot tell slots apart).
-        // Fragment reads go under the first half of the MFMAs, DMA under
-        // the second half.
-        load_frags(a_rd, b_rd, s + 1, fr[nxt]);
-        issue_step();
+      // Program order = issue order: beside MFMA m, fragment unit m (first
+      // half of a k-step) or unit m - kHalf of the next stage (second half
+      // of the last k-step), then the loads placed at m.
+      auto emit = [&](auto mc, int aslot, int bslot, int rs, Frag& f) {
+        constexpr int m = decltype(mc)::value;
+        if constexpr (!last && m < kHalf) read_unit(aslot, bslot, rs, f, m);
+        if constexpr (last && m >= kHalf) read_unit(aslot, bslot, rs, f, m - kHalf);
+        static_for<0, 2 * kBlocks>([&](auto qc) {
+          if constexpr (g4::load_pos(decltype(qc)::value, kBlocks, kT) == s * kMf + m) load(qc);
+        });
+      };
+      auto groups = [&](auto m0, auto m1) {
+        static_for<decltype(m0)::value, decltype(m1)::value>([&](auto mc) {
+          constexpr int m = decltype(mc)::value;
+          constexpr bool reads = last ? m >= kHalf : m < kHalf;
+          constexpr int u = last ? m - kHalf : m;
+          if constexpr (reads) {
+            constexpr int nds = (u < TM ? TA::kReadsPerChunk : TB::kReadsPerChunk) * kLaneChunks;
+            __builtin_amdgcn_sched_group_barrier(0x100, nds, 0);  // DS read
+          }
+          constexpr int nvm = g4::loads_in(kBlocks, kT, s * kMf + m, s * kMf + m + 1);
+          if constexpr (nvm > 0) __builtin_amdgcn_sched_group_barrier(0x010, nvm, 0);  // LDS-DMA
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        });
+      };
+      if constexpr (!last) {
+        static_for<0, kMf>([&](auto mc) { emit(mc, a_rd, b_rd, s + 1, fr[nxt]); });
         mfma_rows(fr[cur], 0, TM);
-        constexpr int kDsG = kFragReads < kHalf ? kFragReads : kHalf;
-        constexpr int kDsPer = (kFragReads + kDsG - 1) / kDsG;
-        constexpr int kVmPer = (nload + (kMf - kDsG) - 1) / (kMf - kDsG);
-        static_for<0, kDsG>([&](auto) {
-          __builtin_amdgcn_sched_group_barrier(0x100, kDsPer, 0);  // DS read
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);       // MFMA
-        });
-        static_for<0, (nload + kVmPer - 1) / kVmPer>([&](auto) {
-          __builtin_amdgcn_sched_group_barrier(0x010, kVmPer, 0);  // VMEM (LDS-DMA)
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);       // MFMA
-        });
+        groups(std::integral_constant<int, 0>{}, std::integral_constant<int, kMf>{});
         __builtin_amdgcn_sched_barrier(0);
       } else {
-        issue_step();
-        mfma_rows(fr[cur], 0, TM / 2);
-        constexpr int kVmPer = (nload + kHalf - 1) / kHalf;
-        static_for<0, (nload + kVmPer - 1) / kVmPer>([&](auto) {
-          __builtin_amdgcn_sched_group_barrier(0x010, kVmPer, 0);  // VMEM (LDS-DMA)
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);       // MFMA
-        });
-        __builtin_amdgcn_sched_barrier(0);
-        // vmcnt <= kBlocks (this wave's A(kt+2) loads) and lgkmcnt = 0.
-        __builtin_amdgcn_s_waitcnt(((kBlocks & 15) | ((kBlocks >> 4) << 14) | (7 << 4)));
-        __builtin_amdgcn_s_barrier();
         const int na = adv(a_rd), nb = adv(b_rd);
-        load_frags(na, nb, 0, fr[kSteps & 1 ? nxt : 0]);
+        static_for<0, kHalf>([&](auto mc) { emit(mc, na, nb, 0, fr[kSteps & 1 ? nxt : 0]); });
+        mfma_rows(fr[cur], 0, TM / 2);
+        groups(std::integral_constant<int, 0>{}, std::integral_constant<int, kHalf>{});
+        __builtin_amdgcn_sched_barrier(0);
+        // vmcnt <= kInFlight (this wave's A(kt+2) loads so far) and lgkmcnt = 0.
+        __builtin_amdgcn_s_waitcnt(((kInFlight & 15) | ((kInFlight >> 4) << 14) | (7 << 4)));
+        __builtin_amdgcn_s_barrier();
+        static_for<kHalf, kMf>([&](auto mc) { emit(mc, na, nb, 0, fr[kSteps & 1 ? nxt : 0]); });
         mfma_rows(fr[cur], TM / 2, TM);
-        constexpr int kDsPer = (kFragReads + kHalf - 1) / kHalf;
-        static_for<0, kHalf>([&](auto) {
-          __builtin_amdgcn_sched_group_barrier(0x100, kDsPer, 0);  // DS read
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);       // MFMA
-        });
+        groups(std::integral_constant<int, kHalf>{}, std::integral_constant<int, kMf>{});
         __builtin_amdgcn_sched_barrier(0);
         a_rd = na;
         b_rd = nb;
@@ -423,7 +440,6 @@ __global__ __launch_bounds__(g4::kThreads) void gemm_w4_kernel(
         a_wr = adv(a_wr);
       }
     });
-    if constexpr (kSteps == 1) fr[0] = fr[1];
   };
   // Iterations whose loads (stages kt + 1 and kt + 2) are whole stages
   // inside K take the fast issue; the last two, and every iteration when K
