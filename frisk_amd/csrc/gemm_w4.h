@@ -365,7 +365,11 @@ __global__ __launch_bounds__(g4::kThreads) void gemm_w4_kernel(
   auto adv = [](int x) { return x >= 3 ? x - 3 : x + 2; };  // (x + 2) mod 5
   constexpr int kMf = TM * TN;
   constexpr int kHalf = kMf / 2;
-  static_assert(TM + TN == kHalf, "one fragment unit per MFMA of a half step");
+  // Fragment unit u (of kUnits per k-step) is read beside MFMA
+  // u kHalf / kUnits of the half k-step that reads.
+  constexpr int kUnits = TM + TN;
+  static_assert(kHalf % kUnits == 0, "fragment units spread evenly over a half step");
+  constexpr int kUnitGap = kHalf / kUnits;
   // The loads that may still be in flight at the last k-step's barrier: the
   // A(kt+2) loads issued before it (every B(kt+1) load is older).
   constexpr int kT = kSteps * kMf;
@@ -391,13 +395,14 @@ __global__ __launch_bounds__(g4::kThreads) void gemm_w4_kernel(
           issue(OpA{}, kt + 2, a_wr, std::integral_constant<int, q - kBlocks>{},
                 std::integral_constant<int, kBlocks>{}, fast);
       };
-      // Program order = issue order: beside MFMA m, fragment unit m (first
-      // half of a k-step) or unit m - kHalf of the next stage (second half
-      // of the last k-step), then the loads placed at m.
+      // Program order = issue order: beside MFMA m, a fragment unit (first
+      // half of a k-step, or the next stage's in the second half of the
+      // last k-step), then the loads placed at m.
       auto emit = [&](auto mc, int aslot, int bslot, int rs, Frag& f) {
         constexpr int m = decltype(mc)::value;
-        if constexpr (!last && m < kHalf) read_unit(aslot, bslot, rs, f, m);
-        if constexpr (last && m >= kHalf) read_unit(aslot, bslot, rs, f, m - kHalf);
+        constexpr int h = last ? m - kHalf : m;  // position in the reading half
+        if constexpr (h >= 0 && h < kHalf && h % kUnitGap == 0)
+          read_unit(aslot, bslot, rs, f, h / kUnitGap);
         static_for<0, 2 * kBlocks>([&](auto qc) {
           if constexpr (g4::load_pos(decltype(qc)::value, kBlocks, kT) == s * kMf + m) load(qc);
         });
@@ -405,9 +410,9 @@ __global__ __launch_bounds__(g4::kThreads) void gemm_w4_kernel(
       auto groups = [&](auto m0, auto m1) {
         static_for<decltype(m0)::value, decltype(m1)::value>([&](auto mc) {
           constexpr int m = decltype(mc)::value;
-          constexpr bool reads = last ? m >= kHalf : m < kHalf;
-          constexpr int u = last ? m - kHalf : m;
-          if constexpr (reads) {
+          constexpr int h = last ? m - kHalf : m;
+          constexpr int u = h / kUnitGap;
+          if constexpr (h >= 0 && h < kHalf && h % kUnitGap == 0) {
             constexpr int nds = (u < TM ? TA::kReadsPerChunk : TB::kReadsPerChunk) * kLaneChunks;
             __builtin_amdgcn_sched_group_barrier(0x100, nds, 0);  // DS read
           }
