@@ -204,6 +204,32 @@ def test_large_tiles_ragged(m, n, k, in_dt, out_dt):
     check(decode(c[rows]), ref + decode(c0[rows]), in_dt, out_dt)
 
 
+SHORT_K = [(8, torch.bfloat16, torch.bfloat16), (64, torch.bfloat16, torch.bfloat16),
+           (72, torch.bfloat16, torch.float32), (136, torch.float16, torch.float16),
+           (16, FP8, torch.bfloat16), (128, FP8, torch.bfloat16), (144, FP8, torch.float32),
+           (272, FP8, torch.bfloat16), (16, torch.int8, torch.int32), (144, torch.int8, torch.int32)]
+
+
+@pytest.mark.parametrize("k,in_dt,out_dt", SHORT_K, ids=lambda x: str(x).replace("torch.", ""))
+@pytest.mark.parametrize("ta,tb", [(False, True), (True, False), (False, False)],
+                         ids=["nt", "tt", "nn"])
+def test_large_tiles_short_k(k, in_dt, out_dt, ta, tb):
+    # 128 tiles of 256x256 over K of less than one 128-byte stage, exactly
+    # one, or one or two and a tail: every iteration of the 256x256 kernel's
+    # loop is a general (edge) one and its loads past the last stage read
+    # zeros.
+    m, n = 4096, 2048
+    print(f"case short-k m={m} n={n} k={k} {in_dt}->{out_dt} ta={ta} tb={tb}", flush=True)
+    a, b, sa, sb = make_operands(m, n, k, in_dt, ta, tb, seed=k + 7)
+    c = torch.full((m, n), 7, dtype=out_dt, device="cuda")
+    assert rt.gemm_plan(a, b, c, trans_a=ta, trans_b=tb)["kernel"] == "gemm_w4"
+    rt.gemm(a, b, c, trans_a=ta, trans_b=tb, scale_a=sa, scale_b=sb)
+    torch.cuda.synchronize()
+    r = sample_rows(m, 48, seed=k)
+    check(decode(c[torch.from_numpy(r).cuda()]), reference(a, b, ta, tb, sa, sb, rows=r),
+          in_dt, out_dt)
+
+
 @pytest.mark.parametrize("m,n,k", [(1024, 4096, 4096), (512, 640, 1000), (300, 1000, 72)])
 def test_mid_size_tiles(m, n, k):
     # Fewer than 128 tiles of 256x256: the 128x128-tile configuration.
