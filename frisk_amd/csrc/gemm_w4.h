@@ -250,10 +250,11 @@ __global__ __launch_bounds__(g4::kThreads) void gemm_w4_kernel(
     return stage >= nk_all ? stage : phys;
   };
   // issue() sends part p of np of one operand tile: blocks
-  // [p kBlocks / np, (p+1) kBlocks / np).  `fast`: the steady state, where the stage is a whole one inside K (no
-  // partial stage exists and the stage is not past the last): every lane's
-  // offset is its stage-invariant one and the stage base is the scalar
-  // offset, so a load is issued with no VALU work at all.
+  // [p kBlocks / np, (p+1) kBlocks / np).  `fast`: the steady state, where
+  // the stage is a whole one inside K (no partial stage exists and the stage
+  // is not past the last): every lane's offset is its stage-invariant one
+  // and the stage base is the scalar offset, so a load is issued with no
+  // VALU work at all.
   auto issue = [&](auto op, int stage, int slot, auto part, auto parts, auto fast) {
     constexpr int p = decltype(part)::value, np = decltype(parts)::value;
     constexpr bool is_a = decltype(op)::value;
@@ -330,9 +331,10 @@ __global__ __launch_bounds__(g4::kThreads) void gemm_w4_kernel(
   // reads A(kt) and B(kt) and issues B(kt+1), then A(kt+2); their slots
   // held A(kt-1) and B(kt-1), which every wave finished reading before the
   // barrier that ended iteration kt-1.  In the last k-step, after half of
-  // its MFMAs, each wave waits for its LDS reads and for all but its newest
-  // kBlocks loads (A(kt+2)), which leaves A(kt+1) (issued an iteration
-  // earlier) and B(kt+1) landed; the workgroup barrier then publishes them.
+  // its MFMAs, each wave waits for its LDS reads and for all but the
+  // A(kt+2) loads it has issued so far (kInFlight), which leaves A(kt+1)
+  // (issued an iteration earlier) and B(kt+1) landed; the workgroup barrier
+  // then publishes them.
   // The iteration's 2 kBlocks loads (B(kt+1) blocks, then A(kt+2) blocks)
   // go out one beside every (kSteps kMf) / (2 kBlocks)-th MFMA over the
   // whole iteration (g4::load_pos), the A loads of the last k-step's second
